@@ -1,0 +1,120 @@
+/*
+ * moe_quant_hip.h -- C ABI of the MI355X (gfx950) quantized-expert library
+ * (libmoe_quant_hip.so).
+ *
+ * Two groups of entry points:
+ *
+ *  1. Drop-ins for the reference's CPU exports, same names, signatures,
+ *     argument meaning and status codes.  Pointers are HOST pointers; the
+ *     library stages them through HBM.  They are reentrant and may be called
+ *     from several threads at once (each call uses its own stream and staging
+ *     buffers).
+ *
+ *  2. Device-resident entry points (prefix mqh_).  Every pointer is a DEVICE
+ *     address in HBM; `stream` is a hipStream_t (NULL = the null stream).
+ *     They only validate arguments and enqueue kernels; they do not
+ *     synchronize.  Numerical faults found by the kernels (non-finite outputs,
+ *     out-of-range expert ids) are latched in the caller's workspace and
+ *     reported by mqh_status().
+ *
+ * GGML type ids: Q8_0 = 8, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14.
+ * Quantized matrices are GGUF row-major: rows = output features, each row a
+ * run of (cols / block_size) blocks.  A stacked expert tensor holds
+ * n_experts such matrices back to back, exactly as a GGUF *_exps tensor.
+ *
+ * Status codes (shared by all entry points):
+ *    0  ok
+ *   -1  invalid argument (null pointer, non-positive or too large size,
+ *       fp16_graph not 0/1, n not a multiple of the block size)
+ *   -2  unsupported type, or a column count not a multiple of its block size
+ *   -3  byte count does not match rows x blocks x bytes_per_block
+ *   -4  non-finite output
+ *   -5  HIP runtime failure (allocation, copy or launch)
+ *   -6  workspace too small
+ *   -9  an expert id outside [0, n_experts)
+ */
+#ifndef MOE_QUANT_HIP_H
+#define MOE_QUANT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* 1. Reference drop-ins (host pointers)                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces dequant_k_supported (cpp/dequant_k.cpp:342-344): 1 if `type` is
+ * one of the five decodable GGML types, else 0. */
+int dequant_k_supported(int type);
+
+/* Replaces dequant_k_block_size (cpp/dequant_k.cpp:346-348): values per block
+ * (32 for Q8_0, 256 for the K-quants), 0 for an unsupported type. */
+int dequant_k_block_size(int type);
+
+/* Replaces dequant_k (cpp/dequant_k.cpp:350-394): decode n values of `type`
+ * from `src` into FP32 (want_f16 = 0) or FP16 bit patterns (want_f16 = 1) at
+ * `dst`.  Bit-identical to the reference.  Returns 0, -1 (unknown type, null
+ * pointer, n <= 0 or n % block_size != 0) or -5. */
+int dequant_k(int type, const uint8_t* src, void* dst, int64_t n, int want_f16);
+
+/* Replaces moe_quant_expert (cpp/moe_quant_dot.cpp:171-214): one token
+ * through one SwiGLU expert straight from quantized bytes,
+ *   output = W_down (silu(W_gate input) * (W_up input)),
+ * gate/up shaped [intermediate x hidden], down [hidden x intermediate].
+ * fp16_graph = 1 rounds to FP16 at the reference's points.  Returns 0, -1,
+ * -2, -3, -4 (non-finite output; the whole output is written) or -5. */
+int moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes,
+                     int up_type, const uint8_t* up, int64_t up_bytes,
+                     int down_type, const uint8_t* down, int64_t down_bytes,
+                     const float* input, int hidden, int intermediate,
+                     float* output, int fp16_graph);
+
+/* ------------------------------------------------------------------------ */
+/* 2. Device-resident entry points                                           */
+/* ------------------------------------------------------------------------ */
+
+/* Device form of dequant_k for weights already in HBM (the conversion that
+ * dequant_to_f16, src/run_q4k_f16_openvino.py:62-85, performs on the host).
+ * `dst` must be 16-byte aligned.  Returns 0, -1 or -5. */
+int mqh_dequant(int type, const void* src, void* dst, int64_t n, int want_f16, void* stream);
+
+/* Bytes of workspace mqh_moe_decode needs for n_tokens tokens of top_k
+ * routed experts (plus one shared slot). */
+int64_t mqh_moe_workspace_bytes(int n_tokens, int top_k, int intermediate, int sh_intermediate);
+
+/* Fused MoE layer for a batch of tokens, replacing the per-expert loop of
+ * run_moe_layer (src/flash_moe/moe_layer.py:39-107) over NativeExpert.forward
+ * (src/flash_moe/native_expert.py:23-37) plus SharedExpert.forward
+ * (src/flash_moe/shared_expert.py:221-251):
+ *   y[t] = sum_s weights[t,s] * E_{ids[t,s]}(x[t]) + sigmoid(x[t].sh_gate_inp) * E_sh(x[t])
+ * gate/up/down are stacked [n_experts x slice] tensors; ids and weights are
+ * [n_tokens x top_k] (int32, FP32) in top-k order; x and y [n_tokens x
+ * hidden] FP32.  The shared expert is optional (sh_gate == NULL: none;
+ * sh_gate_inp == NULL: no sigmoid scale).  fp16_graph applies to the routed
+ * experts.  The workspace must hold mqh_moe_workspace_bytes(...) bytes and be
+ * zeroed once (mqh_workspace_init) before first use.  Returns 0, -1, -2, -5
+ * or -6; kernel-side faults are read with mqh_status. */
+int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
+                   int down_type, const void* down, int n_experts, int hidden, int intermediate,
+                   int sh_gate_type, const void* sh_gate, int sh_up_type, const void* sh_up,
+                   int sh_down_type, const void* sh_down, int sh_intermediate,
+                   const float* sh_gate_inp,
+                   const float* x, int n_tokens, const int32_t* ids, const float* weights, int top_k,
+                   float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Zero a workspace (flags and counters) on `stream`. */
+int mqh_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Synchronize `stream`, then read and clear the fault flags latched in
+ * `workspace`: 0, -4 (non-finite output), -9 (bad expert id), -8 (a kernel
+ * gave up waiting on another workgroup) or -5. */
+int mqh_status(void* workspace, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_QUANT_HIP_H */

@@ -1,0 +1,285 @@
+// capi.hip -- the library's C ABI (declared in include/moe_quant_hip.h).
+//
+// Host-pointer drop-ins stage their buffers through HBM with a pooled staging
+// context per concurrent call; device-resident entry points validate and
+// enqueue only.
+#include <mutex>
+#include <vector>
+
+#include "../../include/moe_quant_hip.h"
+#include "kquant_device.h"
+#include "moe_decode.h"
+
+using namespace mqh;
+
+namespace {
+
+constexpr int ST_OK = 0, ST_ARG = -1, ST_TYPE = -2, ST_BYTES = -3, ST_NONFINITE = -4, ST_HIP = -5,
+              ST_WORKSPACE = -6, ST_TIMEOUT = -8, ST_BAD_ID = -9;
+
+bool supported(int t) { return block_size(t) != 0; }
+
+// Expected bytes of a [rows x cols] matrix, or a negative status.
+int64_t matrix_bytes(int type, int rows, int cols) {
+    const int bs = block_size(type);
+    if (!bs || cols % bs) return ST_TYPE;
+    return (int64_t)rows * (cols / bs) * block_bytes(type);
+}
+
+__global__ void k_zero_words(int* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+hipError_t zero_words(void* p, int64_t n_words, hipStream_t s) {
+    if (n_words <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n_words + 255) / 256, 1024);
+    hipLaunchKernelGGL(k_zero_words, dim3((unsigned)blocks), dim3(256), 0, s, (int*)p, n_words);
+    return hipGetLastError();
+}
+
+// Device buffer that grows on demand (never shrinks).
+struct DevBuf {
+    void* ptr = nullptr;
+    size_t cap = 0;
+    hipError_t reserve(size_t n) {
+        if (n <= cap) return hipSuccess;
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        cap = 0;
+        const size_t want = (n + 4095) & ~(size_t)4095;
+        hipError_t e = hipMalloc(&ptr, want);
+        if (e == hipSuccess) cap = want;
+        return e;
+    }
+};
+
+// Staging for one in-flight host-pointer call.  Pooled, so threads that come
+// and go (the reference runs experts on a ThreadPoolExecutor) reuse them.
+struct Ctx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    DevBuf w, io, ws;
+};
+
+std::mutex g_pool_mu;
+std::vector<Ctx*> g_pool;
+
+Ctx* acquire_ctx(int& status) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) { status = ST_HIP; return nullptr; }
+    {
+        std::lock_guard<std::mutex> lk(g_pool_mu);
+        for (size_t i = 0; i < g_pool.size(); ++i) {
+            if (g_pool[i]->device == dev) {
+                Ctx* c = g_pool[i];
+                g_pool.erase(g_pool.begin() + (long)i);
+                return c;
+            }
+        }
+    }
+    Ctx* c = new Ctx();
+    c->device = dev;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        status = ST_HIP;
+        return nullptr;
+    }
+    return c;
+}
+
+void release_ctx(Ctx* c) {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    g_pool.push_back(c);
+}
+
+int read_and_clear_flags(int* flags_dev, hipStream_t s) {
+    int h[3] = {0, 0, 0};
+    if (hipStreamSynchronize(s) != hipSuccess) return ST_HIP;
+    if (hipMemcpyAsync(h, flags_dev, sizeof(h), hipMemcpyDeviceToHost, s) != hipSuccess) return ST_HIP;
+    if (hipStreamSynchronize(s) != hipSuccess) return ST_HIP;
+    if (h[0] | h[1] | h[2]) {
+        if (zero_words(flags_dev, 3, s) != hipSuccess) return ST_HIP;
+        if (hipStreamSynchronize(s) != hipSuccess) return ST_HIP;
+    }
+    if (h[FLAG_BAD_ID]) return ST_BAD_ID;
+    if (h[FLAG_TIMEOUT]) return ST_TIMEOUT;
+    if (h[FLAG_NONFINITE]) return ST_NONFINITE;
+    return ST_OK;
+}
+
+// Validate shapes and types of one expert triple.  Returns 0 or a status.
+int check_expert_types(int gt, int ut, int dt, int hidden, int inter) {
+    if (!supported(gt) || !supported(ut) || !supported(dt)) return ST_TYPE;
+    if (hidden % block_size(gt) || hidden % block_size(ut) || inter % block_size(dt)) return ST_TYPE;
+    return ST_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dequant_k_supported(int type) { return supported(type) ? 1 : 0; }
+
+int dequant_k_block_size(int type) { return block_size(type); }
+
+int dequant_k(int type, const uint8_t* src, void* dst, int64_t n, int want_f16) {
+    const int bs = block_size(type);
+    if (bs == 0 || src == nullptr || dst == nullptr) return ST_ARG;
+    if (n <= 0 || n % bs != 0) return ST_ARG;
+    int status = ST_OK;
+    Ctx* c = acquire_ctx(status);
+    if (!c) return status;
+    const size_t in_bytes = (size_t)(n / bs) * block_bytes(type);
+    const size_t out_bytes = (size_t)n * (want_f16 ? 2 : 4);
+    status = ST_HIP;
+    if (c->w.reserve(in_bytes) == hipSuccess && c->io.reserve(out_bytes) == hipSuccess &&
+        hipMemcpyAsync(c->w.ptr, src, in_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+        launch_dequant(type, (const uint8_t*)c->w.ptr, c->io.ptr, n, want_f16, c->stream) == hipSuccess &&
+        hipMemcpyAsync(dst, c->io.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
+        hipStreamSynchronize(c->stream) == hipSuccess)
+        status = ST_OK;
+    release_ctx(c);
+    return status;
+}
+
+int moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes, int up_type, const uint8_t* up,
+                     int64_t up_bytes, int down_type, const uint8_t* down, int64_t down_bytes, const float* input,
+                     int hidden, int intermediate, float* output, int fp16_graph) {
+    // validation order and codes of moe_quant_dot.cpp:177-188
+    if (!gate || !up || !down || !input || !output || hidden <= 0 || intermediate <= 0 || hidden > 65536 ||
+        intermediate > 65536 || (fp16_graph != 0 && fp16_graph != 1))
+        return ST_ARG;
+    const int types[3] = {gate_type, up_type, down_type};
+    const int cols[3] = {hidden, hidden, intermediate};
+    const int rows[3] = {intermediate, intermediate, hidden};
+    const int64_t sizes[3] = {gate_bytes, up_bytes, down_bytes};
+    for (int i = 0; i < 3; ++i) {
+        const int64_t want = matrix_bytes(types[i], rows[i], cols[i]);
+        if (want < 0) return (int)want;
+        if (sizes[i] != want) return ST_BYTES;
+    }
+    int status = ST_OK;
+    Ctx* c = acquire_ctx(status);
+    if (!c) return status;
+
+    const int64_t off_up = align256(gate_bytes), off_down = off_up + align256(up_bytes);
+    const int64_t w_total = off_down + align256(down_bytes);
+    // io: x [hidden] | y [hidden] | id | weight
+    const int64_t off_y = align256((int64_t)hidden * 4), off_id = off_y + align256((int64_t)hidden * 4);
+    const int64_t io_total = off_id + 256;
+    const WorkspaceLayout wl = decode_workspace_layout(1, 1, intermediate, 0);
+    const bool fresh_ws = c->ws.cap < (size_t)wl.total;
+
+    status = ST_HIP;
+    if (c->w.reserve(w_total) != hipSuccess || c->io.reserve(io_total) != hipSuccess ||
+        c->ws.reserve(wl.total) != hipSuccess) {
+        release_ctx(c);
+        return ST_HIP;
+    }
+    uint8_t* W = (uint8_t*)c->w.ptr;
+    uint8_t* IO = (uint8_t*)c->io.ptr;
+    uint8_t* WS = (uint8_t*)c->ws.ptr;
+    struct { int32_t id; float w; } route = {0, 1.0f};
+
+    DecodeParams p{};
+    p.gate = W; p.up = W + off_up; p.down = W + off_down;
+    p.gate_type = gate_type; p.up_type = up_type; p.down_type = down_type;
+    p.gate_eb = gate_bytes; p.up_eb = up_bytes; p.down_eb = down_bytes;
+    p.n_experts = 1; p.hidden = hidden; p.inter = intermediate;
+    p.has_shared = 0;
+    p.x = (const float*)IO; p.n_tokens = 1;
+    p.ids = (const int32_t*)(IO + off_id); p.weights = (const float*)(IO + off_id + 4); p.top_k = 1;
+    p.y = (float*)(IO + off_y); p.fp16 = fp16_graph;
+    p.flags = (int*)(WS + wl.flags_off); p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
+    p.S = 1; p.Imax = intermediate;
+
+    if ((!fresh_ws || zero_words(WS, wl.flags_off / 4 + N_FLAGS, c->stream) == hipSuccess) &&
+        hipMemcpyAsync(W, gate, gate_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+        hipMemcpyAsync(W + off_up, up, up_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+        hipMemcpyAsync(W + off_down, down, down_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+        hipMemcpyAsync(IO, input, (size_t)hidden * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+        hipMemcpyAsync(IO + off_id, &route, sizeof(route), hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+        launch_decode_generic(p, c->stream) == hipSuccess &&
+        hipMemcpyAsync(output, IO + off_y, (size_t)hidden * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess)
+        status = read_and_clear_flags(p.flags, c->stream);
+    release_ctx(c);
+    return status;
+}
+
+int mqh_dequant(int type, const void* src, void* dst, int64_t n, int want_f16, void* stream) {
+    const int bs = block_size(type);
+    if (bs == 0 || src == nullptr || dst == nullptr) return ST_ARG;
+    if (n <= 0 || n % bs != 0 || ((uintptr_t)dst & 15)) return ST_ARG;
+    return launch_dequant(type, (const uint8_t*)src, dst, n, want_f16, (hipStream_t)stream) == hipSuccess ? ST_OK
+                                                                                                      : ST_HIP;
+}
+
+int64_t mqh_moe_workspace_bytes(int n_tokens, int top_k, int intermediate, int sh_intermediate) {
+    if (n_tokens <= 0 || top_k < 0 || intermediate < 0 || sh_intermediate < 0) return ST_ARG;
+    if ((top_k > 0 && intermediate == 0) || (top_k == 0 && sh_intermediate == 0)) return ST_ARG;
+    return decode_workspace_layout(n_tokens, top_k, intermediate, sh_intermediate).total;
+}
+
+int mqh_workspace_init(void* workspace, int64_t workspace_bytes, void* stream) {
+    if (!workspace || workspace_bytes < (int64_t)N_FLAGS * 4) return ST_ARG;
+    return zero_words(workspace, N_FLAGS, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
+}
+
+int mqh_status(void* workspace, void* stream) {
+    if (!workspace) return ST_ARG;
+    return read_and_clear_flags((int*)workspace, (hipStream_t)stream);
+}
+
+int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up, int down_type, const void* down,
+                   int n_experts, int hidden, int intermediate, int sh_gate_type, const void* sh_gate,
+                   int sh_up_type, const void* sh_up, int sh_down_type, const void* sh_down, int sh_intermediate,
+                   const float* sh_gate_inp, const float* x, int n_tokens, const int32_t* ids, const float* weights,
+                   int top_k, float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, void* stream) {
+    const bool has_shared = sh_gate != nullptr;
+    if (!x || !y || !workspace) return ST_ARG;
+    if (hidden <= 0 || hidden > 65536 || n_tokens <= 0 || top_k < 0 || top_k > 64 ||
+        (top_k == 0 && !has_shared) || (fp16_graph != 0 && fp16_graph != 1))
+        return ST_ARG;
+    int st = ST_OK;
+    if (top_k > 0) {
+        if (!gate || !up || !down || !ids || !weights) return ST_ARG;
+        if (n_experts <= 0 || intermediate <= 0 || intermediate > 65536) return ST_ARG;
+        st = check_expert_types(gate_type, up_type, down_type, hidden, intermediate);
+        if (st) return st;
+    } else {
+        intermediate = 0;
+    }
+    if (has_shared) {
+        if (!sh_up || !sh_down || sh_intermediate <= 0 || sh_intermediate > 65536) return ST_ARG;
+        st = check_expert_types(sh_gate_type, sh_up_type, sh_down_type, hidden, sh_intermediate);
+        if (st) return st;
+    }
+    const WorkspaceLayout wl = decode_workspace_layout(n_tokens, top_k, intermediate, has_shared ? sh_intermediate : 0);
+    if (workspace_bytes < wl.total) return ST_WORKSPACE;
+
+    uint8_t* WS = (uint8_t*)workspace;
+    DecodeParams p{};
+    p.gate = (const uint8_t*)gate; p.up = (const uint8_t*)up; p.down = (const uint8_t*)down;
+    p.gate_type = gate_type; p.up_type = up_type; p.down_type = down_type;
+    if (top_k > 0) {
+        p.gate_eb = matrix_bytes(gate_type, intermediate, hidden);
+        p.up_eb = matrix_bytes(up_type, intermediate, hidden);
+        p.down_eb = matrix_bytes(down_type, hidden, intermediate);
+    }
+    p.n_experts = n_experts; p.hidden = hidden; p.inter = intermediate;
+    p.has_shared = has_shared ? 1 : 0;
+    if (has_shared) {
+        p.sh_gate = (const uint8_t*)sh_gate; p.sh_up = (const uint8_t*)sh_up; p.sh_down = (const uint8_t*)sh_down;
+        p.sh_gate_type = sh_gate_type; p.sh_up_type = sh_up_type; p.sh_down_type = sh_down_type;
+        p.sh_inter = sh_intermediate; p.sh_gate_inp = sh_gate_inp;
+    }
+    p.x = x; p.n_tokens = n_tokens; p.ids = ids; p.weights = weights; p.top_k = top_k;
+    p.y = y; p.fp16 = fp16_graph;
+    p.flags = (int*)(WS + wl.flags_off); p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
+    p.S = top_k + (has_shared ? 1 : 0);
+    p.Imax = std::max(intermediate, has_shared ? sh_intermediate : 0);
+    return launch_decode_generic(p, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
+}
+
+}  // extern "C"

@@ -1,0 +1,182 @@
+// kquant_device.h -- GGUF K-quant block decoding on gfx950.
+//
+// Every kernel in this library decodes weights through these functions, so a
+// weight value is the same bit pattern in the standalone dequantizer, the
+// decode GEMV and the prefill GEMM.  The arithmetic follows the reference
+// decoders in cpp/dequant_k.cpp (Q8_0 :146-154, scale/min unpack :166-175,
+// Q4_K :182-206, Q5_K :221-240, Q6_K :254-268, Q3_K :278-298):
+//
+//   Q8_0  y = q * d                          (exact)
+//   Q3_K  y = (d * sc) * q                   (exact)
+//   Q4_K  y = (d * sc) * q - (dmin * m)      (one rounding, in the subtraction)
+//   Q5_K  y = (d * sc) * q - (dmin * m)      (one rounding)
+//   Q6_K  y = (d * sc) * q                   (exact: |m_d * sc * q| < 2^23)
+//
+// Products are written with __fmul_rn/__fsub_rn so the compiler cannot fuse
+// them; by the exactness above a fused form would round identically, but the
+// explicit form keeps the claim independent of -ffp-contract.
+//
+// Block bit positions (values i = 0..255 of a 256-value super-block):
+//   Q4_K  qs[32*(i/64) + i%32] >> 4*((i/32)&1), sub-block i/32
+//   Q5_K  as Q4_K at qs@48, plus bit (i/32) of qh[i%32] as bit 4
+//   Q6_K  ql[64h + 32*(s&1) + l] >> 4*(s>>1) | (qh[32h + l] >> 2s & 3) << 4, minus 32,
+//         with h = i/128, s = (i/32)%4, l = i%32; scale i/16
+//   Q3_K  (qs[32h + l] >> 2s & 3) - 4*(1 - (hmask[l] >> (i/32) & 1)); scale i/16
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mqh {
+
+enum : int { T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
+
+__host__ __device__ constexpr int block_size(int t) {
+    return t == T_Q8_0 ? 32 : (t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 256 : 0;
+}
+
+__host__ __device__ constexpr int block_bytes(int t) {
+    return t == T_Q8_0 ? 34 : t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : 0;
+}
+
+// ------------------------------------------------------------------ loads
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *(const uint16_t*)p; }
+
+// 8 bytes from any byte address (gfx950 global loads tolerate misalignment:
+// Q6_K and Q3_K blocks are 210 and 110 bytes, so fields land on 2-byte offsets).
+__device__ __forceinline__ uint64_t ld_u64(const uint8_t* p) {
+    uint64_t v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+
+__device__ __forceinline__ float h2f(uint32_t bits) {
+    return __half2float(__ushort_as_half((unsigned short)bits));
+}
+
+__device__ __forceinline__ uint32_t f2h_rn(float f) {
+    return (uint32_t)__half_as_ushort(__float2half_rn(f));
+}
+
+__device__ __forceinline__ float round16(float f) { return __half2float(__float2half_rn(f)); }
+
+// byte k of a 64-bit word
+__device__ __forceinline__ uint32_t byte_of(uint64_t w, int k) { return (uint32_t)(w >> (8 * k)) & 0xFFu; }
+
+// 6-bit scale and min j (0..7) of Q4_K/Q5_K from the 12 packed bytes at s.
+__device__ __forceinline__ void scale_min_k4(const uint8_t* s, int j, int& sc, int& mn) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        mn = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
+        mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+// signed 6-bit scale j (0..15) of Q3_K from the 12 packed bytes at s
+__device__ __forceinline__ int q3_scale(const uint8_t* s, int j) {
+    const int lo = (j < 8) ? (s[j] & 15) : ((s[j - 8] >> 4) & 15);
+    const int hi = (s[8 + (j & 3)] >> (2 * (j >> 2))) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+
+// ---------------------------------------------------- 8 consecutive values
+//
+// decode8<T>(blk, t, out): values 8t .. 8t+7 of the block at blk, as FP32,
+// bit-identical to the reference decoders.  t ranges over block_size(T)/8.
+
+template <int T>
+__device__ __forceinline__ void decode8(const uint8_t* blk, int t, float out[8]);
+
+template <>
+__device__ __forceinline__ void decode8<T_Q8_0>(const uint8_t* blk, int t, float out[8]) {
+    const float d = h2f(ld_u16(blk));
+    const uint64_t w = ld_u64(blk + 2 + 8 * t);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = __fmul_rn((float)(int8_t)byte_of(w, k), d);
+}
+
+template <>
+__device__ __forceinline__ void decode8<T_Q4_K>(const uint8_t* blk, int t, float out[8]) {
+    const int j = t >> 2;                       // sub-block 0..7
+    const int g = t >> 3, hi = (t >> 2) & 1, lq = 8 * (t & 3);
+    const float d = h2f(ld_u16(blk)), dmin = h2f(ld_u16(blk + 2));
+    int sc, mn;
+    scale_min_k4(blk + 4, j, sc, mn);
+    const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
+    const uint64_t w = ld_u64(blk + 16 + 32 * g + lq) >> (4 * hi);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = __fsub_rn(__fmul_rn(d1, (float)(byte_of(w, k) & 15)), m1);
+}
+
+template <>
+__device__ __forceinline__ void decode8<T_Q5_K>(const uint8_t* blk, int t, float out[8]) {
+    const int j = t >> 2;
+    const int g = t >> 3, hi = (t >> 2) & 1, lq = 8 * (t & 3);
+    const float d = h2f(ld_u16(blk)), dmin = h2f(ld_u16(blk + 2));
+    int sc, mn;
+    scale_min_k4(blk + 4, j, sc, mn);
+    const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
+    const uint64_t lo = ld_u64(blk + 48 + 32 * g + lq) >> (4 * hi);
+    const uint64_t hb = ld_u64(blk + 16 + lq) >> j;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t q = (byte_of(lo, k) & 15) | ((byte_of(hb, k) & 1) << 4);
+        out[k] = __fsub_rn(__fmul_rn(d1, (float)q), m1);
+    }
+}
+
+template <>
+__device__ __forceinline__ void decode8<T_Q6_K>(const uint8_t* blk, int t, float out[8]) {
+    const int h = t >> 4, s = (t >> 2) & 3, lq = 8 * (t & 3);
+    const float d = h2f(ld_u16(blk + 208));
+    const float ds = __fmul_rn(d, (float)(int8_t)blk[192 + (t >> 1)]);
+    const uint64_t lo = ld_u64(blk + 64 * h + 32 * (s & 1) + lq) >> (4 * (s >> 1));
+    const uint64_t hq = ld_u64(blk + 128 + 32 * h + lq) >> (2 * s);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int q = (int)((byte_of(lo, k) & 15) | ((byte_of(hq, k) & 3) << 4)) - 32;
+        out[k] = __fmul_rn(ds, (float)q);
+    }
+}
+
+template <>
+__device__ __forceinline__ void decode8<T_Q3_K>(const uint8_t* blk, int t, float out[8]) {
+    const int h = t >> 4, s = (t >> 2) & 3, lq = 8 * (t & 3);
+    const float d = h2f(ld_u16(blk + 108));
+    const float ds = __fmul_rn(d, (float)q3_scale(blk + 96, t >> 1));
+    const uint64_t lo = ld_u64(blk + 32 + 32 * h + lq) >> (2 * s);
+    const uint64_t hm = ld_u64(blk + lq) >> (t >> 2);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int q = (int)(byte_of(lo, k) & 3) - (int)(((byte_of(hm, k) & 1) ^ 1) << 2);
+        out[k] = __fmul_rn(ds, (float)q);
+    }
+}
+
+// Runtime-type dispatch; `type` is uniform across the wavefront, so the
+// branch does not diverge.
+__device__ __forceinline__ void decode8_any(int type, const uint8_t* blk, int t, float out[8]) {
+    switch (type) {
+        case T_Q8_0: decode8<T_Q8_0>(blk, t, out); break;
+        case T_Q3_K: decode8<T_Q3_K>(blk, t, out); break;
+        case T_Q4_K: decode8<T_Q4_K>(blk, t, out); break;
+        case T_Q5_K: decode8<T_Q5_K>(blk, t, out); break;
+        default:     decode8<T_Q6_K>(blk, t, out); break;
+    }
+}
+
+// ------------------------------------------------------------ reductions
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64);
+// every lane of the group receives the group total.  Fixed butterfly order,
+// so the result is deterministic.
+__device__ __forceinline__ float group_sum(float v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace mqh

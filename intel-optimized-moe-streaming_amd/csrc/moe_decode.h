@@ -1,0 +1,70 @@
+// moe_decode.h -- parameter block shared by the decode kernels and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+namespace mqh {
+
+// workspace flag words (int32), sticky until read by mqh_status
+enum : int { FLAG_NONFINITE = 0, FLAG_BAD_ID = 1, FLAG_TIMEOUT = 2, N_FLAGS = 64 };
+
+constexpr int ROWS_A = 8;    // intermediate rows per workgroup, kernel A
+constexpr int ROWS_W = 4;    // hidden rows per wavefront, kernel B
+constexpr int ROWS_B = 4 * ROWS_W;
+
+struct DecodeParams {
+    // routed experts: stacked GGUF tensors, n_experts consecutive slices each
+    const uint8_t* gate;
+    const uint8_t* up;
+    const uint8_t* down;
+    int gate_type, up_type, down_type;
+    int64_t gate_eb, up_eb, down_eb;  // bytes per expert slice
+    int n_experts;
+    int hidden, inter;
+    // shared expert (has_shared == 0: absent)
+    const uint8_t* sh_gate;
+    const uint8_t* sh_up;
+    const uint8_t* sh_down;
+    int sh_gate_type, sh_up_type, sh_down_type;
+    int sh_inter;
+    const float* sh_gate_inp;  // optional sigmoid gate vector [hidden]
+    int has_shared;
+    // tokens
+    const float* x;         // [n_tokens x hidden]
+    int n_tokens;
+    const int32_t* ids;     // [n_tokens x top_k]
+    const float* weights;   // [n_tokens x top_k]
+    int top_k;
+    float* y;               // [n_tokens x hidden]
+    int fp16;
+    // workspace views
+    int* flags;             // [N_FLAGS]
+    float* sh_scale;        // [n_tokens]
+    float* act;             // [n_tokens x S x Imax]
+    int S, Imax;
+};
+
+struct WorkspaceLayout {
+    int64_t flags_off, scale_off, act_off, total;
+};
+
+inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+inline WorkspaceLayout decode_workspace_layout(int n_tokens, int top_k, int inter, int sh_inter) {
+    WorkspaceLayout w;
+    const int S = top_k + 1;  // room for the shared slot
+    const int Imax = std::max(inter, sh_inter);
+    w.flags_off = 0;
+    w.scale_off = align256(w.flags_off + (int64_t)N_FLAGS * 4);
+    w.act_off = align256(w.scale_off + (int64_t)n_tokens * 4);
+    w.total = align256(w.act_off + (int64_t)n_tokens * S * Imax * 4);
+    return w;
+}
+
+hipError_t launch_decode_generic(const DecodeParams& p, hipStream_t stream);
+hipError_t launch_dequant(int type, const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream);
+
+}  // namespace mqh

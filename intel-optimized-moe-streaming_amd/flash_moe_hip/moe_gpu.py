@@ -1,0 +1,88 @@
+"""Device-resident fused MoE calls (thin wrapper over the mqh_* C ABI).
+
+``MoeRunner.decode(layer, x, ids, weights)`` enqueues one fused launch for
+every routed expert of every token plus the layer's shared expert; nothing is
+synchronized.  ``MoeRunner.status()`` synchronizes and returns the fault
+status latched by the kernels (0, -4 non-finite, -9 bad expert id).
+"""
+from __future__ import annotations
+
+from . import _lib
+from .layer_store import ExpertLayer
+
+_NULL = None
+
+
+class MoeRunner:
+    """Owns the workspace of the fused kernels on one device."""
+
+    def __init__(self, device=None):
+        import torch
+
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.lib = _lib.load()
+        self._ws = None
+        self._ws_bytes = 0
+
+    def _workspace(self, n_tokens: int, top_k: int, inter: int, sh_inter: int, stream):
+        import torch
+
+        need = int(self.lib.mqh_moe_workspace_bytes(n_tokens, top_k, inter, sh_inter))
+        if need < 0:
+            _lib.check(need, "mqh_moe_workspace_bytes")
+        if self._ws is None or need > self._ws_bytes:
+            if self._ws is not None:
+                # keep the latched flags of the old workspace visible
+                _lib.check(self.lib.mqh_status(self._ws.data_ptr(), stream.cuda_stream), "pending kernel")
+            self._ws_bytes = max(need, 2 * self._ws_bytes)
+            self._ws = torch.empty(self._ws_bytes, dtype=torch.uint8, device=self.device)
+            _lib.check(self.lib.mqh_workspace_init(self._ws.data_ptr(), self._ws_bytes, stream.cuda_stream),
+                       "mqh_workspace_init")
+        return self._ws
+
+    def decode(self, layer: ExpertLayer, x, ids=None, weights=None, *, y=None, fp16_graph: int = 0,
+               use_shared: bool = True, stream=None):
+        """y[t] = sum_s weights[t,s] * E_ids[t,s](x[t]) (+ shared).  x [T,H] FP32,
+        ids [T,k] int32, weights [T,k] FP32, all CUDA tensors on the layer's device."""
+        import torch
+
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        x = x.reshape(-1, layer.hidden)
+        T = x.shape[0]
+        if x.dtype != torch.float32 or not x.is_contiguous():
+            raise ValueError("x must be contiguous FP32")
+        top_k = 0 if ids is None else int(ids.shape[-1])
+        if top_k:
+            ids = ids.reshape(T, top_k)
+            weights = weights.reshape(T, top_k)
+            if ids.dtype != torch.int32 or weights.dtype != torch.float32:
+                raise ValueError("ids must be int32 and weights FP32")
+            if not (ids.is_contiguous() and weights.is_contiguous()):
+                raise ValueError("ids and weights must be contiguous")
+        sh = layer.shared if use_shared else None
+        if y is None:
+            y = torch.empty((T, layer.hidden), dtype=torch.float32, device=x.device)
+        ws = self._workspace(T, top_k, layer.intermediate if top_k else 0, sh.intermediate if sh else 0, stream)
+        t = layer.tensors
+        rc = self.lib.mqh_moe_decode(
+            layer.types["gate"], t["gate"].data_ptr(), layer.types["up"], t["up"].data_ptr(),
+            layer.types["down"], t["down"].data_ptr(), layer.n_experts, layer.hidden, layer.intermediate,
+            sh.types["gate"] if sh else 0, sh.gate.data_ptr() if sh else _NULL,
+            sh.types["up"] if sh else 0, sh.up.data_ptr() if sh else _NULL,
+            sh.types["down"] if sh else 0, sh.down.data_ptr() if sh else _NULL,
+            sh.intermediate if sh else 0,
+            sh.gate_inp.data_ptr() if (sh is not None and sh.gate_inp is not None) else _NULL,
+            x.data_ptr(), T, ids.data_ptr() if top_k else _NULL, weights.data_ptr() if top_k else _NULL, top_k,
+            y.data_ptr(), int(fp16_graph), ws.data_ptr(), self._ws_bytes, stream.cuda_stream)
+        _lib.check(rc, "mqh_moe_decode")
+        return y
+
+    def status(self, stream=None) -> int:
+        import torch
+
+        if self._ws is None:
+            return 0
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        return int(self.lib.mqh_status(self._ws.data_ptr(), stream.cuda_stream))

@@ -1,0 +1,55 @@
+"""GGML quantization type ids and block geometry.
+
+Type ids and (values per block, bytes per block) are fixed by the GGUF format;
+they are the same numbers as ``src/flash_moe/dequant.py:30-50`` (by name) and
+``cpp/dequant_k.cpp:37-41,302-322`` (by id).
+"""
+from __future__ import annotations
+
+GGML_TYPE_IDS: dict[str, int] = {"Q8_0": 8, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+TYPE_NAMES: dict[int, str] = {v: k for k, v in GGML_TYPE_IDS.items()}
+
+# The types the HIP kernels decode (native_expert.py:10 lists the same five).
+SUPPORTED_TYPES = frozenset(GGML_TYPE_IDS.values())
+
+# name -> (block_size, bytes_per_block) for every GGUF type the reference names.
+GGML_BLOCK_INFO: dict[str, tuple[int, int]] = {
+    "F32": (1, 4),
+    "F16": (1, 2),
+    "BF16": (1, 2),
+    "Q4_0": (32, 18),
+    "Q4_1": (32, 20),
+    "Q5_0": (32, 22),
+    "Q5_1": (32, 24),
+    "Q8_0": (32, 34),
+    "Q2_K": (256, 84),
+    "Q3_K": (256, 110),
+    "Q4_K": (256, 144),
+    "Q5_K": (256, 176),
+    "Q6_K": (256, 210),
+    "Q8_K": (256, 292),
+    "IQ4_NL": (32, 18),
+    "IQ4_XS": (256, 136),
+    "IQ3_XXS": (256, 98),
+    "IQ2_XXS": (256, 66),
+    "IQ1_S": (256, 50),
+}
+
+
+def block_info(ggml_type: int) -> tuple[int, int]:
+    """(values per block, bytes per block) of a supported type id."""
+    name = TYPE_NAMES.get(int(ggml_type))
+    if name is None:
+        raise ValueError(f"unsupported ggml type {ggml_type}")
+    return GGML_BLOCK_INFO[name]
+
+
+def name_of(ggml_type: int) -> str:
+    return TYPE_NAMES.get(int(ggml_type), f"type_{int(ggml_type)}")
+
+
+def tensor_bytes(ggml_type: int, rows: int, cols: int) -> int:
+    bs, pb = block_info(ggml_type)
+    if cols % bs:
+        raise ValueError(f"{cols} columns is not a multiple of the {name_of(ggml_type)} block ({bs})")
+    return rows * (cols // bs) * pb

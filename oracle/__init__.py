@@ -1,0 +1,191 @@
+"""CPU oracle for the quantized-expert hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
+``bench.py`` may import this package, and only as the checker (or, for the
+baseline, as the thing timed on the host).  The HIP product path never imports
+it and never falls back to it.
+
+Contents
+--------
+* ``liboracle_kquant.so`` (built from ``kquant_oracle.c`` by ``Makefile``): a C
+  restatement of the reference kernels ``cpp/dequant_k.cpp`` and
+  ``cpp/moe_quant_dot.cpp``.  Wrapped here as :func:`dequant_k` and
+  :func:`moe_quant_expert` with the reference's argument meaning and status
+  codes.
+* NumPy restatements of the Python semantics around the kernels:
+  :func:`route` (``src/flash_moe/router.py:140-170``), :func:`combine`
+  (``src/flash_moe/moe_layer.py:70-106``), :func:`shared_expert_forward`
+  (``src/flash_moe/shared_expert.py:221-251``) and :func:`max_relative_error`
+  (``src/flash_moe/dequant.py:198-202``).
+* ``gguf_quants_np``: an independent vectorised restatement of the published
+  ``gguf.quants`` dequantizers, used by the tests to pin the C restatement.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle_kquant.so"
+
+BLOCK = {8: (32, 34), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile the C restatement (make -C oracle)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(f"{LIB_PATH} is not built; run `make -C oracle`")
+        L = C.CDLL(str(LIB_PATH))
+        L.oracle_dequant_k.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int]
+        L.oracle_dequant_k.restype = C.c_int
+        L.oracle_dequant_k_supported.argtypes = [C.c_int]
+        L.oracle_dequant_k_block_size.argtypes = [C.c_int]
+        L.oracle_moe_quant_expert.argtypes = [C.c_int, C.c_void_p, C.c_int64] * 3 + [
+            C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int]
+        L.oracle_moe_quant_expert.restype = C.c_int
+        L.oracle_f32_to_f16.argtypes = [C.c_float]
+        L.oracle_f32_to_f16.restype = C.c_uint16
+        L.oracle_f16_to_f32.argtypes = [C.c_uint16]
+        L.oracle_f16_to_f32.restype = C.c_float
+        L.oracle_f32_to_f16_array.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
+        L.oracle_f16_to_f32_array.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
+        _lib = L
+    return _lib
+
+
+def f32_to_f16_bits(values) -> np.ndarray:
+    v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    out = np.empty(v.size, np.uint16)
+    lib().oracle_f32_to_f16_array(v.ctypes.data, out.ctypes.data, v.size)
+    return out
+
+
+def f16_bits_to_f32(bits) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16).reshape(-1)
+    out = np.empty(b.size, np.float32)
+    lib().oracle_f16_to_f32_array(b.ctypes.data, out.ctypes.data, b.size)
+    return out
+
+
+def dequant_k(ggml_type: int, raw, n: int, want_f16: bool = False):
+    """(status, values) exactly as ``dequant_k`` (dequant_k.cpp:350-394)."""
+    src = np.ascontiguousarray(np.frombuffer(bytes(raw), np.uint8) if isinstance(raw, (bytes, bytearray))
+                               else raw, dtype=np.uint8)
+    out = np.zeros(max(int(n), 0), np.float16 if want_f16 else np.float32)
+    rc = lib().oracle_dequant_k(int(ggml_type), src.ctypes.data, out.ctypes.data, int(n), int(bool(want_f16)))
+    return rc, out
+
+
+def dequant(ggml_type: int, raw, n: int | None = None, want_f16: bool = False) -> np.ndarray:
+    src = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
+    bs, pb = BLOCK[int(ggml_type)]
+    if n is None:
+        n = src.size // pb * bs
+    rc, out = dequant_k(ggml_type, src, n, want_f16)
+    if rc != 0:
+        raise RuntimeError(f"oracle dequant_k failed with status {rc}")
+    return out
+
+
+def moe_quant_expert(tensors: dict, kinds: dict, x, hidden: int, intermediate: int,
+                     fp16_graph: int = 0):
+    """(status, y) with the argument meaning of ``moe_quant_expert``
+    (moe_quant_dot.cpp:171-214).  ``tensors`` maps gate/up/down to raw bytes."""
+    arrays = [np.ascontiguousarray(np.frombuffer(bytes(tensors[k]), np.uint8) if
+                                   isinstance(tensors[k], (bytes, bytearray)) else tensors[k],
+                                   dtype=np.uint8).reshape(-1) for k in ("gate", "up", "down")]
+    args = []
+    for name, raw in zip(("gate", "up", "down"), arrays):
+        args.extend((int(kinds[name]), raw.ctypes.data, raw.nbytes))
+    xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.zeros(hidden, np.float32)
+    rc = lib().oracle_moe_quant_expert(*args, xv.ctypes.data, int(hidden), int(intermediate),
+                                       out.ctypes.data, int(fp16_graph))
+    return rc, out
+
+
+def expert_forward(tensors, kinds, x, hidden, intermediate, fp16_graph=0) -> np.ndarray:
+    rc, y = moe_quant_expert(tensors, kinds, x, hidden, intermediate, fp16_graph)
+    if rc != 0:
+        raise RuntimeError(f"oracle expert failed with status {rc}")
+    return y
+
+
+# ------------------------------------------------------------ Python semantics
+
+def route(x, router_w: np.ndarray, top_k: int):
+    """``ExpertRouter.route`` (router.py:140-170): FP32 scores ``x @ W`` with W
+    shaped (hidden, experts); top-k by descending argsort; float64 softmax over
+    the selected k; uniform weights if the softmax is not finite."""
+    xv = np.asarray(x, dtype=np.float32).reshape(-1)
+    scores = (xv @ np.asarray(router_w, dtype=np.float32)).astype(np.float32)
+    idx = np.argsort(scores)[-top_k:][::-1].astype(np.int64).tolist()
+    sel = scores[idx].astype(np.float64)
+    e = np.exp(sel - np.max(sel))
+    total = e.sum()
+    if not np.isfinite(total) or total <= 0.0:
+        w = np.full(len(idx), 1.0 / len(idx))
+    else:
+        w = e / total
+    return idx, [float(v) for v in w]
+
+
+def combine(expert_outputs, weights, shared_out=None) -> np.ndarray:
+    """Weighted sum of ``run_moe_layer`` (moe_layer.py:70-106): FP32 accumulator,
+    ``combined += w_k * y_k`` in top-k order with the Python-float weight cast to
+    FP32 (NumPy 2 scalar promotion), then ``+ shared``."""
+    combined = np.zeros(np.asarray(expert_outputs[0]).shape[-1], dtype=np.float32)
+    for y, w in zip(expert_outputs, weights):
+        # route() hands out Python floats (router.py:170): a weak scalar, so the
+        # product is taken in FP32
+        combined += float(w) * np.asarray(y, dtype=np.float32)
+    if shared_out is not None:
+        combined = combined + shared_out
+    return combined
+
+
+def _sigmoid(x: np.ndarray) -> np.ndarray:
+    """Stable sigmoid of shared_expert.py:55-62."""
+    x = np.asarray(x)
+    out = np.empty_like(x)
+    pos = x >= 0
+    out[pos] = 1.0 / (1.0 + np.exp(-x[pos]))
+    e = np.exp(x[~pos])
+    out[~pos] = e / (1.0 + e)
+    return out
+
+
+def shared_expert_forward(x, w_gate, w_up, w_down, gate_inp=None) -> np.ndarray:
+    """``SharedExpert.forward`` (shared_expert.py:221-251) on weights that were
+    FP16-dequantized and promoted to FP32 (shared_expert.py:141-149):
+    ``sigmoid(x . g_inp) * (W_d (silu(W_g x) * (W_u x)))``.  With ``gate_inp``
+    None the sigmoid scale is omitted."""
+    xv = np.asarray(x, dtype=np.float32).reshape(-1)
+    g = xv @ np.asarray(w_gate, dtype=np.float32).T
+    act = (g * _sigmoid(g)) * (xv @ np.asarray(w_up, dtype=np.float32).T)
+    out = act @ np.asarray(w_down, dtype=np.float32).T
+    if gate_inp is None:
+        return out.astype(np.float32)
+    gate = _sigmoid((xv @ np.asarray(gate_inp, dtype=np.float32)).reshape(()))
+    return (gate * out).astype(np.float32)
+
+
+def max_relative_error(actual: np.ndarray, reference: np.ndarray) -> float:
+    """The reference's parity metric (dequant.py:198-202): max|a-r| / max|r|."""
+    reference = np.asarray(reference)
+    scale = float(np.abs(reference).max())
+    if scale == 0.0:
+        return float(np.abs(actual).max())
+    return float(np.abs(np.asarray(actual).astype(np.float64) - reference).max() / scale)

@@ -1,0 +1,58 @@
+"""Shared pytest setup.
+
+Markers: ``gpu`` -- needs a HIP GPU (MI355X); everything else runs on the CPU.
+The CPU oracle (``oracle/``) is the checker for every parity test.
+"""
+from __future__ import annotations
+
+import os
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+PKG_DIR = ROOT / "intel-optimized-moe-streaming_amd"
+for p in (str(ROOT), str(PKG_DIR)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+REFERENCE = Path(os.environ.get("MQH_REFERENCE_TREE", "/root/reference"))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a HIP GPU (gfx950)")
+
+
+def gpu_available() -> bool:
+    try:
+        import torch
+    except ImportError:
+        return False
+    return torch.cuda.is_available()
+
+
+@pytest.fixture(scope="session")
+def oracle_mod():
+    import oracle
+
+    if not oracle.LIB_PATH.exists():
+        oracle.build()
+    oracle.lib()
+    return oracle
+
+
+@pytest.fixture(scope="session")
+def hip():
+    """The HIP library (ctypes); GPU tests only."""
+    if not gpu_available():
+        pytest.skip("no HIP GPU")
+    from flash_moe_hip import _lib
+
+    return _lib.load()
+
+
+@pytest.fixture
+def rng():
+    return np.random.default_rng(1234)

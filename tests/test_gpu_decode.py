@@ -1,0 +1,162 @@
+"""Fused decode (all routed experts + shared expert in one call) against the oracle.
+
+The oracle layer is the reference's run_moe_layer arithmetic: each routed
+expert through moe_quant_expert, ``combined += w_k * y_k`` in top-k order
+(FP32), plus ``sigmoid(x . g_inp) * shared(x)``.  Tolerance: max relative
+error <= 1e-3.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+ROLES = ("gate", "up", "down")
+
+
+def make_layer(seed, n_experts, H, I, types, shared_types=None, sh_I=None, scale=0.01):
+    from flash_moe_hip.layer_store import ExpertLayer
+    from flash_moe_hip.synthetic import random_stack
+
+    rng = np.random.default_rng(seed)
+    shapes = {"gate": (I, H), "up": (I, H), "down": (H, I)}
+    host = {r: random_stack(rng, types[r], n_experts, *shapes[r], scale=scale) for r in ROLES}
+    shared = None
+    if shared_types is not None:
+        sh_I = sh_I or I
+        sshapes = {"gate": (sh_I, H), "up": (sh_I, H), "down": (H, sh_I)}
+        shared = {r: random_stack(rng, shared_types[r], 1, *sshapes[r], scale=scale) for r in ROLES}
+        shared.update(types=shared_types, intermediate=sh_I,
+                      gate_inp=(rng.standard_normal(H) * 0.02).astype(np.float32))
+    layer = ExpertLayer.from_host(host, types, n_experts, H, I, shared=shared)
+    return layer, host, shared
+
+
+def host_expert(host, layer, e):
+    return {r: host[r][e * layer.expert_bytes(r):(e + 1) * layer.expert_bytes(r)] for r in ROLES}
+
+
+def oracle_layer(oracle_mod, layer, host, shared, x, ids, weights, fp16=0, shared_semantics="kernel"):
+    H, I = layer.hidden, layer.intermediate
+    outs = [oracle_mod.expert_forward(host_expert(host, layer, e), layer.types, x, H, I, fp16) for e in ids]
+    sh_out = None
+    if shared is not None:
+        gate = oracle_mod._sigmoid(np.float32(x @ shared["gate_inp"]).reshape(()))
+        if shared_semantics == "kernel":
+            y = oracle_mod.expert_forward({r: shared[r] for r in ROLES}, shared["types"], x, H,
+                                          shared["intermediate"], 0)
+            sh_out = (gate * y).astype(np.float32)
+        else:   # reference SharedExpert: FP16-dequantized weights promoted to FP32
+            si = shared["intermediate"]
+            w = {r: oracle_mod.dequant(shared["types"][r], shared[r], want_f16=True).astype(np.float32)
+                 for r in ROLES}
+            sh_out = oracle_mod.shared_expert_forward(x, w["gate"].reshape(si, H), w["up"].reshape(si, H),
+                                                      w["down"].reshape(H, si), shared["gate_inp"])
+    return oracle_mod.combine(outs, weights, sh_out)
+
+
+def run(layer, X, ids, ws, fp16=0, use_shared=True):
+    import torch
+
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    runner = MoeRunner()
+    x = torch.from_numpy(np.ascontiguousarray(X, np.float32)).cuda()
+    tid = torch.from_numpy(np.ascontiguousarray(ids, np.int32)).cuda() if ids is not None else None
+    tw = torch.from_numpy(np.ascontiguousarray(ws, np.float32)).cuda() if ws is not None else None
+    y = runner.decode(layer, x, tid, tw, fp16_graph=fp16, use_shared=use_shared)
+    out = y.cpu().numpy()
+    return out, runner.status()
+
+
+@pytest.fixture(scope="module")
+def decode_layer(hip):
+    # 32 experts of the benchmark shape: gate/up Q4_K [512x2048], down Q6_K, shared the same
+    types = {"gate": 12, "up": 12, "down": 14}
+    return make_layer(7, 32, 2048, 512, types, shared_types=types)
+
+
+def test_one_token_top8_plus_shared(decode_layer, oracle_mod):
+    layer, host, shared = decode_layer
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(2048).astype(np.float32)
+    W = (rng.standard_normal((2048, 32)) * 0.02).astype(np.float32)
+    ids, ws = oracle_mod.route(x, W, 8)
+    print(f"decode 1 token ids={ids}", flush=True)
+    got, st = run(layer, x[None], np.array([ids]), np.array([ws]))
+    assert st == 0
+    want = oracle_layer(oracle_mod, layer, host, shared, x, ids, ws)
+    err = oracle_mod.max_relative_error(got[0], want)
+    print(f"  max rel err (kernel semantics) {err:.3e}", flush=True)
+    assert err <= TOL
+    want_ref = oracle_layer(oracle_mod, layer, host, shared, x, ids, ws, shared_semantics="reference")
+    err_ref = oracle_mod.max_relative_error(got[0], want_ref)
+    print(f"  max rel err (reference shared semantics) {err_ref:.3e}", flush=True)
+    assert err_ref <= TOL
+
+
+def test_shared_only_and_no_shared(decode_layer, oracle_mod):
+    layer, host, shared = decode_layer
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((3, 2048)).astype(np.float32)
+    got, st = run(layer, x, None, None)
+    assert st == 0
+    for t in range(3):
+        want = oracle_layer(oracle_mod, layer, host, shared, x[t], [], [])
+        assert oracle_mod.max_relative_error(got[t], want) <= TOL
+    ids = np.array([[3, 5], [0, 31], [7, 7]])
+    ws = np.array([[0.75, 0.25], [0.5, 0.5], [0.1, 0.9]])
+    got, st = run(layer, x, ids, ws, use_shared=False)
+    assert st == 0
+    for t in range(3):
+        want = oracle_layer(oracle_mod, layer, host, None, x[t], ids[t], ws[t])
+        assert oracle_mod.max_relative_error(got[t], want) <= TOL
+
+
+def test_bad_expert_id_is_reported(decode_layer):
+    layer, _, _ = decode_layer
+    x = np.ones((1, 2048), np.float32)
+    _, st = run(layer, x, np.array([[1, 32]]), np.array([[0.5, 0.5]]))
+    assert st == -9
+    _, st = run(layer, x, np.array([[1, 2]]), np.array([[0.5, 0.5]]))
+    assert st == 0
+
+
+def test_batched_tokens_q3k(hip, oracle_mod):
+    """16 tokens through an all-Q3_K layer, top-8 of N(0,1) logits (experts overlap)."""
+    types = {"gate": 11, "up": 11, "down": 11}
+    layer, host, shared = make_layer(11, 24, 2048, 512, types, shared_types=types)
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((16, 2048)).astype(np.float32)
+    logits = rng.standard_normal((16, 24)).astype(np.float32)
+    ids = np.argsort(-logits, axis=1)[:, :8]
+    sel = np.take_along_axis(logits, ids, 1).astype(np.float64)
+    ws = np.exp(sel - sel.max(1, keepdims=True))
+    ws /= ws.sum(1, keepdims=True)
+    got, st = run(layer, X, ids, ws)
+    assert st == 0
+    worst = 0.0
+    for t in range(16):
+        want = oracle_layer(oracle_mod, layer, host, shared, X[t], ids[t].tolist(), ws[t].tolist())
+        worst = max(worst, oracle_mod.max_relative_error(got[t], want))
+    print(f"batched q3k worst max rel err {worst:.3e}", flush=True)
+    assert worst <= TOL
+
+
+def test_fp16_graph_routed_experts(hip, oracle_mod):
+    """FP16 graph on the routed experts (small-magnitude inputs as in the reference KAT),
+    FP32 graph on the shared expert."""
+    types = {"gate": 12, "up": 13, "down": 14}
+    layer, host, shared = make_layer(13, 8, 256, 256, types, shared_types={"gate": 14, "up": 14, "down": 14},
+                                     scale=0.002)
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal(256) * 0.005).astype(np.float32)
+    ids, ws = [5, 1, 2], [0.5, 0.3, 0.2]
+    got, st = run(layer, x[None], np.array([ids]), np.array([ws]), fp16=1)
+    assert st == 0
+    want = oracle_layer(oracle_mod, layer, host, shared, x, ids, ws, fp16=1)
+    err = oracle_mod.max_relative_error(got[0], want)
+    print(f"fp16 graph max rel err {err:.3e}", flush=True)
+    assert err <= 5e-3

@@ -1,0 +1,98 @@
+"""GPU dequantization is bit-identical to the oracle (dequant_k contract).
+
+Covers every type, FP32 and FP16 output, random blocks with the benchmark
+distributions, edge blocks (zero/negative/subnormal/max scales, saturated
+quant bytes), the host-pointer drop-in ``dequant_k`` and the device entry
+``mqh_dequant``, and -- at the full standalone-dequant workload (256 experts x
+gate/up/down of 512x2048) -- every value of every type.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from test_oracle_pin import edge_blocks, random_blocks
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [8, 11, 12, 13, 14]
+BLOCK = {8: (32, 34), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+
+
+def _blocks(t, n=2048, seed=0):
+    rng = np.random.default_rng(seed + t)
+    from flash_moe_hip.synthetic import random_blocks as bench_blocks
+
+    return np.concatenate([bench_blocks(rng, t, n), random_blocks(rng, t, 256), edge_blocks(t)]).reshape(-1)
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("f16", [0, 1])
+def test_host_dequant_k_bit_exact(hip, oracle_mod, t, f16):
+    print(f"dequant_k type={t} f16={f16}", flush=True)
+    data = _blocks(t)
+    bs, pb = BLOCK[t]
+    n = data.size // pb * bs
+    out = np.zeros(n, np.uint16 if f16 else np.float32)
+    assert hip.dequant_k(t, data.ctypes.data, out.ctypes.data, n, f16) == 0
+    rc, want = oracle_mod.dequant_k(t, data, n, bool(f16))
+    assert rc == 0
+    got_bits = out.view(np.uint16) if f16 else out.view(np.uint32)
+    want_bits = want.view(np.uint16) if f16 else want.view(np.uint32)
+    bad = np.nonzero(got_bits != want_bits)[0]
+    assert bad.size == 0, f"{bad.size} values differ, first at {bad[:5]}"
+    assert hip.dequant_k(t, data.ctypes.data, out.ctypes.data, n + 1, f16) == -1
+
+
+def test_package_dequant_helpers(hip, oracle_mod):
+    from flash_moe_hip import dequant
+
+    data = _blocks(12, 64)
+    n = data.size // 144 * 256
+    buf = np.empty(n, np.float16)
+    got = dequant.dequant_to_f16(data.tobytes(), 12, n, out=buf)
+    assert got is buf
+    np.testing.assert_array_equal(got.view(np.uint16), oracle_mod.dequant(12, data, want_f16=True).view(np.uint16))
+    np.testing.assert_array_equal(dequant.dequantize(data, 12).view(np.uint32),
+                                  oracle_mod.dequant(12, data).view(np.uint32))
+    with pytest.raises(RuntimeError):
+        dequant.dequant_to_f16(data.tobytes(), 99, n)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_device_dequant_bit_exact(hip, oracle_mod, t):
+    import torch
+
+    from flash_moe_hip.dequant import dequant_device
+
+    print(f"mqh_dequant type={t}", flush=True)
+    data = _blocks(t, 4096, seed=9)
+    src = torch.from_numpy(data).cuda()
+    for dtype, view in ((torch.float16, np.uint16), (torch.float32, np.uint32)):
+        got = dequant_device(src, t, dtype=dtype).cpu().numpy().view(view)
+        want = oracle_mod.dequant(t, data, want_f16=dtype == torch.float16).view(view)
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("t", [11, 12, 14, 8])
+def test_full_workload_every_value(hip, oracle_mod, t):
+    """256 experts x (gate, up, down) = 768 matrices of 1,048,576 values, generated on
+    the GPU, dequantized to FP16 on the GPU and compared value by value with the oracle."""
+    import torch
+
+    from flash_moe_hip.dequant import dequant_device
+    from flash_moe_hip.synthetic import torch_random_stack
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2024 + t)
+    for role, (rows, cols) in (("gate", (512, 2048)), ("up", (512, 2048)), ("down", (2048, 512))):
+        print(f"full dequant type={t} role={role}", flush=True)
+        stack = torch_random_stack(t, 256, rows, cols, generator=g, device="cuda")
+        out = dequant_device(stack, t)
+        torch.cuda.synchronize()
+        host_src = stack.cpu().numpy()
+        got = out.cpu().numpy().view(np.uint16)
+        want = oracle_mod.dequant(t, host_src, want_f16=True).view(np.uint16)
+        bad = int(np.count_nonzero(got != want))
+        assert bad == 0, f"{role}: {bad} of {got.size} values differ"
+        del stack, out

@@ -81,9 +81,6 @@ def step_bytes(layer) -> int:
 def parity_check(layer, x, ids, ws, y_gpu) -> float:
     import oracle
 
-    def sl(src, e):
-        return {r: src[r] for r in src} if e < 0 else layer.host_expert(e)
-
     outs = [oracle.expert_forward(layer.host_expert(int(e)), TYPES, x, H, I, 0) for e in ids]
     sh = layer.host_shared()
     gate = oracle._sigmoid(np.float32(x @ layer.shared.gate_inp.cpu().numpy()).reshape(()))
@@ -142,6 +139,9 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch every step from Python instead of a graph")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="run one device-to-device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -179,25 +179,39 @@ def main() -> int:
         log("PARITY FAILURE")
         return 3
 
-    # capture one sweep over all layers as a graph
-    graph = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream(dev)
-    cap.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(cap):
-        sweep()
-    torch.cuda.current_stream(dev).wait_stream(cap)
-    torch.cuda.synchronize()
-    with torch.cuda.graph(graph, stream=cap):
-        sweep()
+    if args.calib_copy_mb:
+        n = args.calib_copy_mb << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy of {n} bytes done")
+        del src, dst
+
     reps_w = max(1, args.warmup // args.layers)
     reps = max(1, args.steps // args.layers)
+    if args.eager:
+        run_sweep = sweep
+    else:
+        # capture one sweep over all layers as a graph
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream(dev)
+        cap.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(cap):
+            sweep()
+        torch.cuda.current_stream(dev).wait_stream(cap)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=cap):
+            sweep()
+        run_sweep = graph.replay
     for _ in range(reps_w):
-        graph.replay()
+        run_sweep()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(reps):
-        graph.replay()
+        run_sweep()
     end.record()
     end.synchronize()
     assert runner.status() == 0, "kernel fault during timing"
@@ -241,7 +255,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "fused decode step (gate/up kernel + down/combine kernel)",
+            "kernel": "k_moe_fused (single launch per token-layer)",
         },
     }
     if not args.no_cpu_baseline:

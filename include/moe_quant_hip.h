@@ -105,6 +105,12 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
                    const float* x, int n_tokens, const int32_t* ids, const float* weights, int top_k,
                    float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Select the kernels behind mqh_moe_decode and moe_quant_expert: 0 (default)
+ * = the single-launch fused kernel whenever the shapes and types allow it,
+ * else the generic two-kernel path; 1 = always the generic path.  Process-wide;
+ * returns the previous setting, or -1 for another value. */
+int mqh_set_decode_path(int path);
+
 /* Zero a workspace (flags and counters) on `stream`. */
 int mqh_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
 

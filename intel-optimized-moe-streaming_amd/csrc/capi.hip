@@ -19,6 +19,15 @@ constexpr int ST_OK = 0, ST_ARG = -1, ST_TYPE = -2, ST_BYTES = -3, ST_NONFINITE 
 
 bool supported(int t) { return block_size(t) != 0; }
 
+// 0: fused single-launch kernel when the shapes allow it, 1: always the
+// generic two-kernel path
+int g_decode_path = 0;
+
+hipError_t launch_decode(const DecodeParams& p, hipStream_t s) {
+    if (g_decode_path == 0 && fused_supported(p)) return launch_decode_fused(p, p.flags + CTR_BASE, s);
+    return launch_decode_generic(p, s);
+}
+
 // Expected bytes of a [rows x cols] matrix, or a negative status.
 int64_t matrix_bytes(int type, int rows, int cols) {
     const int bs = block_size(type);
@@ -200,7 +209,7 @@ int moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes, int
         hipMemcpyAsync(W + off_down, down, down_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
         hipMemcpyAsync(IO, input, (size_t)hidden * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
         hipMemcpyAsync(IO + off_id, &route, sizeof(route), hipMemcpyHostToDevice, c->stream) == hipSuccess &&
-        launch_decode_generic(p, c->stream) == hipSuccess &&
+        launch_decode(p, c->stream) == hipSuccess &&
         hipMemcpyAsync(output, IO + off_y, (size_t)hidden * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess)
         status = read_and_clear_flags(p.flags, c->stream);
     release_ctx(c);
@@ -279,7 +288,14 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
     p.flags = (int*)(WS + wl.flags_off); p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
     p.S = top_k + (has_shared ? 1 : 0);
     p.Imax = std::max(intermediate, has_shared ? sh_intermediate : 0);
-    return launch_decode_generic(p, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
+    return launch_decode(p, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
+}
+
+int mqh_set_decode_path(int path) {
+    if (path != 0 && path != 1) return ST_ARG;
+    const int old = g_decode_path;
+    g_decode_path = path;
+    return old;
 }
 
 }  // extern "C"

@@ -146,7 +146,8 @@ def combine(expert_outputs, weights, shared_out=None) -> np.ndarray:
     """Weighted sum of ``run_moe_layer`` (moe_layer.py:70-106): FP32 accumulator,
     ``combined += w_k * y_k`` in top-k order with the Python-float weight cast to
     FP32 (NumPy 2 scalar promotion), then ``+ shared``."""
-    combined = np.zeros(np.asarray(expert_outputs[0]).shape[-1], dtype=np.float32)
+    width = np.asarray(expert_outputs[0] if len(expert_outputs) else shared_out).shape[-1]
+    combined = np.zeros(width, dtype=np.float32)
     for y, w in zip(expert_outputs, weights):
         # route() hands out Python floats (router.py:170): a weak scalar, so the
         # product is taken in FP32

@@ -1,0 +1,75 @@
+"""The fused decode's integer-digit dot products, built for the host, against the oracle (CPU only).
+
+tests/cpu/chunk_check.cpp compiles kquant_dot.h -- the same __host__
+__device__ code the gfx950 kernel runs, with v_dot4_i32_i8 emulated -- and
+computes full row dot products chunk by chunk.  They must match the FP64 dot
+product of the oracle-dequantized row to ~1e-6 of sum|w*x| (the digit split
+keeps 20 bits of each 32-column group's maximum).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import PKG_DIR, ROOT
+
+SRC = ROOT / "tests" / "cpu" / "chunk_check.cpp"
+OUT = ROOT / "tests" / "cpu" / "_build" / "libchunkcheck.so"
+
+
+@pytest.fixture(scope="module")
+def chk():
+    deps = [SRC, PKG_DIR / "csrc" / "kquant_dot.h", PKG_DIR / "csrc" / "kquant_device.h"]
+    if not OUT.exists() or OUT.stat().st_mtime < max(d.stat().st_mtime for d in deps):
+        OUT.parent.mkdir(exist_ok=True)
+        subprocess.run(["hipcc", "-O2", "-std=c++17", "-fPIC", "-shared", "-x", "hip", "--offload-arch=gfx950",
+                        f"-I{PKG_DIR / 'csrc'}", str(SRC), "-o", str(OUT)], check=True, capture_output=True)
+    L = C.CDLL(str(OUT))
+    L.mqh_cpu_row_dot.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p]
+    L.mqh_cpu_row_dot.restype = C.c_float
+    L.mqh_cpu_digit_roundtrip.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
+    return L
+
+
+def activations(rng, n, kind):
+    if kind == "normal":
+        return rng.standard_normal(n).astype(np.float32)
+    if kind == "heavy":
+        return (rng.standard_t(2, n) * 10.0 ** rng.uniform(-3, 3, n)).astype(np.float32)
+    if kind == "sparse":
+        x = rng.standard_normal(n).astype(np.float32)
+        x[rng.random(n) < 0.7] = 0.0
+        return x
+    return (rng.standard_normal(n) * 1e4).astype(np.float32)
+
+
+@pytest.mark.parametrize("t", [11, 12, 13, 14])
+@pytest.mark.parametrize("kind", ["normal", "heavy", "sparse", "large"])
+def test_row_dot_matches_oracle(chk, oracle_mod, t, kind):
+    from flash_moe_hip.synthetic import random_tensor
+
+    rng = np.random.default_rng(100 * t + len(kind))
+    for ncols in (256, 512, 2048):
+        rows = random_tensor(rng, t, 8, ncols).reshape(8, -1)
+        w = oracle_mod.dequant(t, rows).reshape(8, ncols).astype(np.float64)
+        for r in range(8):
+            x = activations(rng, ncols, kind)
+            got = chk.mqh_cpu_row_dot(t, rows[r].ctypes.data, ncols, x.ctypes.data)
+            want = float(w[r] @ x.astype(np.float64))
+            # digit error <= 2^-20 * (group max) per value, plus FP32 rounding of the sums
+            gmax = np.abs(x.reshape(-1, 32)).max(axis=1).repeat(32).astype(np.float64)
+            bound = 2.0 ** -20 * float(np.abs(w[r]) @ gmax) + 1e-6 * float(np.abs(w[r] * x).sum()) + 1e-30
+            assert abs(got - want) <= bound, (ncols, r, got, want, bound)
+
+
+def test_digit_roundtrip_bound(chk):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(4096), rng.standard_t(1, 4096) * 1e3,
+                        np.zeros(64), np.full(32, 1e-30), np.full(32, -3e30)]).astype(np.float32)
+    out = np.empty_like(x)
+    chk.mqh_cpu_digit_roundtrip(x.ctypes.data, x.size, out.ctypes.data)
+    gmax = np.abs(x.reshape(-1, 32)).max(axis=1).repeat(32)
+    assert np.all(np.abs(out.astype(np.float64) - x) <= 2.0 ** -20 * gmax + 1e-45)

@@ -71,6 +71,14 @@ def run(layer, X, ids, ws, fp16=0, use_shared=True):
     return out, runner.status()
 
 
+@pytest.fixture(params=[0, 1], ids=["fused", "generic"])
+def path(request, hip):
+    """Run the test through the single-launch fused kernel and the generic kernels."""
+    old = hip.mqh_set_decode_path(request.param)
+    yield request.param
+    hip.mqh_set_decode_path(old)
+
+
 @pytest.fixture(scope="module")
 def decode_layer(hip):
     # 32 experts of the benchmark shape: gate/up Q4_K [512x2048], down Q6_K, shared the same
@@ -78,13 +86,13 @@ def decode_layer(hip):
     return make_layer(7, 32, 2048, 512, types, shared_types=types)
 
 
-def test_one_token_top8_plus_shared(decode_layer, oracle_mod):
+def test_one_token_top8_plus_shared(decode_layer, oracle_mod, path):
     layer, host, shared = decode_layer
     rng = np.random.default_rng(1)
     x = rng.standard_normal(2048).astype(np.float32)
     W = (rng.standard_normal((2048, 32)) * 0.02).astype(np.float32)
     ids, ws = oracle_mod.route(x, W, 8)
-    print(f"decode 1 token ids={ids}", flush=True)
+    print(f"decode 1 token path={path} ids={ids}", flush=True)
     got, st = run(layer, x[None], np.array([ids]), np.array([ws]))
     assert st == 0
     want = oracle_layer(oracle_mod, layer, host, shared, x, ids, ws)
@@ -97,7 +105,7 @@ def test_one_token_top8_plus_shared(decode_layer, oracle_mod):
     assert err_ref <= TOL
 
 
-def test_shared_only_and_no_shared(decode_layer, oracle_mod):
+def test_shared_only_and_no_shared(decode_layer, oracle_mod, path):
     layer, host, shared = decode_layer
     rng = np.random.default_rng(2)
     x = rng.standard_normal((3, 2048)).astype(np.float32)
@@ -115,7 +123,7 @@ def test_shared_only_and_no_shared(decode_layer, oracle_mod):
         assert oracle_mod.max_relative_error(got[t], want) <= TOL
 
 
-def test_bad_expert_id_is_reported(decode_layer):
+def test_bad_expert_id_is_reported(decode_layer, path):
     layer, _, _ = decode_layer
     x = np.ones((1, 2048), np.float32)
     _, st = run(layer, x, np.array([[1, 32]]), np.array([[0.5, 0.5]]))
@@ -124,7 +132,7 @@ def test_bad_expert_id_is_reported(decode_layer):
     assert st == 0
 
 
-def test_batched_tokens_q3k(hip, oracle_mod):
+def test_batched_tokens_q3k(hip, oracle_mod, path):
     """16 tokens through an all-Q3_K layer, top-8 of N(0,1) logits (experts overlap)."""
     types = {"gate": 11, "up": 11, "down": 11}
     layer, host, shared = make_layer(11, 24, 2048, 512, types, shared_types=types)
@@ -141,7 +149,7 @@ def test_batched_tokens_q3k(hip, oracle_mod):
     for t in range(16):
         want = oracle_layer(oracle_mod, layer, host, shared, X[t], ids[t].tolist(), ws[t].tolist())
         worst = max(worst, oracle_mod.max_relative_error(got[t], want))
-    print(f"batched q3k worst max rel err {worst:.3e}", flush=True)
+    print(f"batched q3k path={path} worst max rel err {worst:.3e}", flush=True)
     assert worst <= TOL
 
 
@@ -160,3 +168,50 @@ def test_fp16_graph_routed_experts(hip, oracle_mod):
     err = oracle_mod.max_relative_error(got[0], want)
     print(f"fp16 graph max rel err {err:.3e}", flush=True)
     assert err <= 5e-3
+
+
+@pytest.mark.parametrize("types", [(12, 14), (11, 11), (13, 12), (14, 14), (12, 13), (11, 14)])
+def test_fused_type_pairs_against_generic(hip, oracle_mod, types):
+    """Every (gate/up, down) type pair of the fused kernel, 3 tokens, H=I=256 and H=2048/I=512,
+    against the oracle."""
+    gu, dn = types
+    t = {"gate": gu, "up": gu, "down": dn}
+    for H, I in ((256, 256), (2048, 512), (512, 1024)):
+        print(f"fused types={types} H={H} I={I}", flush=True)
+        layer, host, shared = make_layer(29 + gu + dn, 6, H, I, t, shared_types=t)
+        rng = np.random.default_rng(H + I)
+        X = rng.standard_normal((3, H)).astype(np.float32)
+        ids = np.array([[0, 5, 2], [3, 3, 1], [4, 0, 5]])
+        ws = np.array([[0.5, 0.3, 0.2], [0.6, 0.2, 0.2], [0.4, 0.4, 0.2]])
+        old = hip.mqh_set_decode_path(0)
+        try:
+            got, st = run(layer, X, ids, ws)
+        finally:
+            hip.mqh_set_decode_path(old)
+        assert st == 0
+        for tok in range(3):
+            want = oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist())
+            err = oracle_mod.max_relative_error(got[tok], want)
+            assert err <= TOL, (types, H, I, tok, err)
+
+
+def test_fused_repeated_launches_reset_counters(decode_layer, oracle_mod, hip):
+    """Back-to-back launches on one workspace: the kernel's counters reset themselves."""
+    import torch
+
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    layer, host, shared = decode_layer
+    rng = np.random.default_rng(9)
+    runner = MoeRunner()
+    xs = [rng.standard_normal((1, 2048)).astype(np.float32) for _ in range(5)]
+    ids = [rng.permutation(32)[:8].reshape(1, 8) for _ in range(5)]
+    ws = [rng.dirichlet(np.ones(8)).astype(np.float32).reshape(1, 8) for _ in range(5)]
+    ys = []
+    for k in range(5):
+        ys.append(runner.decode(layer, torch.from_numpy(xs[k]).cuda(),
+                                torch.from_numpy(ids[k].astype(np.int32)).cuda(), torch.from_numpy(ws[k]).cuda()))
+    assert runner.status() == 0
+    for k in range(5):
+        want = oracle_layer(oracle_mod, layer, host, shared, xs[k][0], ids[k][0].tolist(), ws[k][0].tolist())
+        assert oracle_mod.max_relative_error(ys[k].cpu().numpy()[0], want) <= TOL

@@ -106,17 +106,17 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
                    float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Select the kernels behind mqh_moe_decode and moe_quant_expert: 0 (default)
- * = the single-launch fused kernel whenever the shapes and types allow it,
- * else the generic two-kernel path; 1 = always the generic path.  Process-wide;
- * returns the previous setting, or -1 for another value. */
+ * = the integer-digit fast kernels whenever the shapes and types allow it
+ * (FP32 graph, K-quant types, hidden and intermediate in 256..2048), else the
+ * generic kernels; 1 = always the generic kernels.  Process-wide; returns the
+ * previous setting, or -1 for another value. */
 int mqh_set_decode_path(int path);
 
 /* Zero a workspace (flags and counters) on `stream`. */
 int mqh_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Synchronize `stream`, then read and clear the fault flags latched in
- * `workspace`: 0, -4 (non-finite output), -9 (bad expert id), -8 (a kernel
- * gave up waiting on another workgroup) or -5. */
+ * `workspace`: 0, -4 (non-finite output), -9 (bad expert id) or -5. */
 int mqh_status(void* workspace, void* stream);
 
 #ifdef __cplusplus

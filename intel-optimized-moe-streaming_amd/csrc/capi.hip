@@ -15,16 +15,16 @@ using namespace mqh;
 namespace {
 
 constexpr int ST_OK = 0, ST_ARG = -1, ST_TYPE = -2, ST_BYTES = -3, ST_NONFINITE = -4, ST_HIP = -5,
-              ST_WORKSPACE = -6, ST_TIMEOUT = -8, ST_BAD_ID = -9;
+              ST_WORKSPACE = -6, ST_BAD_ID = -9;
 
 bool supported(int t) { return block_size(t) != 0; }
 
-// 0: fused single-launch kernel when the shapes allow it, 1: always the
-// generic two-kernel path
+// 0: the integer-digit fast kernels when the shapes allow it, 1: always the
+// generic kernels
 int g_decode_path = 0;
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s) {
-    if (g_decode_path == 0 && fused_supported(p)) return launch_decode_fused(p, p.flags + CTR_BASE, s);
+    if (g_decode_path == 0 && fast_supported(p)) return launch_decode_fast(p, s);
     return launch_decode_generic(p, s);
 }
 
@@ -112,7 +112,6 @@ int read_and_clear_flags(int* flags_dev, hipStream_t s) {
         if (hipStreamSynchronize(s) != hipSuccess) return ST_HIP;
     }
     if (h[FLAG_BAD_ID]) return ST_BAD_ID;
-    if (h[FLAG_TIMEOUT]) return ST_TIMEOUT;
     if (h[FLAG_NONFINITE]) return ST_NONFINITE;
     return ST_OK;
 }

@@ -56,11 +56,19 @@ __device__ __forceinline__ float h2f(uint32_t bits) {
     return __half2float(__ushort_as_half((unsigned short)bits));
 }
 
-__device__ __forceinline__ uint32_t f2h_rn(float f) {
-    return (uint32_t)__half_as_ushort(__float2half_rn(f));
+// Opaque copy of f.  Without it the instruction selector folds a product that
+// feeds an FP16 conversion into v_fma_mix*_f16 with a +0 addend, and
+// (-0) + (+0) = +0 drops the sign of negative-zero results.
+__device__ __forceinline__ float opaque(float f) {
+    __asm__ volatile("" : "+v"(f));
+    return f;
 }
 
-__device__ __forceinline__ float round16(float f) { return __half2float(__float2half_rn(f)); }
+__device__ __forceinline__ uint32_t f2h_rn(float f) {
+    return (uint32_t)__half_as_ushort(__float2half_rn(opaque(f)));
+}
+
+__device__ __forceinline__ float round16(float f) { return __half2float(__float2half_rn(opaque(f))); }
 
 // byte k of a 64-bit word
 __device__ __forceinline__ uint32_t byte_of(uint64_t w, int k) { return (uint32_t)(w >> (8 * k)) & 0xFFu; }

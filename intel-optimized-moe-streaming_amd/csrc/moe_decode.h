@@ -8,9 +8,8 @@
 
 namespace mqh {
 
-// workspace flag words (int32), sticky until read by mqh_status; words
-// CTR_BASE.. hold the fused kernel's self-resetting counters
-enum : int { FLAG_NONFINITE = 0, FLAG_BAD_ID = 1, FLAG_TIMEOUT = 2, CTR_BASE = 8, N_FLAGS = 64 };
+// workspace flag words (int32), sticky until read by mqh_status
+enum : int { FLAG_NONFINITE = 0, FLAG_BAD_ID = 1, N_FLAGS = 64 };
 
 constexpr int ROWS_A = 8;    // intermediate rows per workgroup, kernel A
 constexpr int ROWS_W = 4;    // hidden rows per wavefront, kernel B
@@ -65,9 +64,19 @@ inline WorkspaceLayout decode_workspace_layout(int n_tokens, int top_k, int inte
     return w;
 }
 
+// Layout of one (token, slot) activation in the fast path's workspace region:
+// digit planes int8 [3][inter] at 0, xs16 float [inter/16] at xs_off, sum8
+// float [inter/8] at sum_off; consecutive (token, slot) pairs act_stride apart
+// (at most 4 * inter bytes, the generic path's FP32 row).
+struct FastLayout {
+    int inter;
+    int64_t xs_off, sum_off, act_stride;
+};
+
 hipError_t launch_decode_generic(const DecodeParams& p, hipStream_t stream);
-bool fused_supported(const DecodeParams& p);
-hipError_t launch_decode_fused(const DecodeParams& p, int* counters, hipStream_t stream);
+bool fast_supported(const DecodeParams& p);
+FastLayout fast_layout(int inter);
+hipError_t launch_decode_fast(const DecodeParams& p, hipStream_t stream);
 hipError_t launch_dequant(int type, const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream);
 
 }  // namespace mqh

@@ -1,0 +1,445 @@
+// moe_fast.hip -- the decode fast path: fused quantized SwiGLU experts for a few
+// tokens, as two kernels with no inter-workgroup synchronisation.
+//
+// Same result as the generic kernels of moe_decode.hip (formula and reference
+// lines there): for every token t and slot s (the top-k routed experts in order,
+// then the optional shared expert)
+//   act[t,s] = silu(W_gate x_t) * (W_up x_t)
+//   y[t]     = sum_s w[t,s] * W_down act[t,s]   (+ sigmoid(x_t . g_inp) * shared)
+//
+// Kernel A  grid (I / RA, S, T), 256 threads.  A workgroup computes RA
+//           consecutive intermediate rows of one (token, slot): the token's
+//           activation digits go to LDS, each lane keeps the digits of its 32
+//           columns in registers for all its rows, and the gate and up rows'
+//           quantized bytes are all requested before any arithmetic.  The RA
+//           results are published as digits (16-row runs) to the workspace.
+// Kernel B  grid (H / RB, T), 64*S threads: wave s computes the down rows of
+//           slot s for RB output rows, then the workgroup combines the slots
+//           in top-k order (+ shared) from LDS.
+//
+// Lanes follow kquant_lane.h: lane k of a super-block owns 32 of its weights,
+// so a row of C columns is C/32 consecutive lanes and an instruction covers
+// 64/(C/32) rows.  Every weight byte is read once per (token, slot).
+//
+// Supported (checked by fast_supported): FP32 graph; types Q3_K/Q4_K/Q5_K/Q6_K
+// with gate type == up type; hidden and intermediate in {256, 512, 1024, 2048};
+// at most 16 slots; a shared expert with the routed types and intermediate size.
+#include "kquant_lane.h"
+#include "moe_decode.h"
+
+namespace mqh {
+
+constexpr int FAST_MAX_SLOTS = 16;
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g * (1.0f / (1.0f + expf(-g)))) * u; }
+
+__device__ __forceinline__ float sigmoid_stable(float v) {
+    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+
+// Sum over aligned groups of W lanes (W = 8, 16, 32 or 64); every lane of a
+// group receives the group's sum, in a fixed butterfly order (deterministic).
+// Partners within 32 lanes come from ds_swizzle (bit mode: lane ^ m), across
+// the halves from ds_bpermute.  DPP row operations would keep this in the VALU,
+// but hipcc's DPP combining of this reduction gave intermittently wrong sums on
+// gfx950, so the LDS crossbar forms are used.
+template <int M>
+__device__ __forceinline__ float swz_xor(float v) {
+    static_assert(M > 0 && M < 32, "swizzle xor mask");
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (M << 10)));
+}
+
+template <int W>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    static_assert(W == 8 || W == 16 || W == 32 || W == 64, "group width");
+    v += swz_xor<1>(v);
+    v += swz_xor<2>(v);
+    v += swz_xor<4>(v);
+    if constexpr (W > 8) v += swz_xor<8>(v);
+    if constexpr (W > 16) v += swz_xor<16>(v);
+    if constexpr (W > 32) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Wave-uniform value held in a VGPR, as a scalar.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Workspace view of the digits of act[t, s] (I values).
+__device__ __forceinline__ DigitsRef act_digits(const FastLayout& L, uint8_t* base, int t, int s, int S) {
+    uint8_t* p = base + ((int64_t)t * S + s) * L.act_stride;
+    DigitsRef v;
+    v.planes = (const int8_t*)p;
+    v.xs16 = (const float*)(p + L.xs_off);
+    v.sum8 = (const float*)(p + L.sum_off);
+    v.n = L.inter;
+    return v;
+}
+
+// Digits of n values, one value per lane i of consecutive lanes (n a multiple
+// of 16; lanes with i >= n pass v = 0 and write nothing).  Whole wavefronts.
+__device__ __forceinline__ void publish16(float v, int i, int n, int8_t* planes, int plane_stride, float* xs16,
+                                          float* sum8) {
+    float amax = fabsf(v);
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    float s8 = v;
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) s8 += __shfl_xor(s8, off, 64);
+    if (i < n) {
+        const int e = digit_exp(amax);
+        int8_t d0, d1, d2;
+        split_digits(v, e, d0, d1, d2);
+        planes[i] = d0;
+        planes[plane_stride + i] = d1;
+        planes[2 * plane_stride + i] = d2;
+        if ((i & 15) == 0) xs16[i >> 4] = ldexpf(1.0f, e - 14);
+        if ((i & 7) == 0) sum8[i >> 3] = s8;
+    }
+}
+
+// Digits of the H values of token x into LDS, in two steps so the loads can be
+// issued early: x_load reads this thread's VPT = H/NT consecutive values (a
+// whole workgroup of NT threads, VPT in 1..8), x_digits splits them and
+// writes planes, run scales and 8-value sums.
+template <int H, int NT>
+__device__ __forceinline__ void x_load(const float* x, float v[8]) {
+    constexpr int VPT = H / NT;
+    static_assert(VPT >= 1 && VPT <= 8 && (VPT & (VPT - 1)) == 0, "values per thread");
+    const int i0 = threadIdx.x * VPT;
+    if constexpr (VPT == 8) {
+        const float4 a = *(const float4*)(x + i0), b = *(const float4*)(x + i0 + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else if constexpr (VPT == 4) {
+        const float4 a = *(const float4*)(x + i0);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = v[5] = v[6] = v[7] = 0.0f;
+    } else if constexpr (VPT == 2) {
+        const float2 a = *(const float2*)(x + i0);
+        v[0] = a.x; v[1] = a.y;
+#pragma unroll
+        for (int k = 2; k < 8; ++k) v[k] = 0.0f;
+    } else {
+        v[0] = x[i0];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) v[k] = 0.0f;
+    }
+}
+
+template <int H, int NT>
+__device__ __forceinline__ void x_digits(const float v[8], int8_t* planes, float* xs16, float* sum8) {
+    constexpr int VPT = H / NT;
+    const int i0 = threadIdx.x * VPT;
+    float amax = 0.0f, s8 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        amax = fmaxf(amax, fabsf(v[k]));
+        s8 += v[k];
+    }
+#pragma unroll
+    for (int off = 1; off < 16 / VPT; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+#pragma unroll
+    for (int off = 1; off < 8 / VPT; off <<= 1) s8 += __shfl_xor(s8, off, 64);
+    const int e = digit_exp(amax);
+    uint32_t p0 = 0, p1 = 0, p2 = 0, q0 = 0, q1 = 0, q2 = 0;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        int8_t d0, d1, d2;
+        split_digits(v[k], e, d0, d1, d2);
+        if (k < 4) {
+            p0 |= (uint32_t)(uint8_t)d0 << (8 * k); p1 |= (uint32_t)(uint8_t)d1 << (8 * k);
+            p2 |= (uint32_t)(uint8_t)d2 << (8 * k);
+        } else {
+            q0 |= (uint32_t)(uint8_t)d0 << (8 * (k - 4)); q1 |= (uint32_t)(uint8_t)d1 << (8 * (k - 4));
+            q2 |= (uint32_t)(uint8_t)d2 << (8 * (k - 4));
+        }
+    }
+    if constexpr (VPT == 8) {
+        *(uint2*)(planes + i0) = make_uint2(p0, q0);
+        *(uint2*)(planes + H + i0) = make_uint2(p1, q1);
+        *(uint2*)(planes + 2 * H + i0) = make_uint2(p2, q2);
+    } else if constexpr (VPT == 4) {
+        *(uint32_t*)(planes + i0) = p0;
+        *(uint32_t*)(planes + H + i0) = p1;
+        *(uint32_t*)(planes + 2 * H + i0) = p2;
+    } else if constexpr (VPT == 2) {
+        *(uint16_t*)(planes + i0) = (uint16_t)p0;
+        *(uint16_t*)(planes + H + i0) = (uint16_t)p1;
+        *(uint16_t*)(planes + 2 * H + i0) = (uint16_t)p2;
+    } else {
+        planes[i0] = (int8_t)p0;
+        planes[H + i0] = (int8_t)p1;
+        planes[2 * H + i0] = (int8_t)p2;
+    }
+    if ((i0 & 15) == 0) xs16[i0 >> 4] = ldexpf(1.0f, e - 14);
+    if ((i0 & 7) == 0) sum8[i0 >> 3] = s8;
+}
+
+// ---------------------------------------------------------------- kernel A
+
+// Geometry.  LPR = hidden / 32 lanes per row; an instruction covers RPI =
+// 64 / LPR rows; a wave loads NP such row groups (RW = NP * RPI rows) of both
+// the gate and the up matrix; a workgroup is WPG waves, RA = WPG * RW rows (a
+// multiple of 16: the activation digits are published in 16-row runs).
+template <int LPR>
+struct GeoA {
+    static constexpr int RPI = 64 / LPR;
+    static constexpr int NP = 1;
+    static constexpr int RW = NP * RPI;
+    static constexpr int WPG = RW >= 16 ? 4 : (16 / RW > 16 ? 16 : 16 / RW);
+    static constexpr int RA = WPG * RW;
+    static constexpr int NT = 64 * WPG;
+};
+
+template <int GT, int LPR>
+__global__ __launch_bounds__(GeoA<LPR>::NT) void k_fast_gate_up(DecodeParams p, FastLayout L) {
+    using G_ = GeoA<LPR>;
+    constexpr int N = LaneGeo<GT>::NRAW;
+    constexpr int BB = block_bytes(GT);
+    constexpr int H = 32 * LPR;
+    constexpr int RPI = G_::RPI, NP = G_::NP, RW = G_::RW, RA = G_::RA, NT = G_::NT, WPG = G_::WPG;
+    constexpr int64_t ROW_BYTES = (int64_t)(H / 256) * BB;
+    static_assert(RA % 16 == 0 && RA <= 64 && H % NT == 0, "kernel A geometry");
+    __shared__ __attribute__((aligned(16))) int8_t x_planes[3 * H];
+    __shared__ float x_xs16[H / 16];
+    __shared__ float x_sum8[H / 8];
+    __shared__ float s_act[RA];
+    __shared__ float s_gate[WPG];
+
+    const int t = blockIdx.z, s = blockIdx.y;
+    const bool shared = p.has_shared && s == p.top_k;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+
+    const uint8_t *Gm, *Um;
+    bool bad = false;
+    if (shared) {
+        Gm = p.sh_gate; Um = p.sh_up;
+    } else {
+        int e = p.ids[t * p.top_k + s];
+        if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }
+        Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
+    }
+
+    const int rr = lane / LPR, li = lane % LPR, blk = li >> 3, k = li & 7;
+    const int wrow0 = blockIdx.x * RA + wave * RW;
+
+    // 1. the token's values, then every weight load of this lane (issued in
+    // this order, so waiting for x does not wait for the weights)
+    const float* xt = p.x + (int64_t)t * H;
+    float xv8[8];
+    x_load<H, NT>(xt, xv8);
+    // the shared expert's sigmoid gate vector, same columns as xv8 (one workgroup per token)
+    const bool gate_wg = shared && blockIdx.x == 0 && p.sh_gate_inp != nullptr;
+    float gi8[8];
+    if (gate_wg) x_load<H, NT>(p.sh_gate_inp, gi8);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t rg[NP][N], ru[NP][N];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+        const int64_t off = (int64_t)(wrow0 + q * RPI + rr) * ROW_BYTES + blk * BB;
+        lane_load<GT>(Gm + off, k, rg[q]);
+        lane_load<GT>(Um + off, k, ru[q]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. token digits (the weight loads are in flight meanwhile)
+    x_digits<H, NT>(xv8, x_planes, x_xs16, x_sum8);
+    __syncthreads();
+    DigitsRef xv;
+    xv.planes = x_planes; xv.xs16 = x_xs16; xv.sum8 = x_sum8; xv.n = H;
+    LaneX X;
+    lane_x<GT>(xv, blk, k, X);
+
+    // 3. gate and up dot products, SwiGLU
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+        float g = lane_dot<GT>(rg[q], k, X);
+        float u = lane_dot<GT>(ru[q], k, X);
+        g = lane_group_sum<LPR>(g);
+        u = lane_group_sum<LPR>(u);
+        if (li == 0) s_act[wave * RW + q * RPI + rr] = bad ? 0.0f : silu_mul(g, u);
+    }
+
+    // shared slot: sigmoid(x . g_inp), the shared expert's gate, once per token
+    // (shared_expert.py:221-251); every thread holds VPT products
+    if (gate_wg) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = fmaf(xv8[i], gi8[i], acc);
+        acc = lane_group_sum<64>(acc);
+        if (lane == 0) s_gate[wave] = acc;
+    }
+    if (bad && threadIdx.x == 0 && blockIdx.x == 0) atomicOr(&p.flags[FLAG_BAD_ID], 1);
+    __syncthreads();
+    if (shared && blockIdx.x == 0 && threadIdx.x == 0) {
+        float d = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WPG; ++w) d += s_gate[w];
+        p.sh_scale[t] = gate_wg ? sigmoid_stable(d) : 1.0f;
+    }
+
+    // 4. publish the RA activations as digits
+    if (wave == 0) {
+        uint8_t* base = (uint8_t*)p.act + ((int64_t)t * p.S + s) * L.act_stride;
+        const int r0 = blockIdx.x * RA;
+        publish16(lane < RA ? s_act[lane] : 0.0f, lane, RA, (int8_t*)base + r0, L.inter,
+                  (float*)(base + L.xs_off) + r0 / 16, (float*)(base + L.sum_off) + r0 / 8);
+    }
+}
+
+// ---------------------------------------------------------------- kernel B
+
+// LPR = intermediate / 32 lanes per down row; RPI = 64 / LPR rows per
+// instruction; NPB row groups per wave, so RB = NPB * RPI output rows per
+// workgroup.  Wave s of the workgroup computes slot s.
+template <int LPR>
+struct GeoB {
+    static constexpr int RPI = 64 / LPR;
+    static constexpr int NPB = 2;
+    static constexpr int RB = NPB * RPI;
+};
+
+template <int DT, int LPR>
+__global__ __launch_bounds__(1024) void k_fast_down(DecodeParams p, FastLayout L) {
+    constexpr int N = LaneGeo<DT>::NRAW;
+    constexpr int BB = block_bytes(DT);
+    constexpr int I = 32 * LPR;
+    constexpr int RPI = GeoB<LPR>::RPI, NPB = GeoB<LPR>::NPB, RB = GeoB<LPR>::RB;
+    constexpr int64_t ROW_BYTES = (int64_t)(I / 256) * BB;
+    __shared__ float s_y[FAST_MAX_SLOTS][RB];
+    __shared__ float s_w[FAST_MAX_SLOTS];
+
+    const int t = blockIdx.y;
+    const int lane = threadIdx.x & 63, s = uniform(threadIdx.x >> 6);   // wave = slot
+    const int rr = lane / LPR, li = lane % LPR, blk = li >> 3, k = li & 7;
+    const int r0 = blockIdx.x * RB;
+    const bool shared = p.has_shared && s == p.top_k;
+
+    const uint8_t* D;
+    bool bad = false;
+    float w = 0.0f;
+    if (shared) {
+        D = p.sh_down;
+    } else {
+        int e = p.ids[t * p.top_k + s];
+        if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }
+        D = p.down + (int64_t)e * p.down_eb;
+        w = bad ? 0.0f : p.weights[t * p.top_k + s];
+    }
+
+    // activation digits first (small, in L2), then every weight load
+    LaneX X;
+    lane_x<DT>(act_digits(L, (uint8_t*)p.act, t, s, p.S), blk, k, X);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t raw[NPB][N];
+#pragma unroll
+    for (int q = 0; q < NPB; ++q) lane_load<DT>(D + (int64_t)(r0 + q * RPI + rr) * ROW_BYTES + blk * BB, k, raw[q]);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int q = 0; q < NPB; ++q) {
+        float v = lane_dot<DT>(raw[q], k, X);
+        v = lane_group_sum<LPR>(v);
+        if (li == 0) s_y[s][q * RPI + rr] = bad ? 0.0f : v;
+    }
+    if (lane == 0) s_w[s] = shared ? p.sh_scale[t] : w;
+    __syncthreads();
+
+    // combine in top-k order, then the shared expert (moe_layer.py:70-106)
+    if (threadIdx.x < RB) {
+        const int r = threadIdx.x;
+        float acc = 0.0f;
+        for (int j = 0; j < p.top_k; ++j) acc = __fadd_rn(acc, __fmul_rn(s_w[j], s_y[j][r]));
+        if (p.has_shared) acc = __fadd_rn(acc, __fmul_rn(s_w[p.top_k], s_y[p.top_k][r]));
+        p.y[(int64_t)t * p.hidden + r0 + r] = acc;
+        if (!isfinite(acc)) atomicOr(&p.flags[FLAG_NONFINITE], 1);
+    }
+}
+
+// ------------------------------------------------------------------ launch
+
+static bool fast_type(int t) { return t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+static bool fast_dim(int n) { return n == 256 || n == 512 || n == 1024 || n == 2048; }
+
+bool fast_supported(const DecodeParams& p) {
+    if (p.fp16) return false;
+    if (!fast_dim(p.hidden) || p.S > FAST_MAX_SLOTS || p.S < 1) return false;
+    int gt = -1, dt = -1, I = -1;
+    if (p.top_k > 0) {
+        if (!(fast_type(p.gate_type) && p.up_type == p.gate_type && fast_type(p.down_type))) return false;
+        gt = p.gate_type; dt = p.down_type; I = p.inter;
+    }
+    if (p.has_shared) {
+        if (!(fast_type(p.sh_gate_type) && p.sh_up_type == p.sh_gate_type && fast_type(p.sh_down_type))) return false;
+        if (gt >= 0 && (p.sh_gate_type != gt || p.sh_down_type != dt || p.sh_inter != I)) return false;
+    }
+    const int inter = p.top_k > 0 ? p.inter : p.sh_inter;
+    return fast_dim(inter);
+}
+
+FastLayout fast_layout(int inter) {
+    FastLayout L;
+    L.inter = inter;
+    L.xs_off = 3 * inter;
+    L.sum_off = L.xs_off + (inter / 16) * 4;
+    L.act_stride = align256(L.sum_off + (inter / 8) * 4);
+    return L;
+}
+
+template <int GT, int LPR>
+static void launch_a(const DecodeParams& p, const FastLayout& L, hipStream_t stream) {
+    dim3 grid(p.inter / GeoA<LPR>::RA, p.S, p.n_tokens);
+    hipLaunchKernelGGL((k_fast_gate_up<GT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, p, L);
+}
+
+template <int GT>
+static void launch_a_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream) {
+    switch (p.hidden) {
+        case 256: launch_a<GT, 8>(p, L, stream); break;
+        case 512: launch_a<GT, 16>(p, L, stream); break;
+        case 1024: launch_a<GT, 32>(p, L, stream); break;
+        default: launch_a<GT, 64>(p, L, stream); break;
+    }
+}
+
+template <int DT, int LPR>
+static void launch_b(const DecodeParams& p, const FastLayout& L, hipStream_t stream) {
+    dim3 grid(p.hidden / GeoB<LPR>::RB, p.n_tokens);
+    hipLaunchKernelGGL((k_fast_down<DT, LPR>), grid, dim3(64 * p.S), 0, stream, p, L);
+}
+
+template <int DT>
+static void launch_b_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream) {
+    switch (p.inter) {
+        case 256: launch_b<DT, 8>(p, L, stream); break;
+        case 512: launch_b<DT, 16>(p, L, stream); break;
+        case 1024: launch_b<DT, 32>(p, L, stream); break;
+        default: launch_b<DT, 64>(p, L, stream); break;
+    }
+}
+
+hipError_t launch_decode_fast(const DecodeParams& p0, hipStream_t stream) {
+    DecodeParams p = p0;
+    if (p.top_k == 0) {   // shared expert only: present it as the routed types
+        p.gate_type = p.sh_gate_type; p.up_type = p.sh_up_type; p.down_type = p.sh_down_type;
+        p.inter = p.sh_inter;
+    }
+    const FastLayout L = fast_layout(p.inter);
+    switch (p.gate_type) {
+        case T_Q4_K: launch_a_t<T_Q4_K>(p, L, stream); break;
+        case T_Q5_K: launch_a_t<T_Q5_K>(p, L, stream); break;
+        case T_Q6_K: launch_a_t<T_Q6_K>(p, L, stream); break;
+        default: launch_a_t<T_Q3_K>(p, L, stream); break;
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    switch (p.down_type) {
+        case T_Q4_K: launch_b_t<T_Q4_K>(p, L, stream); break;
+        case T_Q5_K: launch_b_t<T_Q5_K>(p, L, stream); break;
+        case T_Q6_K: launch_b_t<T_Q6_K>(p, L, stream); break;
+        default: launch_b_t<T_Q3_K>(p, L, stream); break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mqh

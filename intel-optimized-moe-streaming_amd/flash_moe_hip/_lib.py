@@ -36,7 +36,6 @@ STATUS_TEXT = {
     -4: "non-finite output",
     -5: "HIP runtime failure",
     -6: "workspace too small",
-    -8: "kernel wait timed out",
     -9: "expert id out of range",
 }
 

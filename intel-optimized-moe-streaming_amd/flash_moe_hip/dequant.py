@@ -36,11 +36,14 @@ def _as_bytes(raw) -> np.ndarray:
 
 
 def _host_dequant(raw, ggml_type: int, n_elements: int, out: np.ndarray, want_f16: int) -> np.ndarray:
+    lib = _lib.load()
+    if not lib.dequant_k_supported(int(ggml_type)):
+        _lib.check(-1, f"dequant_k(type {ggml_type})")
     src = _as_bytes(raw)
     bs, pb = block_info(ggml_type)
     if n_elements % bs or src.nbytes < n_elements // bs * pb:
         raise ValueError(f"{src.nbytes} bytes cannot hold {n_elements} {name_of(ggml_type)} values")
-    rc = _lib.load().dequant_k(int(ggml_type), src.ctypes.data, out.ctypes.data, int(n_elements), want_f16)
+    rc = lib.dequant_k(int(ggml_type), src.ctypes.data, out.ctypes.data, int(n_elements), want_f16)
     _lib.check(rc, "dequant_k")
     return out
 

@@ -1,10 +1,11 @@
-"""The fused decode's integer-digit dot products, built for the host, against the oracle (CPU only).
+"""The decode fast path's integer-digit dot products, built for the host, against the oracle (CPU only).
 
-tests/cpu/chunk_check.cpp compiles kquant_dot.h -- the same __host__
-__device__ code the gfx950 kernel runs, with v_dot4_i32_i8 emulated -- and
-computes full row dot products chunk by chunk.  They must match the FP64 dot
-product of the oracle-dequantized row to ~1e-6 of sum|w*x| (the digit split
-keeps 20 bits of each 32-column group's maximum).
+tests/cpu/lane_check.cpp compiles kquant_lane.h -- the same __host__
+__device__ code the gfx950 kernels run, with v_dot4_i32_i8 emulated -- and
+computes full row dot products lane by lane (8 lanes of 32 weights per
+super-block).  They must match the FP64 dot product of the oracle-dequantized
+row to ~1e-6 of sum|w*x| (the digit split keeps 20 bits of each 16-column
+run's maximum).
 """
 from __future__ import annotations
 
@@ -16,13 +17,13 @@ import pytest
 
 from conftest import PKG_DIR, ROOT
 
-SRC = ROOT / "tests" / "cpu" / "chunk_check.cpp"
-OUT = ROOT / "tests" / "cpu" / "_build" / "libchunkcheck.so"
+SRC = ROOT / "tests" / "cpu" / "lane_check.cpp"
+OUT = ROOT / "tests" / "cpu" / "_build" / "liblanecheck.so"
 
 
 @pytest.fixture(scope="module")
 def chk():
-    deps = [SRC, PKG_DIR / "csrc" / "kquant_dot.h", PKG_DIR / "csrc" / "kquant_device.h"]
+    deps = [SRC, PKG_DIR / "csrc" / "kquant_lane.h", PKG_DIR / "csrc" / "kquant_device.h"]
     if not OUT.exists() or OUT.stat().st_mtime < max(d.stat().st_mtime for d in deps):
         OUT.parent.mkdir(exist_ok=True)
         subprocess.run(["hipcc", "-O2", "-std=c++17", "-fPIC", "-shared", "-x", "hip", "--offload-arch=gfx950",
@@ -31,6 +32,7 @@ def chk():
     L.mqh_cpu_row_dot.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p]
     L.mqh_cpu_row_dot.restype = C.c_float
     L.mqh_cpu_digit_roundtrip.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
+    L.mqh_cpu_lane_cover.argtypes = [C.c_int, C.c_void_p]
     return L
 
 
@@ -59,8 +61,8 @@ def test_row_dot_matches_oracle(chk, oracle_mod, t, kind):
             x = activations(rng, ncols, kind)
             got = chk.mqh_cpu_row_dot(t, rows[r].ctypes.data, ncols, x.ctypes.data)
             want = float(w[r] @ x.astype(np.float64))
-            # digit error <= 2^-20 * (group max) per value, plus FP32 rounding of the sums
-            gmax = np.abs(x.reshape(-1, 32)).max(axis=1).repeat(32).astype(np.float64)
+            # digit error <= 2^-20 * (run max) per value, plus FP32 rounding of the sums
+            gmax = np.abs(x.reshape(-1, 16)).max(axis=1).repeat(16).astype(np.float64)
             bound = 2.0 ** -20 * float(np.abs(w[r]) @ gmax) + 1e-6 * float(np.abs(w[r] * x).sum()) + 1e-30
             assert abs(got - want) <= bound, (ncols, r, got, want, bound)
 
@@ -71,5 +73,12 @@ def test_digit_roundtrip_bound(chk):
                         np.zeros(64), np.full(32, 1e-30), np.full(32, -3e30)]).astype(np.float32)
     out = np.empty_like(x)
     chk.mqh_cpu_digit_roundtrip(x.ctypes.data, x.size, out.ctypes.data)
-    gmax = np.abs(x.reshape(-1, 32)).max(axis=1).repeat(32)
+    gmax = np.abs(x.reshape(-1, 16)).max(axis=1).repeat(16)
     assert np.all(np.abs(out.astype(np.float64) - x) <= 2.0 ** -20 * gmax + 1e-45)
+
+
+@pytest.mark.parametrize("t", [11, 12, 13, 14])
+def test_lanes_cover_each_column_once(chk, t):
+    count = np.zeros(256, np.int32)
+    chk.mqh_cpu_lane_cover(t, count.ctypes.data)
+    assert np.all(count == 1)

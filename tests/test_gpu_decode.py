@@ -71,9 +71,9 @@ def run(layer, X, ids, ws, fp16=0, use_shared=True):
     return out, runner.status()
 
 
-@pytest.fixture(params=[0, 1], ids=["fused", "generic"])
+@pytest.fixture(params=[0, 1], ids=["fast", "generic"])
 def path(request, hip):
-    """Run the test through the single-launch fused kernel and the generic kernels."""
+    """Run the test through the integer-digit fast kernels and the generic kernels."""
     old = hip.mqh_set_decode_path(request.param)
     yield request.param
     hip.mqh_set_decode_path(old)
@@ -171,13 +171,13 @@ def test_fp16_graph_routed_experts(hip, oracle_mod):
 
 
 @pytest.mark.parametrize("types", [(12, 14), (11, 11), (13, 12), (14, 14), (12, 13), (11, 14)])
-def test_fused_type_pairs_against_generic(hip, oracle_mod, types):
-    """Every (gate/up, down) type pair of the fused kernel, 3 tokens, H=I=256 and H=2048/I=512,
+def test_fast_type_pairs(hip, oracle_mod, types):
+    """Every (gate/up, down) type pair of the fast kernels, 3 tokens, H=I=256 and H=2048/I=512,
     against the oracle."""
     gu, dn = types
     t = {"gate": gu, "up": gu, "down": dn}
     for H, I in ((256, 256), (2048, 512), (512, 1024)):
-        print(f"fused types={types} H={H} I={I}", flush=True)
+        print(f"fast types={types} H={H} I={I}", flush=True)
         layer, host, shared = make_layer(29 + gu + dn, 6, H, I, t, shared_types=t)
         rng = np.random.default_rng(H + I)
         X = rng.standard_normal((3, H)).astype(np.float32)
@@ -195,8 +195,8 @@ def test_fused_type_pairs_against_generic(hip, oracle_mod, types):
             assert err <= TOL, (types, H, I, tok, err)
 
 
-def test_fused_repeated_launches_reset_counters(decode_layer, oracle_mod, hip):
-    """Back-to-back launches on one workspace: the kernel's counters reset themselves."""
+def test_fast_repeated_launches_share_workspace(decode_layer, oracle_mod, hip):
+    """Back-to-back launches on one workspace, read once at the end: each result is its own."""
     import torch
 
     from flash_moe_hip.moe_gpu import MoeRunner

@@ -4,14 +4,17 @@ Headline workload (one "step" = one token through one MoE layer):
   hidden 2048; 256 experts x intermediate 512; top-8 routing plus one shared
   expert (intermediate 512, sigmoid-gated); gate/up Q4_K, down Q6_K; router
   FP32 [2048 x 256] ~ N(0, 0.02), top-8 of the scores, softmax renormalised.
-  One fused GPU call covers the 9 experts and the weighted combine.  40
+  One GPU call (two kernels) covers the 9 experts and the weighted combine.  40
   independently seeded layers are resident in HBM (~21 GB) and the steps
   rotate through them, so the 256 MB Infinity Cache cannot hold the working set.
 
 value = quantized weight bytes the step must read (9 x 2,039,808 B =
 18,358,272 B) / time per step, in GB/s.  Inputs (weights, activations,
 routing) are resident in HBM before timing starts; the 40-layer sweep is
-captured once as a HIP graph and replayed.
+captured once as a HIP graph and replayed, so the time per step includes the
+gap between graph nodes.  roofline: the dominant kernel's algorithmic bytes /
+its average duration, from HIP events the runtime records at each kernel's
+start and end during a second, eager pass over the same layers.
 
 cpu_baseline: the CPU oracle (a restatement of the reference's AVX2 kernel)
 running the same layer as 9 moe_quant_expert calls on 4 worker threads -- the
@@ -78,6 +81,23 @@ def step_bytes(layer) -> int:
     return (K + 1) * layer.bytes_per_expert()
 
 
+def roofline(kern: dict, layer) -> dict:
+    """The dominant kernel (the larger average duration) against HBM peak.
+    Algorithmic bytes per launch: the quantized weight bytes it must read --
+    kernel A the gate and up slices of the 9 experts, kernel B their down
+    slices -- plus activations in and out (a few KB)."""
+    a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
+    b_bytes = (K + 1) * layer.expert_bytes("down")
+    if kern["a_us"] >= kern["b_us"]:
+        name, nbytes, us = "k_fast_gate_up", a_bytes, kern["a_us"]
+    else:
+        name, nbytes, us = "k_fast_down", b_bytes, kern["b_us"]
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+            "algorithmic_bytes": nbytes, "kernel_us": round(us, 3)}
+
+
 def parity_check(layer, x, ids, ws, y_gpu) -> float:
     import oracle
 
@@ -129,6 +149,57 @@ def cpu_baseline(layers, xs, ids, ws, seconds: float, workers: int = 4):
                   f"{dt:.1f} s on {workers} threads; host has {os.cpu_count()} logical CPUs",
         "us_per_layer": round(per_step * 1e6, 1),
     }
+
+
+def _hip_runtime():
+    """The process's HIP runtime (the one torch and the library already share)."""
+    import ctypes as C
+
+    rt = C.CDLL("libamdhip64.so.7")
+    rt.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+    rt.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+    rt.hipEventDestroy.argtypes = [C.c_void_p]
+    return rt
+
+
+def kernel_times(runner, layers, X, IDS, WS, Y, reps: int) -> dict:
+    """Average duration of each decode kernel: an eager pass of reps x layers
+    steps, every kernel launched with start/stop HIP events."""
+    import ctypes as C
+
+    import torch
+
+    from flash_moe_hip import _lib
+
+    lib, rt = _lib.load(), _hip_runtime()
+    n = reps * len(layers)
+    ev = []
+    for _ in range(4 * n):
+        h = C.c_void_p()
+        if rt.hipEventCreate(C.byref(h)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        ev.append(h)
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    for i in range(n):
+        l = i % len(layers)
+        _lib.check(lib.mqh_profile_next_decode(ev[4 * i], ev[4 * i + 1], ev[4 * i + 2], ev[4 * i + 3]),
+                   "mqh_profile_next_decode")
+        runner.decode(layers[l], X[l:l + 1], IDS[l:l + 1], WS[l:l + 1], y=Y[l:l + 1], stream=stream)
+    torch.cuda.synchronize()
+
+    def ms(a, b):
+        v = C.c_float()
+        if rt.hipEventElapsedTime(C.byref(v), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return v.value
+
+    a = [ms(ev[4 * i], ev[4 * i + 1]) * 1e3 for i in range(n)]
+    b = [ms(ev[4 * i + 2], ev[4 * i + 3]) * 1e3 for i in range(n)]
+    for h in ev:
+        rt.hipEventDestroy(h)
+    return {"a_us": float(np.mean(a)), "b_us": float(np.mean(b)), "launches": n,
+            "a_us_median": float(np.median(a)), "b_us_median": float(np.median(b))}
 
 
 def main() -> int:
@@ -226,6 +297,12 @@ def main() -> int:
     y_graph = Y[0].cpu().numpy()
     err_graph = parity_check(layers[0], xs[0], ids[0], ws[0], y_graph)
 
+    # per-kernel durations: every step of an eager pass over the same layers,
+    # each kernel bracketed by HIP events recorded by the runtime at its
+    # start and end (mqh_profile_next_decode), on the stream it runs on
+    kern = kernel_times(runner, layers, X, IDS, WS, Y, reps=max(1, min(reps, 10)))
+    log(f"kernel A (gate/up) {kern['a_us']:.3f} us, kernel B (down+combine) {kern['b_us']:.3f} us per launch")
+
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -248,15 +325,9 @@ def main() -> int:
         },
         "us_per_layer": round(ms_step * 1e3, 3),
         "parity_max_rel_err": float(f"{max(err, err_graph):.3e}"),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(gbs, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "k_moe_fused (single launch per token-layer)",
-        },
+        "kernels_us": {"k_fast_gate_up": round(kern["a_us"], 3), "k_fast_down": round(kern["b_us"], 3),
+                       "launches_each": kern["launches"]},
+        "roofline": roofline(kern, layers[0]),
     }
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle, 4 threads)")

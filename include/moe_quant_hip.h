@@ -112,6 +112,13 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
  * previous setting, or -1 for another value. */
 int mqh_set_decode_path(int path);
 
+/* Profiling: record HIP events (hipEvent_t, any may be NULL) at the start and
+ * end of the two kernels of the calling thread's next mqh_moe_decode or
+ * moe_quant_expert -- A: gate/up and SwiGLU, B: down projection and combine.
+ * One-shot; the launch itself is unchanged.  No counterpart in the reference
+ * (its timers are host wall clocks, bench_phases.py:45-56). */
+int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_stop);
+
 /* Zero a workspace (flags and counters) on `stream`. */
 int mqh_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
 

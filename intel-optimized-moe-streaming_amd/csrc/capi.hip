@@ -23,9 +23,14 @@ bool supported(int t) { return block_size(t) != 0; }
 // generic kernels
 int g_decode_path = 0;
 
+// events armed by mqh_profile_next_decode for this thread's next decode
+thread_local KernelEvents t_events;
+
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s) {
-    if (g_decode_path == 0 && fast_supported(p)) return launch_decode_fast(p, s);
-    return launch_decode_generic(p, s);
+    const KernelEvents ev = t_events;
+    t_events = KernelEvents();
+    if (g_decode_path == 0 && fast_supported(p)) return launch_decode_fast(p, s, ev);
+    return launch_decode_generic(p, s, ev);
 }
 
 // Expected bytes of a [rows x cols] matrix, or a negative status.
@@ -288,6 +293,14 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
     p.S = top_k + (has_shared ? 1 : 0);
     p.Imax = std::max(intermediate, has_shared ? sh_intermediate : 0);
     return launch_decode(p, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
+}
+
+int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_stop) {
+    t_events.a_start = (hipEvent_t)a_start;
+    t_events.a_stop = (hipEvent_t)a_stop;
+    t_events.b_start = (hipEvent_t)b_start;
+    t_events.b_stop = (hipEvent_t)b_stop;
+    return ST_OK;
 }
 
 int mqh_set_decode_path(int path) {

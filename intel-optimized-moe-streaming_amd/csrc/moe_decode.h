@@ -73,10 +73,18 @@ struct FastLayout {
     int64_t xs_off, sum_off, act_stride;
 };
 
-hipError_t launch_decode_generic(const DecodeParams& p, hipStream_t stream);
+// Optional HIP events recorded at the start and end of the two decode kernels
+// (A: gate/up, B: down + combine), for profiling; null members are ignored.
+struct KernelEvents {
+    hipEvent_t a_start = nullptr, a_stop = nullptr, b_start = nullptr, b_stop = nullptr;
+    bool armed_a() const { return a_start || a_stop; }
+    bool armed_b() const { return b_start || b_stop; }
+};
+
+hipError_t launch_decode_generic(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev);
 bool fast_supported(const DecodeParams& p);
 FastLayout fast_layout(int inter);
-hipError_t launch_decode_fast(const DecodeParams& p, hipStream_t stream);
+hipError_t launch_decode_fast(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev);
 hipError_t launch_dequant(int type, const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream);
 
 }  // namespace mqh

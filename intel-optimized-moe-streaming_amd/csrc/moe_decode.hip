@@ -20,6 +20,8 @@
 // routed experts (x, weights, g, u, sigmoid, silu, act and y rounded to FP16
 // at the points of moe_quant_dot.cpp:192-209); the shared expert always runs
 // the FP32 graph, as the reference's NumPy shared expert does.
+#include <hip/hip_ext.h>
+
 #include "kquant_device.h"
 #include "moe_decode.h"
 
@@ -238,13 +240,25 @@ static int nk_for(int cols) {
     return (P + L - 1) / L;
 }
 
-hipError_t launch_decode_generic(const DecodeParams& p, hipStream_t stream) {
+hipError_t launch_decode_generic(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     const int nk_a = nk_for(p.hidden);
     const int nk_b = std::max(nk_for(p.inter), p.has_shared ? nk_for(p.sh_inter) : 1);
     dim3 ga((p.Imax + ROWS_A - 1) / ROWS_A, p.S, p.n_tokens);
     dim3 gb((p.hidden + ROWS_B - 1) / ROWS_B, p.n_tokens);
-#define MQH_LAUNCH_A(NK) hipLaunchKernelGGL((k_gate_up<NK>), ga, dim3(256), 0, stream, p)
-#define MQH_LAUNCH_B(NK) hipLaunchKernelGGL((k_down_combine<NK>), gb, dim3(256), 0, stream, p)
+#define MQH_LAUNCH_A(NK)                                                                                     \
+    do {                                                                                                     \
+        if (ev.armed_a())                                                                                    \
+            hipExtLaunchKernelGGL((k_gate_up<NK>), ga, dim3(256), 0, stream, ev.a_start, ev.a_stop, 0, p);   \
+        else                                                                                                 \
+            hipLaunchKernelGGL((k_gate_up<NK>), ga, dim3(256), 0, stream, p);                                \
+    } while (0)
+#define MQH_LAUNCH_B(NK)                                                                                     \
+    do {                                                                                                     \
+        if (ev.armed_b())                                                                                    \
+            hipExtLaunchKernelGGL((k_down_combine<NK>), gb, dim3(256), 0, stream, ev.b_start, ev.b_stop, 0, p); \
+        else                                                                                                 \
+            hipLaunchKernelGGL((k_down_combine<NK>), gb, dim3(256), 0, stream, p);                           \
+    } while (0)
     if (nk_a == 1) MQH_LAUNCH_A(1);
     else if (nk_a == 2) MQH_LAUNCH_A(2);
     else if (nk_a <= 4) MQH_LAUNCH_A(4);

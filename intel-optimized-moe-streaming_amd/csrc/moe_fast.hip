@@ -24,6 +24,8 @@
 // Supported (checked by fast_supported): FP32 graph; types Q3_K/Q4_K/Q5_K/Q6_K
 // with gate type == up type; hidden and intermediate in {256, 512, 1024, 2048};
 // at most 16 slots; a shared expert with the routed types and intermediate size.
+#include <hip/hip_ext.h>
+
 #include "kquant_lane.h"
 #include "moe_decode.h"
 
@@ -387,38 +389,45 @@ FastLayout fast_layout(int inter) {
 }
 
 template <int GT, int LPR>
-static void launch_a(const DecodeParams& p, const FastLayout& L, hipStream_t stream) {
+static void launch_a(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
     dim3 grid(p.inter / GeoA<LPR>::RA, p.S, p.n_tokens);
-    hipLaunchKernelGGL((k_fast_gate_up<GT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, p, L);
+    if (ev.armed_a())
+        hipExtLaunchKernelGGL((k_fast_gate_up<GT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, ev.a_start, ev.a_stop, 0,
+                              p, L);
+    else
+        hipLaunchKernelGGL((k_fast_gate_up<GT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, p, L);
 }
 
 template <int GT>
-static void launch_a_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream) {
+static void launch_a_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
     switch (p.hidden) {
-        case 256: launch_a<GT, 8>(p, L, stream); break;
-        case 512: launch_a<GT, 16>(p, L, stream); break;
-        case 1024: launch_a<GT, 32>(p, L, stream); break;
-        default: launch_a<GT, 64>(p, L, stream); break;
+        case 256: launch_a<GT, 8>(p, L, stream, ev); break;
+        case 512: launch_a<GT, 16>(p, L, stream, ev); break;
+        case 1024: launch_a<GT, 32>(p, L, stream, ev); break;
+        default: launch_a<GT, 64>(p, L, stream, ev); break;
     }
 }
 
 template <int DT, int LPR>
-static void launch_b(const DecodeParams& p, const FastLayout& L, hipStream_t stream) {
+static void launch_b(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
     dim3 grid(p.hidden / GeoB<LPR>::RB, p.n_tokens);
-    hipLaunchKernelGGL((k_fast_down<DT, LPR>), grid, dim3(64 * p.S), 0, stream, p, L);
+    if (ev.armed_b())
+        hipExtLaunchKernelGGL((k_fast_down<DT, LPR>), grid, dim3(64 * p.S), 0, stream, ev.b_start, ev.b_stop, 0, p, L);
+    else
+        hipLaunchKernelGGL((k_fast_down<DT, LPR>), grid, dim3(64 * p.S), 0, stream, p, L);
 }
 
 template <int DT>
-static void launch_b_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream) {
+static void launch_b_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
     switch (p.inter) {
-        case 256: launch_b<DT, 8>(p, L, stream); break;
-        case 512: launch_b<DT, 16>(p, L, stream); break;
-        case 1024: launch_b<DT, 32>(p, L, stream); break;
-        default: launch_b<DT, 64>(p, L, stream); break;
+        case 256: launch_b<DT, 8>(p, L, stream, ev); break;
+        case 512: launch_b<DT, 16>(p, L, stream, ev); break;
+        case 1024: launch_b<DT, 32>(p, L, stream, ev); break;
+        default: launch_b<DT, 64>(p, L, stream, ev); break;
     }
 }
 
-hipError_t launch_decode_fast(const DecodeParams& p0, hipStream_t stream) {
+hipError_t launch_decode_fast(const DecodeParams& p0, hipStream_t stream, const KernelEvents& ev) {
     DecodeParams p = p0;
     if (p.top_k == 0) {   // shared expert only: present it as the routed types
         p.gate_type = p.sh_gate_type; p.up_type = p.sh_up_type; p.down_type = p.sh_down_type;
@@ -426,18 +435,18 @@ hipError_t launch_decode_fast(const DecodeParams& p0, hipStream_t stream) {
     }
     const FastLayout L = fast_layout(p.inter);
     switch (p.gate_type) {
-        case T_Q4_K: launch_a_t<T_Q4_K>(p, L, stream); break;
-        case T_Q5_K: launch_a_t<T_Q5_K>(p, L, stream); break;
-        case T_Q6_K: launch_a_t<T_Q6_K>(p, L, stream); break;
-        default: launch_a_t<T_Q3_K>(p, L, stream); break;
+        case T_Q4_K: launch_a_t<T_Q4_K>(p, L, stream, ev); break;
+        case T_Q5_K: launch_a_t<T_Q5_K>(p, L, stream, ev); break;
+        case T_Q6_K: launch_a_t<T_Q6_K>(p, L, stream, ev); break;
+        default: launch_a_t<T_Q3_K>(p, L, stream, ev); break;
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     switch (p.down_type) {
-        case T_Q4_K: launch_b_t<T_Q4_K>(p, L, stream); break;
-        case T_Q5_K: launch_b_t<T_Q5_K>(p, L, stream); break;
-        case T_Q6_K: launch_b_t<T_Q6_K>(p, L, stream); break;
-        default: launch_b_t<T_Q3_K>(p, L, stream); break;
+        case T_Q4_K: launch_b_t<T_Q4_K>(p, L, stream, ev); break;
+        case T_Q5_K: launch_b_t<T_Q5_K>(p, L, stream, ev); break;
+        case T_Q6_K: launch_b_t<T_Q6_K>(p, L, stream, ev); break;
+        default: launch_b_t<T_Q3_K>(p, L, stream, ev); break;
     }
     return hipGetLastError();
 }

@@ -24,6 +24,7 @@ EXPORTS = (
     "mqh_moe_workspace_bytes",
     "mqh_moe_decode",
     "mqh_set_decode_path",
+    "mqh_profile_next_decode",
     "mqh_workspace_init",
     "mqh_status",
 )
@@ -71,6 +72,8 @@ def _declare(lib: C.CDLL) -> C.CDLL:
         _P, _I, _P, _I64, _P,                    # y, fp16_graph, workspace, ws bytes, stream
     ]
     lib.mqh_moe_decode.restype = _I
+    lib.mqh_profile_next_decode.argtypes = [_P, _P, _P, _P]
+    lib.mqh_profile_next_decode.restype = _I
     lib.mqh_set_decode_path.argtypes = [_I]
     lib.mqh_set_decode_path.restype = _I
     lib.mqh_workspace_init.argtypes = [_P, _I64, _P]

@@ -7,19 +7,18 @@
 //   act[t,s] = silu(W_gate x_t) * (W_up x_t)
 //   y[t]     = sum_s w[t,s] * W_down act[t,s]   (+ sigmoid(x_t . g_inp) * shared)
 //
-// Kernel A  grid (I / RA, S, T), 256 threads.  A workgroup computes RA
-//           consecutive intermediate rows of one (token, slot): the token's
-//           activation digits go to LDS, each lane keeps the digits of its 32
-//           columns in registers for all its rows, and the gate and up rows'
-//           quantized bytes are all requested before any arithmetic.  The RA
-//           results are published as digits (16-row runs) to the workspace.
+// Kernel A  grid (I / 16, S, T).  A workgroup computes 16 consecutive
+//           intermediate rows of one (token, slot): the token's activation digits
+//           go to LDS, each lane keeps the digits of its 64 columns in registers,
+//           and the gate and up rows' quantized bytes are all requested before any
+//           arithmetic.  The 16 results are published as digits to the workspace.
 // Kernel B  grid (H / RB, T), 64*S threads: wave s computes the down rows of
-//           slot s for RB output rows, then the workgroup combines the slots
-//           in top-k order (+ shared) from LDS.
+//           slot s for RB output rows, then the workgroup combines the slots in
+//           top-k order (+ shared) from LDS.
 //
-// Lanes follow kquant_lane.h: lane k of a super-block owns 32 of its weights,
-// so a row of C columns is C/32 consecutive lanes and an instruction covers
-// 64/(C/32) rows.  Every weight byte is read once per (token, slot).
+// Lanes follow kquant_lane.h: lane k of a super-block owns 64 of its weights,
+// so a row of C columns is C/64 consecutive lanes and an instruction covers
+// 64/(C/64) rows.  Every weight byte is read once per (token, slot).
 //
 // Supported (checked by fast_supported): FP32 graph; types Q3_K/Q4_K/Q5_K/Q6_K
 // with gate type == up type; hidden and intermediate in {256, 512, 1024, 2048};
@@ -32,8 +31,14 @@
 namespace mqh {
 
 constexpr int FAST_MAX_SLOTS = 16;
+constexpr int RUN = 16;          // activation digit run (columns sharing one scale)
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return (g * (1.0f / (1.0f + expf(-g)))) * u; }
+// silu(g) * u with the hardware exp2 and reciprocal (a few ulp; the FP32 graph
+// of moe_quant_dot.cpp:200-206 with std::exp and a division)
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);   // exp(-g)
+    return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
+}
 
 __device__ __forceinline__ float sigmoid_stable(float v) {
     if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
@@ -41,12 +46,12 @@ __device__ __forceinline__ float sigmoid_stable(float v) {
     return e / (1.0f + e);
 }
 
-// Sum over aligned groups of W lanes (W = 8, 16, 32 or 64); every lane of a
-// group receives the group's sum, in a fixed butterfly order (deterministic).
+// Sum over aligned groups of W lanes (W = 4 .. 64); every lane of a group
+// receives the group's sum, in a fixed butterfly order (deterministic).
 // Partners within 32 lanes come from ds_swizzle (bit mode: lane ^ m), across
 // the halves from ds_bpermute.  DPP row operations would keep this in the VALU,
-// but hipcc's DPP combining of this reduction gave intermittently wrong sums on
-// gfx950, so the LDS crossbar forms are used.
+// but hipcc's DPP-combined form of this reduction gave intermittently wrong
+// sums on gfx950, so the LDS crossbar forms are used.
 template <int M>
 __device__ __forceinline__ float swz_xor(float v) {
     static_assert(M > 0 && M < 32, "swizzle xor mask");
@@ -55,10 +60,10 @@ __device__ __forceinline__ float swz_xor(float v) {
 
 template <int W>
 __device__ __forceinline__ float lane_group_sum(float v) {
-    static_assert(W == 8 || W == 16 || W == 32 || W == 64, "group width");
+    static_assert(W >= 4 && W <= 64 && (W & (W - 1)) == 0, "group width");
     v += swz_xor<1>(v);
     v += swz_xor<2>(v);
-    v += swz_xor<4>(v);
+    if constexpr (W > 4) v += swz_xor<4>(v);
     if constexpr (W > 8) v += swz_xor<8>(v);
     if constexpr (W > 16) v += swz_xor<16>(v);
     if constexpr (W > 32) v += __shfl_xor(v, 32, 64);
@@ -69,127 +74,80 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // Workspace view of the digits of act[t, s] (I values).
-__device__ __forceinline__ DigitsRef act_digits(const FastLayout& L, uint8_t* base, int t, int s, int S) {
-    uint8_t* p = base + ((int64_t)t * S + s) * L.act_stride;
+__device__ __forceinline__ DigitsRef act_digits(const FastLayout& L, const uint8_t* base, int t, int s, int S) {
+    const uint8_t* p = base + ((int64_t)t * S + s) * L.act_stride;
     DigitsRef v;
     v.planes = (const int8_t*)p;
     v.xs16 = (const float*)(p + L.xs_off);
-    v.sum8 = (const float*)(p + L.sum_off);
+    v.sum16 = (const float*)(p + L.sum_off);
     v.n = L.inter;
     return v;
 }
 
-// Digits of n values, one value per lane i of consecutive lanes (n a multiple
-// of 16; lanes with i >= n pass v = 0 and write nothing).  Whole wavefronts.
-__device__ __forceinline__ void publish16(float v, int i, int n, int8_t* planes, int plane_stride, float* xs16,
-                                          float* sum8) {
-    float amax = fabsf(v);
+// Digits of the 16 values of one run held in LDS (vals, 16-byte aligned):
+// lanes 0..15 each read the whole run (broadcast reads, no cross-lane chain),
+// take its max and sum, and write their value's two digits; lane 0 writes the
+// run scale and sum.
+__device__ __forceinline__ void publish_run(const float* vals, int lane, int8_t* planes, int plane_stride,
+                                            float* xs16, float* sum16) {
+    if (lane < RUN) {
+        float amax = 0.0f, s = 0.0f;
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    float s8 = v;
-#pragma unroll
-    for (int off = 1; off < 8; off <<= 1) s8 += __shfl_xor(s8, off, 64);
-    if (i < n) {
-        const int e = digit_exp(amax);
-        int8_t d0, d1, d2;
-        split_digits(v, e, d0, d1, d2);
-        planes[i] = d0;
-        planes[plane_stride + i] = d1;
-        planes[2 * plane_stride + i] = d2;
-        if ((i & 15) == 0) xs16[i >> 4] = ldexpf(1.0f, e - 14);
-        if ((i & 7) == 0) sum8[i >> 3] = s8;
+        for (int i = 0; i < RUN; i += 4) {
+            const float4 q = *(const float4*)(vals + i);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w))));
+            s += (q.x + q.y) + (q.z + q.w);
+        }
+        const uint32_t dg = split2(vals[lane], digit_inv(amax));
+        planes[lane] = (int8_t)(dg & 0xFFu);
+        planes[plane_stride + lane] = (int8_t)(dg >> 8);
+        if (lane == 0) {
+            *xs16 = digit_scale(amax);
+            *sum16 = s;
+        }
     }
 }
 
 // Digits of the H values of token x into LDS, in two steps so the loads can be
-// issued early: x_load reads this thread's VPT = H/NT consecutive values (a
-// whole workgroup of NT threads, VPT in 1..8), x_digits splits them and
-// writes planes, run scales and 8-value sums.
+// issued early: x_load reads this thread's 4 consecutive values (a whole
+// workgroup of NT = H/4 threads, as every supported shape has), x_digits splits
+// them and writes the two planes, run scales and run sums.
 template <int H, int NT>
-__device__ __forceinline__ void x_load(const float* x, float v[8]) {
-    constexpr int VPT = H / NT;
-    static_assert(VPT >= 1 && VPT <= 8 && (VPT & (VPT - 1)) == 0, "values per thread");
-    const int i0 = threadIdx.x * VPT;
-    if constexpr (VPT == 8) {
-        const float4 a = *(const float4*)(x + i0), b = *(const float4*)(x + i0 + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else if constexpr (VPT == 4) {
-        const float4 a = *(const float4*)(x + i0);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = v[5] = v[6] = v[7] = 0.0f;
-    } else if constexpr (VPT == 2) {
-        const float2 a = *(const float2*)(x + i0);
-        v[0] = a.x; v[1] = a.y;
-#pragma unroll
-        for (int k = 2; k < 8; ++k) v[k] = 0.0f;
-    } else {
-        v[0] = x[i0];
-#pragma unroll
-        for (int k = 1; k < 8; ++k) v[k] = 0.0f;
-    }
+__device__ __forceinline__ float4 x_load(const float* x) {
+    static_assert(H / NT == 4, "four values per thread");
+    return *(const float4*)(x + threadIdx.x * 4);
 }
 
 template <int H, int NT>
-__device__ __forceinline__ void x_digits(const float v[8], int8_t* planes, float* xs16, float* sum8) {
-    constexpr int VPT = H / NT;
-    const int i0 = threadIdx.x * VPT;
-    float amax = 0.0f, s8 = 0.0f;
+__device__ __forceinline__ void x_digits(float4 v, int8_t* planes, float* xs16, float* sum16) {
+    const int i0 = threadIdx.x * 4;
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    float s = (v.x + v.y) + (v.z + v.w);
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-        amax = fmaxf(amax, fabsf(v[k]));
-        s8 += v[k];
+    for (int off = 1; off < RUN / 4; off <<= 1) {   // 4 threads per 16-column run
+        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        s += __shfl_xor(s, off, 64);
     }
-#pragma unroll
-    for (int off = 1; off < 16 / VPT; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-#pragma unroll
-    for (int off = 1; off < 8 / VPT; off <<= 1) s8 += __shfl_xor(s8, off, 64);
-    const int e = digit_exp(amax);
-    uint32_t p0 = 0, p1 = 0, p2 = 0, q0 = 0, q1 = 0, q2 = 0;
-#pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-        int8_t d0, d1, d2;
-        split_digits(v[k], e, d0, d1, d2);
-        if (k < 4) {
-            p0 |= (uint32_t)(uint8_t)d0 << (8 * k); p1 |= (uint32_t)(uint8_t)d1 << (8 * k);
-            p2 |= (uint32_t)(uint8_t)d2 << (8 * k);
-        } else {
-            q0 |= (uint32_t)(uint8_t)d0 << (8 * (k - 4)); q1 |= (uint32_t)(uint8_t)d1 << (8 * (k - 4));
-            q2 |= (uint32_t)(uint8_t)d2 << (8 * (k - 4));
-        }
+    const float inv = digit_inv(amax);
+    const uint32_t a = split2(v.x, inv), b = split2(v.y, inv), c = split2(v.z, inv), d = split2(v.w, inv);
+    *(uint32_t*)(planes + i0) = (a & 0xFFu) | ((b & 0xFFu) << 8) | ((c & 0xFFu) << 16) | ((d & 0xFFu) << 24);
+    *(uint32_t*)(planes + H + i0) = (a >> 8) | ((b >> 8) << 8) | ((c >> 8) << 16) | ((d >> 8) << 24);
+    if ((i0 & (RUN - 1)) == 0) {
+        xs16[i0 / RUN] = digit_scale(amax);
+        sum16[i0 / RUN] = s;
     }
-    if constexpr (VPT == 8) {
-        *(uint2*)(planes + i0) = make_uint2(p0, q0);
-        *(uint2*)(planes + H + i0) = make_uint2(p1, q1);
-        *(uint2*)(planes + 2 * H + i0) = make_uint2(p2, q2);
-    } else if constexpr (VPT == 4) {
-        *(uint32_t*)(planes + i0) = p0;
-        *(uint32_t*)(planes + H + i0) = p1;
-        *(uint32_t*)(planes + 2 * H + i0) = p2;
-    } else if constexpr (VPT == 2) {
-        *(uint16_t*)(planes + i0) = (uint16_t)p0;
-        *(uint16_t*)(planes + H + i0) = (uint16_t)p1;
-        *(uint16_t*)(planes + 2 * H + i0) = (uint16_t)p2;
-    } else {
-        planes[i0] = (int8_t)p0;
-        planes[H + i0] = (int8_t)p1;
-        planes[2 * H + i0] = (int8_t)p2;
-    }
-    if ((i0 & 15) == 0) xs16[i0 >> 4] = ldexpf(1.0f, e - 14);
-    if ((i0 & 7) == 0) sum8[i0 >> 3] = s8;
 }
 
 // ---------------------------------------------------------------- kernel A
 
-// Geometry.  LPR = hidden / 32 lanes per row; an instruction covers RPI =
-// 64 / LPR rows; a wave loads NP such row groups (RW = NP * RPI rows) of both
-// the gate and the up matrix; a workgroup is WPG waves, RA = WPG * RW rows (a
-// multiple of 16: the activation digits are published in 16-row runs).
+// Geometry.  LPR = hidden / 64 lanes per row; an instruction covers RPI =
+// 64 / LPR rows of the gate and of the up matrix; a workgroup is WPG = 16 / RPI
+// waves, 16 rows (one activation digit run).
 template <int LPR>
 struct GeoA {
     static constexpr int RPI = 64 / LPR;
-    static constexpr int NP = 1;
-    static constexpr int RW = NP * RPI;
-    static constexpr int WPG = RW >= 16 ? 4 : (16 / RW > 16 ? 16 : 16 / RW);
-    static constexpr int RA = WPG * RW;
+    static constexpr int RA = 16;
+    static constexpr int WPG = RA / RPI;
     static constexpr int NT = 64 * WPG;
 };
 
@@ -198,14 +156,13 @@ __global__ __launch_bounds__(GeoA<LPR>::NT) void k_fast_gate_up(DecodeParams p, 
     using G_ = GeoA<LPR>;
     constexpr int N = LaneGeo<GT>::NRAW;
     constexpr int BB = block_bytes(GT);
-    constexpr int H = 32 * LPR;
-    constexpr int RPI = G_::RPI, NP = G_::NP, RW = G_::RW, RA = G_::RA, NT = G_::NT, WPG = G_::WPG;
+    constexpr int H = 64 * LPR;
+    constexpr int RPI = G_::RPI, RA = G_::RA, NT = G_::NT, WPG = G_::WPG;
     constexpr int64_t ROW_BYTES = (int64_t)(H / 256) * BB;
-    static_assert(RA % 16 == 0 && RA <= 64 && H % NT == 0, "kernel A geometry");
-    __shared__ __attribute__((aligned(16))) int8_t x_planes[3 * H];
-    __shared__ float x_xs16[H / 16];
-    __shared__ float x_sum8[H / 8];
-    __shared__ float s_act[RA];
+    __shared__ __attribute__((aligned(16))) int8_t x_planes[2 * H];
+    __shared__ float x_xs16[H / RUN];
+    __shared__ float x_sum16[H / RUN];
+    __shared__ __attribute__((aligned(16))) float s_act[RA];
     __shared__ float s_gate[WPG];
 
     const int t = blockIdx.z, s = blockIdx.y;
@@ -222,82 +179,73 @@ __global__ __launch_bounds__(GeoA<LPR>::NT) void k_fast_gate_up(DecodeParams p, 
         Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
     }
 
-    const int rr = lane / LPR, li = lane % LPR, blk = li >> 3, k = li & 7;
-    const int wrow0 = blockIdx.x * RA + wave * RW;
+    const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
+    const int row = blockIdx.x * RA + wave * RPI + rr;
 
     // 1. the token's values, then every weight load of this lane (issued in
     // this order, so waiting for x does not wait for the weights)
     const float* xt = p.x + (int64_t)t * H;
-    float xv8[8];
-    x_load<H, NT>(xt, xv8);
-    // the shared expert's sigmoid gate vector, same columns as xv8 (one workgroup per token)
+    const float4 xv = x_load<H, NT>(xt);
+    // the shared expert's sigmoid gate vector, same columns (one workgroup per token)
     const bool gate_wg = shared && blockIdx.x == 0 && p.sh_gate_inp != nullptr;
-    float gi8[8];
-    if (gate_wg) x_load<H, NT>(p.sh_gate_inp, gi8);
+    float4 gi = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (gate_wg) gi = x_load<H, NT>(p.sh_gate_inp);
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t rg[NP][N], ru[NP][N];
-#pragma unroll
-    for (int q = 0; q < NP; ++q) {
-        const int64_t off = (int64_t)(wrow0 + q * RPI + rr) * ROW_BYTES + blk * BB;
-        lane_load<GT>(Gm + off, k, rg[q]);
-        lane_load<GT>(Um + off, k, ru[q]);
-    }
+    uint32_t rg[N], ru[N];
+    const int64_t off = (int64_t)row * ROW_BYTES + blk * BB;
+    lane_load<GT>(Gm + off, k, rg);
+    lane_load<GT>(Um + off, k, ru);
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. token digits (the weight loads are in flight meanwhile)
-    x_digits<H, NT>(xv8, x_planes, x_xs16, x_sum8);
+    x_digits<H, NT>(xv, x_planes, x_xs16, x_sum16);
     __syncthreads();
-    DigitsRef xv;
-    xv.planes = x_planes; xv.xs16 = x_xs16; xv.sum8 = x_sum8; xv.n = H;
+    DigitsRef xd;
+    xd.planes = x_planes; xd.xs16 = x_xs16; xd.sum16 = x_sum16; xd.n = H;
     LaneX X;
-    lane_x<GT>(xv, blk, k, X);
+    lane_x<GT>(xd, blk, k, X);
 
     // 3. gate and up dot products, SwiGLU
-#pragma unroll
-    for (int q = 0; q < NP; ++q) {
-        float g = lane_dot<GT>(rg[q], k, X);
-        float u = lane_dot<GT>(ru[q], k, X);
-        g = lane_group_sum<LPR>(g);
-        u = lane_group_sum<LPR>(u);
-        if (li == 0) s_act[wave * RW + q * RPI + rr] = bad ? 0.0f : silu_mul(g, u);
-    }
+    float g = lane_dot<GT>(rg, k, X);
+    float u = lane_dot<GT>(ru, k, X);
+    g = lane_group_sum<LPR>(g);
+    u = lane_group_sum<LPR>(u);
+    if (li == 0) s_act[wave * RPI + rr] = bad ? 0.0f : silu_mul(g, u);
 
     // shared slot: sigmoid(x . g_inp), the shared expert's gate, once per token
-    // (shared_expert.py:221-251); every thread holds VPT products
+    // (shared_expert.py:221-251); every thread holds 4 products
     if (gate_wg) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(xv8[i], gi8[i], acc);
+        float acc = fmaf(xv.x, gi.x, xv.y * gi.y) + fmaf(xv.z, gi.z, xv.w * gi.w);
         acc = lane_group_sum<64>(acc);
         if (lane == 0) s_gate[wave] = acc;
     }
     if (bad && threadIdx.x == 0 && blockIdx.x == 0) atomicOr(&p.flags[FLAG_BAD_ID], 1);
     __syncthreads();
     if (shared && blockIdx.x == 0 && threadIdx.x == 0) {
-        float d = 0.0f;
+        float dsum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < WPG; ++w) d += s_gate[w];
-        p.sh_scale[t] = gate_wg ? sigmoid_stable(d) : 1.0f;
+        for (int w = 0; w < WPG; ++w) dsum += s_gate[w];
+        p.sh_scale[t] = gate_wg ? sigmoid_stable(dsum) : 1.0f;
     }
 
     // 4. publish the RA activations as digits
     if (wave == 0) {
         uint8_t* base = (uint8_t*)p.act + ((int64_t)t * p.S + s) * L.act_stride;
         const int r0 = blockIdx.x * RA;
-        publish16(lane < RA ? s_act[lane] : 0.0f, lane, RA, (int8_t*)base + r0, L.inter,
-                  (float*)(base + L.xs_off) + r0 / 16, (float*)(base + L.sum_off) + r0 / 8);
+        publish_run(s_act, lane, (int8_t*)base + r0, L.inter, (float*)(base + L.xs_off) + r0 / RUN,
+                    (float*)(base + L.sum_off) + r0 / RUN);
     }
 }
 
 // ---------------------------------------------------------------- kernel B
 
-// LPR = intermediate / 32 lanes per down row; RPI = 64 / LPR rows per
+// LPR = intermediate / 64 lanes per down row; RPI = 64 / LPR rows per
 // instruction; NPB row groups per wave, so RB = NPB * RPI output rows per
 // workgroup.  Wave s of the workgroup computes slot s.
 template <int LPR>
 struct GeoB {
     static constexpr int RPI = 64 / LPR;
-    static constexpr int NPB = 2;
+    static constexpr int NPB = 1;
     static constexpr int RB = NPB * RPI;
 };
 
@@ -305,7 +253,7 @@ template <int DT, int LPR>
 __global__ __launch_bounds__(1024) void k_fast_down(DecodeParams p, FastLayout L) {
     constexpr int N = LaneGeo<DT>::NRAW;
     constexpr int BB = block_bytes(DT);
-    constexpr int I = 32 * LPR;
+    constexpr int I = 64 * LPR;
     constexpr int RPI = GeoB<LPR>::RPI, NPB = GeoB<LPR>::NPB, RB = GeoB<LPR>::RB;
     constexpr int64_t ROW_BYTES = (int64_t)(I / 256) * BB;
     __shared__ float s_y[FAST_MAX_SLOTS][RB];
@@ -313,7 +261,7 @@ __global__ __launch_bounds__(1024) void k_fast_down(DecodeParams p, FastLayout L
 
     const int t = blockIdx.y;
     const int lane = threadIdx.x & 63, s = uniform(threadIdx.x >> 6);   // wave = slot
-    const int rr = lane / LPR, li = lane % LPR, blk = li >> 3, k = li & 7;
+    const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
     const int r0 = blockIdx.x * RB;
     const bool shared = p.has_shared && s == p.top_k;
 
@@ -331,7 +279,7 @@ __global__ __launch_bounds__(1024) void k_fast_down(DecodeParams p, FastLayout L
 
     // activation digits first (small, in L2), then every weight load
     LaneX X;
-    lane_x<DT>(act_digits(L, (uint8_t*)p.act, t, s, p.S), blk, k, X);
+    lane_x<DT>(act_digits(L, (const uint8_t*)p.act, t, s, p.S), blk, k, X);
     __builtin_amdgcn_sched_barrier(0);
     uint32_t raw[NPB][N];
 #pragma unroll
@@ -382,9 +330,9 @@ bool fast_supported(const DecodeParams& p) {
 FastLayout fast_layout(int inter) {
     FastLayout L;
     L.inter = inter;
-    L.xs_off = 3 * inter;
-    L.sum_off = L.xs_off + (inter / 16) * 4;
-    L.act_stride = align256(L.sum_off + (inter / 8) * 4);
+    L.xs_off = 2 * inter;
+    L.sum_off = L.xs_off + (inter / RUN) * 4;
+    L.act_stride = align256(L.sum_off + (inter / RUN) * 4);
     return L;
 }
 
@@ -401,10 +349,10 @@ static void launch_a(const DecodeParams& p, const FastLayout& L, hipStream_t str
 template <int GT>
 static void launch_a_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
     switch (p.hidden) {
-        case 256: launch_a<GT, 8>(p, L, stream, ev); break;
-        case 512: launch_a<GT, 16>(p, L, stream, ev); break;
-        case 1024: launch_a<GT, 32>(p, L, stream, ev); break;
-        default: launch_a<GT, 64>(p, L, stream, ev); break;
+        case 256: launch_a<GT, 4>(p, L, stream, ev); break;
+        case 512: launch_a<GT, 8>(p, L, stream, ev); break;
+        case 1024: launch_a<GT, 16>(p, L, stream, ev); break;
+        default: launch_a<GT, 32>(p, L, stream, ev); break;
     }
 }
 
@@ -420,10 +368,10 @@ static void launch_b(const DecodeParams& p, const FastLayout& L, hipStream_t str
 template <int DT>
 static void launch_b_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
     switch (p.inter) {
-        case 256: launch_b<DT, 8>(p, L, stream, ev); break;
-        case 512: launch_b<DT, 16>(p, L, stream, ev); break;
-        case 1024: launch_b<DT, 32>(p, L, stream, ev); break;
-        default: launch_b<DT, 64>(p, L, stream, ev); break;
+        case 256: launch_b<DT, 4>(p, L, stream, ev); break;
+        case 512: launch_b<DT, 8>(p, L, stream, ev); break;
+        case 1024: launch_b<DT, 16>(p, L, stream, ev); break;
+        default: launch_b<DT, 32>(p, L, stream, ev); break;
     }
 }
 

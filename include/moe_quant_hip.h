@@ -105,6 +105,30 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
                    const float* x, int n_tokens, const int32_t* ids, const float* weights, int top_k,
                    float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Bytes of workspace mqh_moe_prefill needs (has_shared: 0 or 1). */
+int64_t mqh_moe_prefill_workspace_bytes(int n_tokens, int top_k, int n_experts, int hidden, int intermediate,
+                                        int has_shared);
+
+/* Grouped-GEMM MoE layer for a prompt, replacing run_moe_sequence
+ * (src/flash_moe/moe_layer.py:110-195): the expert-by-expert batched forward of
+ * the routed experts (backend_ov.py:210-237, 407-431, or NativeExpert.forward
+ * per token) and the batched shared expert (src/flash_moe/shared_expert.py:200-219):
+ *   y[t] = sum_s weights[t,s] * E_{ids[t,s]}(x[t]) + sigmoid(x[t].sh_gate_inp) * E_sh(x[t])
+ * Same tensors and ids/weights as mqh_moe_decode; x is [n_tokens x hidden],
+ * FP32 (x_bf16 = 0) or BF16 (x_bf16 = 1), 16-byte aligned; y FP32.  The shared
+ * expert (optional, sh_gate == NULL: none) has the routed experts' types and
+ * intermediate size.  Tokens are bucketed per expert on the device; weights are
+ * multiplied as exact integer MFMA operands with FP32 accumulation.  Supported:
+ * Q3_K/Q4_K/Q5_K/Q6_K with gate == up type, hidden and intermediate in
+ * {256, 512, 1024, 2048}, at most 1024 experts; else -2.  The workspace
+ * (256-byte aligned, mqh_moe_prefill_workspace_bytes(...)) is zeroed once with
+ * mqh_workspace_init.  Returns 0, -1, -2, -5 or -6; mqh_status reads -4 / -9. */
+int mqh_moe_prefill(int gate_type, const void* gate, int up_type, const void* up,
+                    int down_type, const void* down, int n_experts, int hidden, int intermediate,
+                    const void* sh_gate, const void* sh_up, const void* sh_down, const float* sh_gate_inp,
+                    const void* x, int x_bf16, int n_tokens, const int32_t* ids, const float* weights,
+                    int top_k, float* y, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Select the kernels behind mqh_moe_decode and moe_quant_expert: 0 (default)
  * = the integer-digit fast kernels whenever the shapes and types allow it
  * (FP32 graph, K-quant types, hidden and intermediate in 256..2048), else the
@@ -113,8 +137,9 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
 int mqh_set_decode_path(int path);
 
 /* Profiling: record HIP events (hipEvent_t, any may be NULL) at the start and
- * end of the two kernels of the calling thread's next mqh_moe_decode or
- * moe_quant_expert -- A: gate/up and SwiGLU, B: down projection and combine.
+ * end of the two GEMM kernels of the calling thread's next mqh_moe_decode,
+ * moe_quant_expert or mqh_moe_prefill -- A: gate/up and SwiGLU, B: down
+ * projection (with the weighted combine in decode).
  * One-shot; the launch itself is unchanged.  No counterpart in the reference
  * (its timers are host wall clocks, bench_phases.py:45-56). */
 int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_stop);

@@ -295,6 +295,57 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
     return launch_decode(p, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
 }
 
+int64_t mqh_moe_prefill_workspace_bytes(int n_tokens, int top_k, int n_experts, int hidden, int intermediate,
+                                        int has_shared) {
+    if (n_tokens <= 0 || top_k < 0 || top_k > 64 || n_experts <= 0 || hidden <= 0 || intermediate <= 0 ||
+        (has_shared != 0 && has_shared != 1) || (top_k == 0 && !has_shared))
+        return ST_ARG;
+    return prefill_layout(n_tokens, top_k, n_experts, hidden, intermediate, has_shared).total;
+}
+
+int mqh_moe_prefill(int gate_type, const void* gate, int up_type, const void* up, int down_type, const void* down,
+                    int n_experts, int hidden, int intermediate, const void* sh_gate, const void* sh_up,
+                    const void* sh_down, const float* sh_gate_inp, const void* x, int x_bf16, int n_tokens,
+                    const int32_t* ids, const float* weights, int top_k, float* y, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
+    const int has_shared = sh_gate != nullptr ? 1 : 0;
+    if (!x || !y || !workspace || (x_bf16 != 0 && x_bf16 != 1)) return ST_ARG;
+    if (n_tokens <= 0 || top_k < 0 || top_k > 64 || (top_k == 0 && !has_shared)) return ST_ARG;
+    if (n_experts <= 0 || hidden <= 0 || intermediate <= 0) return ST_ARG;
+    if (top_k > 0 && (!gate || !up || !down || !ids || !weights)) return ST_ARG;
+    if (has_shared && (!sh_up || !sh_down)) return ST_ARG;
+    const int st = check_expert_types(gate_type, up_type, down_type, hidden, intermediate);
+    if (st) return st;
+    // 16-byte vector loads of x rows, of the gate vector and of the packed tile records
+    if (((uintptr_t)x & 15) || ((uintptr_t)sh_gate_inp & 15) || ((uintptr_t)workspace & 255)) return ST_ARG;
+
+    PrefillParams p{};
+    p.gate = (const uint8_t*)gate; p.up = (const uint8_t*)up; p.down = (const uint8_t*)down;
+    p.gate_type = gate_type; p.up_type = up_type; p.down_type = down_type;
+    p.gate_eb = matrix_bytes(gate_type, intermediate, hidden);
+    p.up_eb = matrix_bytes(up_type, intermediate, hidden);
+    p.down_eb = matrix_bytes(down_type, hidden, intermediate);
+    p.n_experts = n_experts; p.hidden = hidden; p.inter = intermediate;
+    if (!prefill_supported(p)) return ST_TYPE;
+    const PrefillLayout L = prefill_layout(n_tokens, top_k, n_experts, hidden, intermediate, has_shared);
+    if (workspace_bytes < L.total) return ST_WORKSPACE;
+
+    uint8_t* WS = (uint8_t*)workspace;
+    p.sh_gate = (const uint8_t*)sh_gate; p.sh_up = (const uint8_t*)sh_up; p.sh_down = (const uint8_t*)sh_down;
+    p.sh_gate_inp = sh_gate_inp; p.has_shared = has_shared;
+    p.x = x; p.x_bf16 = x_bf16; p.n_tokens = n_tokens;
+    p.ids = ids; p.weights = weights; p.top_k = top_k; p.S = top_k + has_shared;
+    p.y = y;
+    p.flags = (int*)(WS + L.flags_off); p.sh_scale = (float*)(WS + L.scale_off);
+    p.tiles = (int*)(WS + L.tiles_off); p.n_tiles = (int*)(WS + L.ntiles_off);
+    p.pair_tok = (int*)(WS + L.pair_off); p.pos = (int*)(WS + L.pos_off);
+    p.act = (float*)(WS + L.act_off); p.ypair = (float*)(WS + L.ypair_off);
+    p.max_tiles = L.max_tiles;
+    const KernelEvents ev = t_events;
+    t_events = KernelEvents();
+    return launch_prefill(p, (hipStream_t)stream, ev) == hipSuccess ? ST_OK : ST_HIP;
+}
+
 int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_stop) {
     t_events.a_start = (hipEvent_t)a_start;
     t_events.a_stop = (hipEvent_t)a_stop;

@@ -73,8 +73,55 @@ struct FastLayout {
     int64_t xs_off, sum_off, act_stride;
 };
 
-// Optional HIP events recorded at the start and end of the two decode kernels
-// (A: gate/up, B: down + combine), for profiling; null members are ignored.
+// Grouped prefill (moe_prefill.hip).  Token/slot pairs are bucketed by expert
+// on the device; a tile is up to PREFILL_TILE tokens of one expert (or of the
+// shared expert, expert id -1).
+constexpr int PREFILL_TILE = 16;
+constexpr int PREFILL_MAX_EXPERTS = 1024;
+
+struct PrefillParams {
+    const uint8_t* gate;
+    const uint8_t* up;
+    const uint8_t* down;
+    int gate_type, up_type, down_type;
+    int64_t gate_eb, up_eb, down_eb;
+    int n_experts, hidden, inter;
+    const uint8_t* sh_gate;
+    const uint8_t* sh_up;
+    const uint8_t* sh_down;
+    const float* sh_gate_inp;
+    int has_shared;
+    const void* x;          // [n_tokens x hidden], FP32 or BF16
+    int x_bf16;
+    int n_tokens;
+    const int32_t* ids;     // [n_tokens x top_k]
+    const float* weights;
+    int top_k;
+    int S;                  // slots per token: top_k + has_shared
+    float* y;               // [n_tokens x hidden]
+    // workspace views
+    int* flags;             // [N_FLAGS]
+    float* sh_scale;        // [n_tokens]
+    int* tiles;             // [max_tiles x 4]: expert, first pair, token count, 0
+    int* n_tiles;           // [1]
+    int* pair_tok;          // [P]: token of sorted pair p (P = n_tokens * S)
+    int* pos;               // [n_tokens x S]: sorted pair index of (token, slot)
+    float* act;             // [P x inter] SwiGLU activations
+    float* ypair;           // [P x hidden] expert outputs per pair
+    int max_tiles;
+};
+
+struct PrefillLayout {
+    int64_t flags_off, scale_off, tiles_off, ntiles_off, pair_off, pos_off, act_off, ypair_off, total;
+    int max_tiles;
+};
+
+PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden, int inter, int has_shared);
+bool prefill_supported(const PrefillParams& p);
+
+// Optional HIP events recorded at the start and end of the two GEMM kernels of
+// a layer (A: gate/up + SwiGLU, B: down projection, with the combine in
+// decode), for profiling; null members are ignored.
 struct KernelEvents {
     hipEvent_t a_start = nullptr, a_stop = nullptr, b_start = nullptr, b_stop = nullptr;
     bool armed_a() const { return a_start || a_stop; }
@@ -85,6 +132,7 @@ hipError_t launch_decode_generic(const DecodeParams& p, hipStream_t stream, cons
 bool fast_supported(const DecodeParams& p);
 FastLayout fast_layout(int inter);
 hipError_t launch_decode_fast(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev);
+hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream, const KernelEvents& ev);
 hipError_t launch_dequant(int type, const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream);
 
 }  // namespace mqh

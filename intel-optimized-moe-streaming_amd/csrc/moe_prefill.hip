@@ -1,0 +1,486 @@
+// moe_prefill.hip -- grouped-GEMM MoE layer for a prompt (many tokens).
+//
+// Replaces run_moe_sequence (src/flash_moe/moe_layer.py:110-195), which runs the
+// routed experts expert by expert on their token batches (backend_ov.py:210-237,
+// 407-431) and then adds the batched shared expert (shared_expert.py:200-219):
+//   for every expert e and the tokens routed to it:
+//     act = silu(X_e W_gate^T) * (X_e W_up^T),  Y_e = act W_down^T
+//   y[t] = sum_s w[t,s] * Y_{ids[t,s]}[t]  (top-k order)  + sigmoid(x_t . g_inp) * shared(x_t)
+//
+// Four launches, no inter-workgroup synchronisation:
+//   P0 k_prefill_route     one workgroup: buckets the (token, slot) pairs by expert
+//                          and cuts each expert's tokens into tiles of 16.
+//   P1 k_prefill_gate_up   grid (I/64, max_tiles): 64 intermediate rows x one tile,
+//                          SwiGLU fused; the shared expert's tiles also produce its
+//                          sigmoid gate.
+//   P2 k_prefill_down      grid (H/64, max_tiles): 64 output rows x one tile.
+//   P3 k_prefill_combine   grid (H/256, T): the weighted sum in top-k order.
+//
+// P1/P2 are MFMA GEMMs (v_mfma_f32_16x16x32_f16, FP32 accumulate) whose weight
+// operand is built in registers straight from the quantized blocks as exact
+// integers (kquant_frag.h); the tile's tokens are the other operand, staged
+// once per workgroup in LDS as FP16 planes with a power-of-two scale per token.
+#include <hip/hip_ext.h>
+
+#include <utility>
+
+#include "kquant_frag.h"
+#include "moe_decode.h"
+
+namespace mqh {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int PF_ROWS = 64;      // weight rows per workgroup: 4 waves x 16
+constexpr int PF_RING = 2;       // super-blocks of loads in flight per lane while one is computed
+constexpr int PF_PAD = 8;        // LDS row padding (halves)
+
+template <int... Ms, class F>
+__device__ __forceinline__ void pf_unroll(std::integer_sequence<int, Ms...>, F&& f) {
+    (f(std::integral_constant<int, Ms>{}), ...);
+}
+
+__device__ __forceinline__ float pf_silu_mul(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+    return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
+}
+
+__device__ __forceinline__ float pf_sigmoid(float v) {
+    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+
+__device__ __forceinline__ float pf_wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float pf_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ------------------------------------------------------------ token staging
+//
+// One wave stages token row `row` of src (K values, FP32 or BF16) as LDS column
+// j of the B operand: high plane xh[j][K + PF_PAD], low plane xl (SPLIT only),
+// and the 32-column sub-block sums / 32 as [j][block][hi 0..7 | lo 0..7] in xs.
+// A lane owns 8 consecutive values per 512-column pass.  With gvec set, the
+// wave also returns x_row . gvec (FP32, unscaled) in every lane.
+template <int K, bool BF16, bool SPLIT>
+__device__ __forceinline__ float pf_stage(const void* src, int64_t row, int j, _Float16* xh, _Float16* xl,
+                                          _Float16* xs, int* s_exp, const float* gvec) {
+    constexpr int NIT = K >= 512 ? K / 512 : 1, KP = K + PF_PAD, NB = K / 256;
+    const int lane = threadIdx.x & 63;
+    float v[NIT][8];
+    float amax = 0.0f, gdot = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int c = 512 * it + 8 * lane;
+        if (c < K) {
+            if constexpr (BF16) {
+                const uint4 raw = *(const uint4*)((const uint16_t*)src + row * K + c);
+                const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[it][2 * e] = __uint_as_float(w[e] << 16);
+                    v[it][2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+                }
+            } else {
+                const float4 a = *(const float4*)((const float*)src + row * K + c);
+                const float4 b = *(const float4*)((const float*)src + row * K + c + 4);
+                v[it][0] = a.x; v[it][1] = a.y; v[it][2] = a.z; v[it][3] = a.w;
+                v[it][4] = b.x; v[it][5] = b.y; v[it][6] = b.z; v[it][7] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[it][e] = 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[it][e]));
+        if (gvec != nullptr && c < K) {
+            const float4 g0 = *(const float4*)(gvec + c), g1 = *(const float4*)(gvec + c + 4);
+            gdot = fmaf(v[it][0], g0.x, gdot); gdot = fmaf(v[it][1], g0.y, gdot);
+            gdot = fmaf(v[it][2], g0.z, gdot); gdot = fmaf(v[it][3], g0.w, gdot);
+            gdot = fmaf(v[it][4], g1.x, gdot); gdot = fmaf(v[it][5], g1.y, gdot);
+            gdot = fmaf(v[it][6], g1.z, gdot); gdot = fmaf(v[it][7], g1.w, gdot);
+        }
+    }
+    const int k = frag_exp(pf_wave_max(amax));
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int c = 512 * it + 8 * lane;
+        h8_t hi, lo;
+        float s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            _Float16 h, l;
+            frag_split(v[it][e], k, h, l);
+            hi[e] = h;
+            lo[e] = l;
+            s += ldexpf(v[it][e], -k);
+        }
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        if (c < K) {
+            *(h8_t*)(xh + j * KP + c) = hi;
+            if constexpr (SPLIT) *(h8_t*)(xl + j * KP + c) = lo;
+            if ((lane & 3) == 0) {
+                const int sb = c >> 5;   // sub-block: block sb / 8, slot sb % 8
+                _Float16 h, l;
+                frag_split(s, 5, h, l);
+                xs[(j * NB + (sb >> 3)) * 16 + (sb & 7)] = h;
+                xs[(j * NB + (sb >> 3)) * 16 + 8 + (sb & 7)] = l;
+            }
+        }
+    }
+    if (lane == 0) s_exp[j] = k;
+    return pf_wave_sum(gdot);
+}
+
+// ------------------------------------------------------------ the GEMM core
+//
+// acc[mt] += W_mt[16 rows of this wave] x B^T over K = NB * 256 columns for NMAT
+// weight matrices sharing the B operand.  prefetch() loads the first blocks
+// before the caller stages the tokens, so that the two overlap.  D layout:
+// lane l holds rows 4(l/16) + i, token column l % 16.
+template <int T, int NMAT, int NB>
+struct PfRows {
+    static constexpr int NW = FragGeo<T>::NW, BB = block_bytes(T);
+    static constexpr int D = NB < PF_RING ? NB : PF_RING;
+    static_assert(NB % D == 0, "blocks per row must be a multiple of the ring size");
+    uint32_t raw[D][NMAT][NW];
+
+    __device__ __forceinline__ void load(const uint8_t* const (&W)[NMAT], int b, int q, uint32_t (&dst)[NMAT][NW]) {
+#pragma unroll
+        for (int mt = 0; mt < NMAT; ++mt) frag_load<T>(W[mt] + b * BB, q, dst[mt]);
+    }
+
+    __device__ __forceinline__ void prefetch(const uint8_t* const (&W)[NMAT], int q) {
+#pragma unroll
+        for (int b = 0; b < D; ++b) load(W, b, q, raw[b]);
+    }
+
+    template <bool SPLIT>
+    __device__ __forceinline__ void run(const uint8_t* const (&W)[NMAT], int q, const _Float16* xh, const _Float16* xl,
+                                        const _Float16* xs, f32x4 (&acc)[NMAT]) {
+        constexpr int KP = NB * 256 + PF_PAD;
+        const int lane = threadIdx.x & 63, tok = lane & 15;
+        // a runtime loop over groups of D blocks keeps one block's operands live at a
+        // time; the refill of a ring slot is unconditional (the tail re-reads the
+        // last block, in bounds and unused)
+#pragma unroll 1
+        for (int b0 = 0; b0 < NB; b0 += D)
+#pragma unroll
+        for (int bi = 0; bi < D; ++bi) {
+            const int b = b0 + bi;
+            uint32_t cur[NMAT][NW];
+#pragma unroll
+            for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+                for (int i = 0; i < NW; ++i) cur[mt][i] = raw[bi][mt][i];
+            load(W, min(b + D, NB - 1), q, raw[bi]);
+
+            f32x4 P[NMAT];
+#pragma unroll
+            for (int mt = 0; mt < NMAT; ++mt) P[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            pf_unroll(std::make_integer_sequence<int, 8>{}, [&](auto mc) {
+                constexpr int m = decltype(mc)::value;
+                const int off = tok * KP + b * 256 + 32 * m + 8 * q;
+                const h8_t bh = *(const h8_t*)(xh + off);
+                h8_t bl;
+                if constexpr (SPLIT) bl = *(const h8_t*)(xl + off);
+#pragma unroll
+                for (int mt = 0; mt < NMAT; ++mt) {
+                    h8_t a[2];
+                    frag_step<T, m>(cur[mt], q, a);
+                    P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], bh, P[mt], 0, 0, 0);
+                    if constexpr (FragGeo<T>::NA == 2) P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], bh, P[mt], 0, 0, 0);
+                    if constexpr (SPLIT)
+                        P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag_lo_operand<T>(a), bl, P[mt], 0, 0, 0);
+                }
+            });
+            f32x4 Mn[NMAT];
+            if constexpr (FragGeo<T>::MIN) {
+                const h4_t bs = *(const h4_t*)(xs + (tok * NB + b) * 16 + 4 * q);
+#pragma unroll
+                for (int mt = 0; mt < NMAT; ++mt)
+                    Mn[mt] = __builtin_amdgcn_mfma_f32_16x16x16f16(frag_mins<T>(cur[mt], q), bs,
+                                                                   f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            }
+            // d (and dmin) of D row 4q + i live in the header word of A lane 4q + i
+#pragma unroll
+            for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t hdr = (uint32_t)__shfl((int)cur[mt][FragGeo<T>::HDR], 4 * q + i, 64);
+                    acc[mt][i] = fmaf(frag_h2f(hdr), P[mt][i], acc[mt][i]);
+                    if constexpr (FragGeo<T>::MIN) acc[mt][i] = fmaf(-frag_h2f(hdr >> 16), Mn[mt][i], acc[mt][i]);
+                }
+        }
+    }
+};
+
+__device__ __forceinline__ int4 pf_tile(const PrefillParams& p, int tile) { return ((const int4*)p.tiles)[tile]; }
+
+// ------------------------------------------------------------ P0
+
+__global__ __launch_bounds__(1024) void k_prefill_route(PrefillParams p) {
+    __shared__ int cnt[PREFILL_MAX_EXPERTS], off[PREFILL_MAX_EXPERTS], fill[PREFILL_MAX_EXPERTS];
+    __shared__ int wsum[16][2];
+    const int T = p.n_tokens, K = p.top_k, E = p.n_experts, TK = T * K;
+    const int e = threadIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (e < E) { cnt[e] = 0; fill[e] = 0; }
+    __syncthreads();
+    for (int i = threadIdx.x; i < TK; i += blockDim.x) {
+        const int id = p.ids[i];
+        if (id < 0 || id >= E) atomicOr(&p.flags[FLAG_BAD_ID], 1);
+        else atomicAdd(&cnt[id], 1);
+    }
+    __syncthreads();
+    // exclusive scans of pair counts and tile counts over experts
+    const int c = e < E ? cnt[e] : 0, tc = (c + PREFILL_TILE - 1) / PREFILL_TILE;
+    int ic = c, it = tc;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int yc = __shfl_up(ic, o, 64), yt = __shfl_up(it, o, 64);
+        if (lane >= o) { ic += yc; it += yt; }
+    }
+    if (lane == 63) { wsum[wave][0] = ic; wsum[wave][1] = it; }
+    __syncthreads();
+    int bc = 0, bt = 0, tott = 0;
+    for (int w = 0; w < 16; ++w) {
+        if (w < wave) { bc += wsum[w][0]; bt += wsum[w][1]; }
+        tott += wsum[w][1];
+    }
+    const int first = bc + ic - c, tfirst = bt + it - tc;
+    if (e < E) {
+        off[e] = first;
+        for (int j = 0; j < tc; ++j)
+            ((int4*)p.tiles)[tfirst + j] =
+                make_int4(e, first + PREFILL_TILE * j, min(PREFILL_TILE, c - PREFILL_TILE * j), 0);
+    }
+    if (threadIdx.x == 0) {
+        int nt = tott;
+        if (p.has_shared)
+            for (int j = 0; j < T; j += PREFILL_TILE) ((int4*)p.tiles)[nt++] = make_int4(-1, TK + j, min(PREFILL_TILE, T - j), 0);
+        *p.n_tiles = nt;
+    }
+    __syncthreads();
+    // pair order inside an expert follows the atomics; a pair's result does not
+    // depend on its column in the tile, so outputs do not depend on it
+    for (int i = threadIdx.x; i < TK; i += blockDim.x) {
+        const int id = p.ids[i];
+        int pp = -1;
+        if (id >= 0 && id < E) {
+            pp = off[id] + atomicAdd(&fill[id], 1);
+            p.pair_tok[pp] = i / K;
+        }
+        p.pos[(i / K) * p.S + (i % K)] = pp;
+    }
+    if (p.has_shared)
+        for (int t = threadIdx.x; t < T; t += blockDim.x) {
+            p.pair_tok[TK + t] = t;
+            p.pos[t * p.S + K] = TK + t;
+        }
+}
+
+// ------------------------------------------------------------ P1
+
+template <int GT, int NBH, bool XBF16>
+__global__ __launch_bounds__(256) void k_prefill_gate_up(PrefillParams p) {
+    constexpr int H = NBH * 256, KP = H + PF_PAD;
+    constexpr bool SPLIT = !XBF16;   // BF16 tokens are exact in the high plane
+    __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
+    __shared__ __attribute__((aligned(16))) _Float16 xl[SPLIT ? PREFILL_TILE * KP : 8];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[PREFILL_TILE * NBH * 16];
+    __shared__ int s_exp[PREFILL_TILE];
+    const int tile = blockIdx.y;
+    if (tile >= *p.n_tiles) return;
+    const int4 td = pf_tile(p, tile);
+    const int e = td.x, first = td.y, cnt = td.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
+    const int r0 = blockIdx.x * PF_ROWS + wave * 16;
+    const int64_t row_bytes = (int64_t)NBH * block_bytes(GT);
+    const uint8_t* W[2];
+    if (e < 0) { W[0] = p.sh_gate; W[1] = p.sh_up; }
+    else { W[0] = p.gate + (int64_t)e * p.gate_eb; W[1] = p.up + (int64_t)e * p.up_eb; }
+    W[0] += (int64_t)(r0 + (lane & 15)) * row_bytes;
+    W[1] += (int64_t)(r0 + (lane & 15)) * row_bytes;
+
+    PfRows<GT, 2, NBH> g;
+    g.prefetch(W, q);
+    const bool gate_out = e < 0 && blockIdx.x == 0;
+    for (int j = wave; j < cnt; j += 4) {
+        const int t = p.pair_tok[first + j];
+        const float gd = pf_stage<H, XBF16, SPLIT>(p.x, t, j, xh, xl, xs, s_exp, gate_out ? p.sh_gate_inp : nullptr);
+        if (gate_out && lane == 0) p.sh_scale[t] = p.sh_gate_inp != nullptr ? pf_sigmoid(gd) : 1.0f;
+    }
+    __syncthreads();
+
+    f32x4 acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+    g.template run<SPLIT>(W, q, xh, xl, xs, acc);
+
+    // columns at or past cnt hold stale LDS; their results are never stored
+    const int col = lane & 15;
+    if (col < cnt) {
+        const float sc = ldexpf(1.0f, s_exp[col]);
+        float4 a;
+        a.x = pf_silu_mul(acc[0][0] * sc, acc[1][0] * sc);
+        a.y = pf_silu_mul(acc[0][1] * sc, acc[1][1] * sc);
+        a.z = pf_silu_mul(acc[0][2] * sc, acc[1][2] * sc);
+        a.w = pf_silu_mul(acc[0][3] * sc, acc[1][3] * sc);
+        *(float4*)(p.act + (int64_t)(first + col) * p.inter + r0 + 4 * q) = a;
+    }
+}
+
+// ------------------------------------------------------------ P2
+
+template <int DT, int NBI>
+__global__ __launch_bounds__(256) void k_prefill_down(PrefillParams p) {
+    constexpr int I = NBI * 256, KP = I + PF_PAD;
+    __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
+    __shared__ __attribute__((aligned(16))) _Float16 xl[PREFILL_TILE * KP];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[PREFILL_TILE * NBI * 16];
+    __shared__ int s_exp[PREFILL_TILE];
+    const int tile = blockIdx.y;
+    if (tile >= *p.n_tiles) return;
+    const int4 td = pf_tile(p, tile);
+    const int e = td.x, first = td.y, cnt = td.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
+    const int r0 = blockIdx.x * PF_ROWS + wave * 16;
+    const int64_t row_bytes = (int64_t)NBI * block_bytes(DT);
+    const uint8_t* W[1] = {(e < 0 ? p.sh_down : p.down + (int64_t)e * p.down_eb) + (int64_t)(r0 + (lane & 15)) * row_bytes};
+
+    PfRows<DT, 1, NBI> g;
+    g.prefetch(W, q);
+    for (int j = wave; j < cnt; j += 4) pf_stage<I, false, true>(p.act, first + j, j, xh, xl, xs, s_exp, nullptr);
+    __syncthreads();
+
+    f32x4 acc[1] = {{0, 0, 0, 0}};
+    g.template run<true>(W, q, xh, xl, xs, acc);
+
+    const int col = lane & 15;
+    if (col < cnt) {
+        const float sc = ldexpf(1.0f, s_exp[col]);
+        *(float4*)(p.ypair + (int64_t)(first + col) * p.hidden + r0 + 4 * q) =
+            make_float4(acc[0][0] * sc, acc[0][1] * sc, acc[0][2] * sc, acc[0][3] * sc);
+    }
+}
+
+// ------------------------------------------------------------ P3
+
+__global__ __launch_bounds__(256) void k_prefill_combine(PrefillParams p) {
+    const int t = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
+    if (h >= p.hidden) return;
+    float acc = 0.0f;
+    for (int s = 0; s < p.top_k; ++s) {
+        const int pp = p.pos[t * p.S + s];
+        if (pp < 0) continue;   // expert id out of range: flagged by the route pass
+        acc = __fadd_rn(acc, __fmul_rn(p.weights[t * p.top_k + s], p.ypair[(int64_t)pp * p.hidden + h]));
+    }
+    if (p.has_shared) {
+        const int pp = p.pos[t * p.S + p.top_k];
+        acc = __fadd_rn(acc, __fmul_rn(p.sh_scale[t], p.ypair[(int64_t)pp * p.hidden + h]));
+    }
+    p.y[(int64_t)t * p.hidden + h] = acc;
+    if (!isfinite(acc)) atomicOr(&p.flags[FLAG_NONFINITE], 1);
+}
+
+// ------------------------------------------------------------ host side
+
+static bool pf_type(int t) { return t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+static bool pf_dim(int n) { return n == 256 || n == 512 || n == 1024 || n == 2048; }
+
+bool prefill_supported(const PrefillParams& p) {
+    if (!pf_dim(p.hidden) || !pf_dim(p.inter) || p.n_experts < 1 || p.n_experts > PREFILL_MAX_EXPERTS) return false;
+    if (!(pf_type(p.gate_type) && p.up_type == p.gate_type && pf_type(p.down_type))) return false;
+    return true;
+}
+
+PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden, int inter, int has_shared) {
+    PrefillLayout L;
+    const int S = top_k + (has_shared ? 1 : 0);
+    const int64_t P = (int64_t)n_tokens * S;
+    const int64_t TK = (int64_t)n_tokens * top_k;
+    L.max_tiles = (int)(std::min<int64_t>(n_experts, TK) + (TK + PREFILL_TILE - 1) / PREFILL_TILE +
+                        (has_shared ? (n_tokens + PREFILL_TILE - 1) / PREFILL_TILE : 0));
+    L.flags_off = 0;
+    L.scale_off = align256((int64_t)N_FLAGS * 4);
+    L.tiles_off = align256(L.scale_off + (int64_t)n_tokens * 4);
+    L.ntiles_off = align256(L.tiles_off + (int64_t)std::max(L.max_tiles, 1) * 16);
+    L.pair_off = align256(L.ntiles_off + 4);
+    L.pos_off = align256(L.pair_off + P * 4);
+    L.act_off = align256(L.pos_off + P * 4);
+    L.ypair_off = align256(L.act_off + P * inter * 4);
+    L.total = align256(L.ypair_off + P * hidden * 4);
+    return L;
+}
+
+// a kernel launch, bracketed by the profiling events when they are armed
+#define PF_LAUNCH(kernel, grid, armed, e0, e1, s, p)                                    \
+    do {                                                                                \
+        if (armed) hipExtLaunchKernelGGL(kernel, grid, dim3(256), 0, s, e0, e1, 0, p); \
+        else hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, p);                      \
+    } while (0)
+
+template <int GT, int NBH>
+static void launch_p1(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
+    const dim3 grid(p.inter / PF_ROWS, p.max_tiles);
+    if (p.x_bf16) PF_LAUNCH((k_prefill_gate_up<GT, NBH, true>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p);
+    else PF_LAUNCH((k_prefill_gate_up<GT, NBH, false>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p);
+}
+
+template <int GT>
+static void launch_p1_h(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
+    switch (p.hidden) {
+        case 256: launch_p1<GT, 1>(p, s, ev); break;
+        case 512: launch_p1<GT, 2>(p, s, ev); break;
+        case 1024: launch_p1<GT, 4>(p, s, ev); break;
+        default: launch_p1<GT, 8>(p, s, ev); break;
+    }
+}
+
+template <int DT, int NBI>
+static void launch_p2(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
+    const dim3 grid(p.hidden / PF_ROWS, p.max_tiles);
+    PF_LAUNCH((k_prefill_down<DT, NBI>), grid, ev.armed_b(), ev.b_start, ev.b_stop, s, p);
+}
+
+template <int DT>
+static void launch_p2_i(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
+    switch (p.inter) {
+        case 256: launch_p2<DT, 1>(p, s, ev); break;
+        case 512: launch_p2<DT, 2>(p, s, ev); break;
+        case 1024: launch_p2<DT, 4>(p, s, ev); break;
+        default: launch_p2<DT, 8>(p, s, ev); break;
+    }
+}
+
+hipError_t launch_prefill(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
+    if (p.n_tokens <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_prefill_route, dim3(1), dim3(1024), 0, s, p);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    switch (p.gate_type) {
+        case T_Q4_K: launch_p1_h<T_Q4_K>(p, s, ev); break;
+        case T_Q5_K: launch_p1_h<T_Q5_K>(p, s, ev); break;
+        case T_Q6_K: launch_p1_h<T_Q6_K>(p, s, ev); break;
+        default: launch_p1_h<T_Q3_K>(p, s, ev); break;
+    }
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    switch (p.down_type) {
+        case T_Q4_K: launch_p2_i<T_Q4_K>(p, s, ev); break;
+        case T_Q5_K: launch_p2_i<T_Q5_K>(p, s, ev); break;
+        case T_Q6_K: launch_p2_i<T_Q6_K>(p, s, ev); break;
+        default: launch_p2_i<T_Q3_K>(p, s, ev); break;
+    }
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL(k_prefill_combine, dim3((p.hidden + 255) / 256, p.n_tokens), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+}  // namespace mqh

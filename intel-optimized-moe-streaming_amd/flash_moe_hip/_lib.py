@@ -23,6 +23,8 @@ EXPORTS = (
     "mqh_dequant",
     "mqh_moe_workspace_bytes",
     "mqh_moe_decode",
+    "mqh_moe_prefill_workspace_bytes",
+    "mqh_moe_prefill",
     "mqh_set_decode_path",
     "mqh_profile_next_decode",
     "mqh_workspace_init",
@@ -72,6 +74,15 @@ def _declare(lib: C.CDLL) -> C.CDLL:
         _P, _I, _P, _I64, _P,                    # y, fp16_graph, workspace, ws bytes, stream
     ]
     lib.mqh_moe_decode.restype = _I
+    lib.mqh_moe_prefill_workspace_bytes.argtypes = [_I, _I, _I, _I, _I, _I]
+    lib.mqh_moe_prefill_workspace_bytes.restype = _I64
+    lib.mqh_moe_prefill.argtypes = [
+        _I, _P, _I, _P, _I, _P, _I, _I, _I,      # routed types/tensors, n_experts, hidden, inter
+        _P, _P, _P, _P,                          # shared tensors, sh_gate_inp
+        _P, _I, _I, _P, _P, _I,                  # x, x_bf16, n_tokens, ids, weights, top_k
+        _P, _P, _I64, _P,                        # y, workspace, ws bytes, stream
+    ]
+    lib.mqh_moe_prefill.restype = _I
     lib.mqh_profile_next_decode.argtypes = [_P, _P, _P, _P]
     lib.mqh_profile_next_decode.restype = _I
     lib.mqh_set_decode_path.argtypes = [_I]

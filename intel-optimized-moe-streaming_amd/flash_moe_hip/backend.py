@@ -115,8 +115,19 @@ class HipExpertBackend:
         return self._finish(y, "fused MoE layer").reshape(L.hidden)
 
     def moe_tokens(self, layer: int, activations, ids, weights, include_shared: bool = True) -> np.ndarray:
+        """A prompt's tokens through the layer (run_moe_sequence): the grouped
+        prefill kernels when they cover the layer (FP32 graph, more than one
+        token), else the fused decode kernels."""
+        import torch
+
         L = self.layers[layer]
-        y = self._run(L, self._x(activations, L.hidden), ids, weights, include_shared, self.fp16_graph)
+        x = self._x(activations, L.hidden)
+        if self.fp16_graph == 0 and x.shape[0] > 1 and self.runner.prefill_supported(L):
+            tid = torch.from_numpy(np.ascontiguousarray(ids, dtype=np.int32)).to(self.device)
+            tw = torch.from_numpy(np.ascontiguousarray(weights, dtype=np.float32)).to(self.device)
+            y = self.runner.prefill(L, x, tid, tw, use_shared=include_shared)
+        else:
+            y = self._run(L, x, ids, weights, include_shared, self.fp16_graph)
         return self._finish(y, "fused MoE tokens")
 
     def shared_forward(self, layer: int, activations) -> np.ndarray | None:

@@ -1,9 +1,11 @@
 """Device-resident fused MoE calls (thin wrapper over the mqh_* C ABI).
 
-``MoeRunner.decode(layer, x, ids, weights)`` enqueues one fused launch for
-every routed expert of every token plus the layer's shared expert; nothing is
-synchronized.  ``MoeRunner.status()`` synchronizes and returns the fault
-status latched by the kernels (0, -4 non-finite, -9 bad expert id).
+``MoeRunner.decode(layer, x, ids, weights)`` enqueues the fused GEMV kernels
+for every routed expert of every token plus the layer's shared expert;
+``MoeRunner.prefill(...)`` the grouped-GEMM kernels for a prompt (tokens
+bucketed per expert on the device).  Nothing is synchronized.
+``MoeRunner.status()`` synchronizes and returns the fault status latched by
+the kernels (0, -4 non-finite, -9 bad expert id).
 """
 from __future__ import annotations
 
@@ -11,6 +13,11 @@ from . import _lib
 from .layer_store import ExpertLayer
 
 _NULL = None
+
+# shapes and types the grouped prefill kernels are built for
+PREFILL_TYPES = (11, 12, 13, 14)
+PREFILL_DIMS = (256, 512, 1024, 2048)
+PREFILL_MAX_EXPERTS = 1024
 
 
 class MoeRunner:
@@ -25,11 +32,14 @@ class MoeRunner:
         self._ws_bytes = 0
 
     def _workspace(self, n_tokens: int, top_k: int, inter: int, sh_inter: int, stream):
-        import torch
-
         need = int(self.lib.mqh_moe_workspace_bytes(n_tokens, top_k, inter, sh_inter))
         if need < 0:
             _lib.check(need, "mqh_moe_workspace_bytes")
+        return self._reserve(need, stream)
+
+    def _reserve(self, need: int, stream):
+        import torch
+
         if self._ws is None or need > self._ws_bytes:
             if self._ws is not None:
                 # keep the latched flags of the old workspace visible
@@ -76,6 +86,67 @@ class MoeRunner:
             x.data_ptr(), T, ids.data_ptr() if top_k else _NULL, weights.data_ptr() if top_k else _NULL, top_k,
             y.data_ptr(), int(fp16_graph), ws.data_ptr(), self._ws_bytes, stream.cuda_stream)
         _lib.check(rc, "mqh_moe_decode")
+        return y
+
+    @staticmethod
+    def prefill_supported(layer: ExpertLayer) -> bool:
+        """Whether the grouped prefill kernels cover this layer's routed experts."""
+        t = layer.types
+        return (t["gate"] == t["up"] and all(t[r] in PREFILL_TYPES for r in ("gate", "up", "down"))
+                and layer.hidden in PREFILL_DIMS and layer.intermediate in PREFILL_DIMS
+                and layer.n_experts <= PREFILL_MAX_EXPERTS)
+
+    @staticmethod
+    def _shared_in_prefill(layer: ExpertLayer) -> bool:
+        sh = layer.shared
+        return sh is not None and sh.types == layer.types and sh.intermediate == layer.intermediate
+
+    def prefill(self, layer: ExpertLayer, x, ids, weights, *, y=None, use_shared: bool = True, stream=None):
+        """The layer for a prompt: x [T,H] FP32 or BF16, ids [T,k] int32, weights
+        [T,k] FP32 (CUDA tensors).  Same result as ``decode`` up to FP32
+        summation order inside each dot product.  A shared expert whose types or
+        size differ from the routed experts' runs through the decode kernels and
+        is added after the routed sum, as in run_moe_sequence."""
+        import torch
+
+        if not self.prefill_supported(layer):
+            raise ValueError("the grouped prefill kernels do not cover this layer's types or shape")
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        x = x.reshape(-1, layer.hidden)
+        T = x.shape[0]
+        if x.dtype not in (torch.float32, torch.bfloat16) or not x.is_contiguous():
+            raise ValueError("x must be contiguous FP32 or BF16")
+        top_k = int(ids.shape[-1])
+        ids = ids.reshape(T, top_k)
+        weights = weights.reshape(T, top_k)
+        if ids.dtype != torch.int32 or weights.dtype != torch.float32:
+            raise ValueError("ids must be int32 and weights FP32")
+        if not (ids.is_contiguous() and weights.is_contiguous()):
+            raise ValueError("ids and weights must be contiguous")
+        sh = layer.shared if use_shared else None
+        inside = sh is not None and self._shared_in_prefill(layer)
+        if y is None:
+            y = torch.empty((T, layer.hidden), dtype=torch.float32, device=x.device)
+        if T == 0:
+            return y
+        need = int(self.lib.mqh_moe_prefill_workspace_bytes(T, top_k, layer.n_experts, layer.hidden,
+                                                           layer.intermediate, int(inside)))
+        if need < 0:
+            _lib.check(need, "mqh_moe_prefill_workspace_bytes")
+        ws = self._reserve(need, stream)
+        t = layer.tensors
+        rc = self.lib.mqh_moe_prefill(
+            layer.types["gate"], t["gate"].data_ptr(), layer.types["up"], t["up"].data_ptr(),
+            layer.types["down"], t["down"].data_ptr(), layer.n_experts, layer.hidden, layer.intermediate,
+            sh.gate.data_ptr() if inside else _NULL, sh.up.data_ptr() if inside else _NULL,
+            sh.down.data_ptr() if inside else _NULL,
+            sh.gate_inp.data_ptr() if (inside and sh.gate_inp is not None) else _NULL,
+            x.data_ptr(), int(x.dtype == torch.bfloat16), T, ids.data_ptr(), weights.data_ptr(), top_k,
+            y.data_ptr(), ws.data_ptr(), self._ws_bytes, stream.cuda_stream)
+        _lib.check(rc, "mqh_moe_prefill")
+        if sh is not None and not inside:
+            y += self.decode(layer, x.float(), None, None, use_shared=True, stream=stream)
         return y
 
     def status(self, stream=None) -> int:

@@ -1,0 +1,130 @@
+// Host build of the prefill GEMM's operand math (kquant_frag.h): a 64-lane wave
+// emulated lane by lane, with the MFMA layouts of v_mfma_f32_16x16x32_f16
+// (A: row l%16, k = 8(l/16) + i; B: column l%16, same k) and
+// v_mfma_f32_16x16x16_f16 (k = 4(l/16) + i), for checking the integer-operand
+// decomposition against the oracle without a GPU.  Test helper only.
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <vector>
+
+#include "kquant_frag.h"
+
+using namespace mqh;
+
+namespace {
+
+struct Tile {
+    int ntok, K;
+    std::vector<float> xh, xl;   // [ntok][K], the FP16 planes as floats
+    std::vector<float> sh, sl;   // [ntok][K/32] sub-block sums / 32, FP16 planes
+    std::vector<int> k;          // power-of-two exponent per token
+};
+
+Tile stage(const float* x, int ntok, int K, int split) {
+    Tile t;
+    t.ntok = ntok;
+    t.K = K;
+    t.xh.assign((size_t)ntok * K, 0.0f);
+    t.xl.assign((size_t)ntok * K, 0.0f);
+    t.sh.assign((size_t)ntok * K / 32, 0.0f);
+    t.sl.assign((size_t)ntok * K / 32, 0.0f);
+    t.k.assign(ntok, 0);
+    for (int j = 0; j < ntok; ++j) {
+        const float* row = x + (size_t)j * K;
+        float amax = 0.0f;
+        for (int c = 0; c < K; ++c) amax = fmaxf(amax, fabsf(row[c]));
+        const int k = frag_exp(amax);
+        t.k[j] = k;
+        for (int g = 0; g < K / 32; ++g) {
+            float s = 0.0f;
+            for (int c = 32 * g; c < 32 * g + 32; ++c) {
+                _Float16 hi, lo;
+                frag_split(row[c], k, hi, lo);
+                t.xh[(size_t)j * K + c] = (float)hi;
+                t.xl[(size_t)j * K + c] = split ? (float)lo : 0.0f;
+                s += ldexpf(row[c], -k);
+            }
+            _Float16 hi, lo;
+            frag_split(s, 5, hi, lo);
+            t.sh[(size_t)j * K / 32 + g] = (float)hi;
+            t.sl[(size_t)j * K / 32 + g] = (float)lo;
+        }
+    }
+    return t;
+}
+
+template <int T, int M>
+void step(const uint32_t* r, int row, int q, int b, const Tile& t, int split, std::vector<double>& P) {
+    h8_t a[2];
+    frag_step<T, M>(r, q, a);
+    const h8_t alo = frag_lo_operand<T>(a);
+    for (int j = 0; j < t.ntok; ++j) {
+        const size_t base = (size_t)j * t.K + 256 * b + 32 * M + 8 * q;
+        double s = 0.0;
+        for (int e = 0; e < 8; ++e) {
+            for (int n = 0; n < FragGeo<T>::NA; ++n) s += (double)(float)a[n][e] * t.xh[base + e];
+            if (split) s += (double)(float)alo[e] * t.xl[base + e];
+        }
+        P[row * 16 + j] += s;
+    }
+}
+
+template <int T>
+void gemm(const uint8_t* w, int K, const Tile& t, int split, float* out) {
+    constexpr int BB = block_bytes(T);
+    const int nb = K / 256;
+    std::vector<double> acc(16 * 16, 0.0);
+    for (int b = 0; b < nb; ++b) {
+        std::vector<double> P(16 * 16, 0.0), Mn(16 * 16, 0.0);
+        float d[16], dmin[16];
+        for (int l = 0; l < 64; ++l) {
+            const int row = l % 16, q = l / 16;
+            uint32_t r[FragGeo<T>::NW];
+            frag_load<T>(w + (size_t)row * nb * BB + (size_t)b * BB, q, r);
+            step<T, 0>(r, row, q, b, t, split, P);
+            step<T, 1>(r, row, q, b, t, split, P);
+            step<T, 2>(r, row, q, b, t, split, P);
+            step<T, 3>(r, row, q, b, t, split, P);
+            step<T, 4>(r, row, q, b, t, split, P);
+            step<T, 5>(r, row, q, b, t, split, P);
+            step<T, 6>(r, row, q, b, t, split, P);
+            step<T, 7>(r, row, q, b, t, split, P);
+            const uint32_t hdr = r[FragGeo<T>::HDR];
+            d[row] = frag_h2f(hdr);
+            dmin[row] = frag_h2f(hdr >> 16);
+            if constexpr (FragGeo<T>::MIN) {
+                const h4_t mm = frag_mins<T>(r, q);
+                for (int j = 0; j < t.ntok; ++j)
+                    for (int i = 0; i < 4; ++i) {
+                        const int kk = 4 * q + i;   // k < 8: high sums, k >= 8: low sums
+                        const float bx = kk < 8 ? t.sh[(size_t)j * K / 32 + 8 * b + kk] : t.sl[(size_t)j * K / 32 + 8 * b + kk - 8];
+                        Mn[row * 16 + j] += (double)(float)mm[i] * bx;
+                    }
+            }
+        }
+        for (int row = 0; row < 16; ++row)
+            for (int j = 0; j < t.ntok; ++j) {
+                acc[row * 16 + j] += (double)d[row] * P[row * 16 + j];
+                if constexpr (FragGeo<T>::MIN) acc[row * 16 + j] -= (double)dmin[row] * Mn[row * 16 + j];
+            }
+    }
+    for (int j = 0; j < t.ntok; ++j)
+        for (int row = 0; row < 16; ++row) out[(size_t)j * 16 + row] = (float)ldexp(acc[row * 16 + j], t.k[j]);
+}
+
+}  // namespace
+
+// out[tok][row] = sum_c W[row][c] x[tok][c] for 16 quantized rows (K columns)
+// and ntok <= 16 FP32 token rows, computed from the kernel's operands.  split:
+// 1 = high and low FP16 planes of x, 0 = high plane only (BF16 inputs).
+extern "C" void mqh_cpu_frag_gemm(int type, const uint8_t* w, int K, const float* x, int ntok, int split, float* out) {
+    const Tile t = stage(x, ntok, K, split);
+    switch (type) {
+        case T_Q4_K: gemm<T_Q4_K>(w, K, t, split, out); break;
+        case T_Q5_K: gemm<T_Q5_K>(w, K, t, split, out); break;
+        case T_Q6_K: gemm<T_Q6_K>(w, K, t, split, out); break;
+        default: gemm<T_Q3_K>(w, K, t, split, out); break;
+    }
+}

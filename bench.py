@@ -202,6 +202,335 @@ def kernel_times(runner, layers, X, IDS, WS, Y, reps: int) -> dict:
             "a_us_median": float(np.median(a)), "b_us_median": float(np.median(b))}
 
 
+# ---------------------------------------------------------------- other workloads
+
+CPU_THREADS = 16   # the GPU box's host-CPU share per GPU
+DEQ_TYPES = (11, 12, 14, 8)
+
+
+def _graph(fn, dev):
+    """Capture fn() (already run once eagerly) as a graph; return its replay."""
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(dev)
+    cap.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(cap):
+        fn()
+    torch.cuda.current_stream(dev).wait_stream(cap)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=cap):
+        fn()
+    return g.replay
+
+
+def _time(fn, reps: int) -> float:
+    """ms per call of fn over reps calls, after one warm call."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def _kernel_pair_times(calls, reps: int) -> dict:
+    """Average duration of the two GEMM kernels (A: gate/up, B: down) of each
+    call in calls (run eagerly reps times each), from runtime HIP events."""
+    import ctypes as C
+
+    import torch
+
+    from flash_moe_hip import _lib
+
+    lib, rt = _lib.load(), _hip_runtime()
+    n = reps * len(calls)
+    ev = []
+    for _ in range(4 * n):
+        h = C.c_void_p()
+        if rt.hipEventCreate(C.byref(h)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        ev.append(h)
+    torch.cuda.synchronize()
+    for i in range(n):
+        _lib.check(lib.mqh_profile_next_decode(ev[4 * i], ev[4 * i + 1], ev[4 * i + 2], ev[4 * i + 3]),
+                   "mqh_profile_next_decode")
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+
+    def us(a, b):
+        v = C.c_float()
+        if rt.hipEventElapsedTime(C.byref(v), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return v.value * 1e3
+
+    a = [us(ev[4 * i], ev[4 * i + 1]) for i in range(n)]
+    b = [us(ev[4 * i + 2], ev[4 * i + 3]) for i in range(n)]
+    for h in ev:
+        rt.hipEventDestroy(h)
+    return {"a_us": float(np.mean(a)), "b_us": float(np.mean(b)), "launches": n}
+
+
+def _hbm_roofline(name: str, nbytes: float, us: float) -> dict:
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+            "algorithmic_bytes": int(nbytes), "kernel_us": round(us, 3)}
+
+
+def _topk_routing(rng, T: int, k: int):
+    """top-k of N(0,1) logits per token, softmax over the selected k."""
+    logits = rng.standard_normal((T, E))
+    ids = np.argsort(-logits, axis=1)[:, :k]
+    sel = np.take_along_axis(logits, ids, 1)
+    w = np.exp(sel - sel.max(axis=1, keepdims=True))
+    return ids.astype(np.int32), (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def _oracle_tokens(layer, types, X, ids, ws, t_list):
+    """Oracle layer outputs (run_moe_sequence arithmetic) for tokens t_list."""
+    import oracle
+
+    sh = layer.host_shared()
+    gi = layer.shared.gate_inp.cpu().numpy()
+    out = {}
+    for t in t_list:
+        x = X[t]
+        outs = [oracle.expert_forward(layer.host_expert(int(e)), types, x, H, I, 0) for e in ids[t]]
+        gate = oracle._sigmoid(np.float32(x @ gi).reshape(()))
+        sh_out = (gate * oracle.expert_forward(sh, layer.shared.types, x, H, I, 0)).astype(np.float32)
+        out[t] = oracle.combine(outs, [float(v) for v in ws[t]], sh_out)
+    return out
+
+
+def _cpu_pairs(jobs, seconds: float, workers: int):
+    """Run oracle expert calls (types, bytes, x) on `workers` threads for about
+    `seconds`; returns (calls, elapsed)."""
+    import oracle
+
+    oracle.lib()
+    calls, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(workers) as pool:
+        while time.perf_counter() - t0 < seconds:
+            batch = [jobs[(calls + i) % len(jobs)] for i in range(4 * workers)]
+            list(pool.map(lambda j: oracle.expert_forward(j[1], j[0], j[2], H, I, 0), batch))
+            calls += len(batch)
+    return calls, time.perf_counter() - t0
+
+
+def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> dict:
+    """16 tokens through one all-Q3_K layer, top-8 of N(0,1) logits + shared;
+    n_layers independently seeded layers rotated.  Both kernel families are
+    timed; the reported value is the faster one."""
+    import torch
+
+    from flash_moe_hip.layer_store import ExpertLayer
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    T, types = 16, {"gate": 11, "up": 11, "down": 11}
+    layers = [ExpertLayer.synthetic(types, E, H, I, seed=7000 + 1000 * l, shared_types=types,
+                                    shared_intermediate=I, gate_inp=True, device=dev) for l in range(n_layers)]
+    rng = np.random.default_rng(4)
+    Xh, IDh, WSh = [], [], []
+    for _ in range(n_layers):
+        Xh.append(rng.standard_normal((T, H)).astype(np.float32))
+        i, w = _topk_routing(rng, T, K)
+        IDh.append(i)
+        WSh.append(w)
+    X = [torch.from_numpy(v).to(dev) for v in Xh]
+    IDS = [torch.from_numpy(v).to(dev) for v in IDh]
+    WS = [torch.from_numpy(v).to(dev) for v in WSh]
+    Y = torch.empty((T, H), dtype=torch.float32, device=dev)
+    U = [len(np.unique(v)) for v in IDh]
+    nbytes = float(np.mean([(u + 1) * layers[0].bytes_per_expert() for u in U]))
+    runner = MoeRunner(dev)
+    paths = {
+        "prefill": lambda l: runner.prefill(layers[l], X[l], IDS[l], WS[l], y=Y),
+        "decode": lambda l: runner.decode(layers[l], X[l], IDS[l], WS[l], y=Y),
+    }
+    res = {}
+    want = _oracle_tokens(layers[0], types, Xh[0], IDh[0], WSh[0], [0, 7, 15])
+    import oracle
+
+    for name, call in paths.items():
+        call(0)
+        torch.cuda.synchronize()
+        assert runner.status() == 0
+        got = Y.cpu().numpy()
+        err = max(oracle.max_relative_error(got[t], want[t]) for t in want)
+        replay = _graph(lambda: [call(l) for l in range(n_layers)], dev)
+        ms = _time(replay, max(1, steps // n_layers)) / n_layers
+        kern = _kernel_pair_times([lambda l=l: call(l) for l in range(n_layers)], 2)
+        res[name] = {"us_per_layer": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "parity_max_rel_err": float(f"{err:.3e}"),
+                     "kernels_us": {"A": round(kern["a_us"], 2), "B": round(kern["b_us"], 2)}}
+        log(f"batched decode via {name}: {ms * 1e3:.2f} us/layer, parity {err:.2e}")
+    best = min(res, key=lambda k: res[k]["us_per_layer"])
+    kb = res[best]["kernels_us"]
+    frac_a = (layers[0].expert_bytes("gate") + layers[0].expert_bytes("up")) / layers[0].bytes_per_expert()
+    dom = "A" if kb["A"] >= kb["B"] else "B"
+    kname = {"prefill": {"A": "k_prefill_gate_up", "B": "k_prefill_down"},
+             "decode": {"A": "k_fast_gate_up", "B": "k_fast_down"}}[best][dom]
+    out = {
+        "workload": f"batched decode: {T} tokens, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
+                    f"logits + shared, all Q3_K, {n_layers} resident layers rotated",
+        "metric": "quant-weight GB/s per layer-step (weights of the U distinct routed experts + shared)",
+        "value": res[best]["gbs"], "unit": "GB/s", "us_per_layer": res[best]["us_per_layer"],
+        "path": best, "paths": res, "distinct_experts_mean": float(np.mean(U)),
+        "weight_bytes_per_step": int(nbytes),
+        "roofline": _hbm_roofline(kname, nbytes * (frac_a if dom == "A" else 1 - frac_a), kb[dom]),
+    }
+    if cpu_seconds > 0:
+        L0 = layers[0]
+        jobs = [(types, L0.host_expert(int(e)), Xh[0][t]) for t in range(T) for e in IDh[0][t]]
+        jobs += [(types, L0.host_shared(), Xh[0][t]) for t in range(T)]
+        calls, dt = _cpu_pairs(jobs, cpu_seconds, CPU_THREADS)
+        per_step = dt / calls * T * (K + 1)
+        out["cpu_baseline"] = {"value": round(nbytes / per_step / 1e9, 3), "unit": "GB/s", "cores": CPU_THREADS,
+                               "kind": "port", "us_per_layer": round(per_step * 1e6, 1),
+                               "sample": f"{calls} per-token expert calls (16 tokens x 9 per step), {dt:.1f} s"}
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
+    """128-token BF16 prompt through one layer (gate/up Q4_K, down Q6_K, top-8 of
+    N(0,1) logits + shared), n_layers seeded layers rotated."""
+    import torch
+
+    from flash_moe_hip.layer_store import ExpertLayer
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    T = 128
+    layers = [ExpertLayer.synthetic(TYPES, E, H, I, seed=9000 + 1000 * l, shared_types=TYPES,
+                                    shared_intermediate=I, gate_inp=True, device=dev) for l in range(n_layers)]
+    rng = np.random.default_rng(5)
+    gen = torch.Generator().manual_seed(5)
+    Xh, IDh, WSh = [], [], []
+    for _ in range(n_layers):
+        x = torch.randn((T, H), generator=gen).to(torch.bfloat16)
+        Xh.append(x)
+        i, w = _topk_routing(rng, T, K)
+        IDh.append(i)
+        WSh.append(w)
+    X = [v.to(dev) for v in Xh]
+    IDS = [torch.from_numpy(v).to(dev) for v in IDh]
+    WS = [torch.from_numpy(v).to(dev) for v in WSh]
+    Y = torch.empty((T, H), dtype=torch.float32, device=dev)
+    runner = MoeRunner(dev)
+    call = lambda l: runner.prefill(layers[l], X[l], IDS[l], WS[l], y=Y)
+    call(0)
+    torch.cuda.synchronize()
+    assert runner.status() == 0
+    import oracle
+
+    xf = Xh[0].float().numpy()
+    want = _oracle_tokens(layers[0], TYPES, xf, IDh[0], WSh[0], [0, 64, 127])
+    got = Y.cpu().numpy()
+    err = max(oracle.max_relative_error(got[t], want[t]) for t in want)
+    replay = _graph(lambda: [call(l) for l in range(n_layers)], dev)
+    ms = _time(replay, reps) / n_layers
+    kern = _kernel_pair_times([lambda l=l: call(l) for l in range(n_layers)], 3)
+    U = [len(np.unique(v)) for v in IDh]
+    flop = 2.0 * T * (K + 1) * 3 * H * I
+    nbytes = float(np.mean([(u + 1) * layers[0].bytes_per_expert() for u in U]))
+    gu = float(np.mean([(u + 1) * (layers[0].expert_bytes("gate") + layers[0].expert_bytes("up")) for u in U]))
+    tflops = flop / (ms * 1e-3) / 1e12
+    dom = "A" if kern["a_us"] >= kern["b_us"] else "B"
+    roof = _hbm_roofline("k_prefill_gate_up" if dom == "A" else "k_prefill_down",
+                         gu if dom == "A" else nbytes - gu, kern["a_us"] if dom == "A" else kern["b_us"])
+    log(f"prefill: {ms * 1e3:.1f} us/layer, {tflops:.1f} TFLOP/s, parity {err:.2e}; "
+        f"gate/up {kern['a_us']:.1f} us, down {kern['b_us']:.1f} us")
+    out = {
+        "workload": f"prefill: {T}-token BF16 prompt, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
+                    f"logits + shared, gate/up Q4_K, down Q6_K, {n_layers} resident layers rotated",
+        "metric": "prefill TFLOP/s (useful FLOPs: 1152 pairs x 6,291,456)", "value": round(tflops, 2),
+        "unit": "TFLOP/s", "us_per_layer": round(ms * 1e3, 2), "flop_per_layer": int(flop),
+        "weight_bytes_per_layer": int(nbytes), "weight_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "distinct_experts_mean": float(np.mean(U)), "parity_max_rel_err": float(f"{err:.3e}"),
+        "kernels_us": {"k_prefill_gate_up": round(kern["a_us"], 2), "k_prefill_down": round(kern["b_us"], 2)},
+        "roofline": roof,
+        "mfma_ceiling": {"peak_tflops_fp16_dense": 2500.0, "frac": round(tflops / 2500.0, 5)},
+    }
+    if cpu_seconds > 0:
+        L0 = layers[0]
+        jobs = [(TYPES, L0.host_expert(int(e)), xf[t]) for t in range(0, T, 8) for e in IDh[0][t]]
+        calls, dt = _cpu_pairs(jobs, cpu_seconds, CPU_THREADS)
+        per_layer = dt / calls * T * (K + 1)
+        out["cpu_baseline"] = {"value": round(flop / per_layer / 1e12, 5), "unit": "TFLOP/s",
+                               "cores": CPU_THREADS, "kind": "port", "us_per_layer": round(per_layer * 1e6, 1),
+                               "sample": f"{calls} (token, expert) calls of the native-kernel port, {dt:.1f} s; "
+                                         "the reference prefill (OpenVINO) is not available"}
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_dequant(dev, reps: int, cpu_seconds: float) -> dict:
+    """256 experts x 3 matrices (gate/up [512x2048], down [2048x512]) to FP16,
+    once per type; GB/s over quantized bytes read + FP16 bytes written."""
+    import torch
+
+    import oracle
+    from flash_moe_hip.dequant import dequant_device
+    from flash_moe_hip.quant_types import block_info
+    from flash_moe_hip.synthetic import torch_random_stack
+
+    n = 3 * E * H * I
+    out = torch.empty(n, dtype=torch.float16, device=dev)
+    res = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    for t in DEQ_TYPES:
+        src = torch_random_stack(t, 3 * E, I, H, generator=g, device=dev)
+        dequant_device(src, t, n, out=out)
+        torch.cuda.synchronize()
+        # bit-exact check on a sample of blocks
+        bs, pb = block_info(t)
+        nb = 4096
+        sample = src[: nb * pb].cpu().numpy()
+        want = oracle.dequant(t, sample, nb * bs, want_f16=True)
+        ok = bool(np.array_equal(out[: nb * bs].cpu().numpy().view(np.uint16), np.asarray(want).view(np.uint16)))
+        ms = _time(lambda: dequant_device(src, t, n, out=out), reps)
+        nbytes = src.numel() + 2 * n
+        res[str(t)] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 1), "bytes": nbytes,
+                       "bit_exact_sample": ok, "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"dequant type {t}: {ms * 1e3:.1f} us, {res[str(t)]['gbs']} GB/s, bit-exact sample {ok}")
+        del src
+    best = max(res, key=lambda k: res[k]["gbs"])
+    worst = min(res, key=lambda k: res[k]["gbs"])
+    out_d = {
+        "workload": "dequantization to FP16: 256 experts x 3 matrices ([512x2048] gate, up, [2048x512] down), "
+                    "types Q3_K (11), Q4_K (12), Q6_K (14), Q8_0 (8)",
+        "metric": "GB/s (quantized bytes read + FP16 bytes written)", "per_type": res,
+        "value": res[worst]["gbs"], "unit": "GB/s",
+        "roofline": _hbm_roofline("k_dequant (slowest type %s)" % worst, res[worst]["bytes"], res[worst]["us"]),
+    }
+    if cpu_seconds > 0:
+        t = 12
+        src = torch_random_stack(t, 64, I, H, generator=g, device=dev).cpu().numpy()
+        mats = src.reshape(64, -1)
+        oracle.lib()
+        done, t0 = 0, time.perf_counter()
+        with ThreadPoolExecutor(CPU_THREADS) as pool:
+            while time.perf_counter() - t0 < cpu_seconds:
+                list(pool.map(lambda m: oracle.dequant(t, m, H * I, want_f16=True), mats))
+                done += len(mats)
+        dt = time.perf_counter() - t0
+        per = (mats.shape[1] + 2 * H * I) * done / dt
+        out_d["cpu_baseline"] = {"value": round(per / 1e9, 3), "unit": "GB/s", "cores": CPU_THREADS, "kind": "port",
+                                 "sample": f"{done} Q4_K matrices [512x2048] -> FP16 in {dt:.1f} s"}
+    del out
+    torch.cuda.empty_cache()
+    return out_d
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,6 +540,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch every step from Python instead of a graph")
+    ap.add_argument("--only-decode", action="store_true", help="skip the batched-decode, prefill and dequant lines")
+    ap.add_argument("--extra-cpu-seconds", type=float, default=4.0)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -262,6 +593,7 @@ def main() -> int:
 
     reps_w = max(1, args.warmup // args.layers)
     reps = max(1, args.steps // args.layers)
+    graph = None
     if args.eager:
         run_sweep = sweep
     else:
@@ -332,6 +664,15 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle, 4 threads)")
         result["cpu_baseline"] = cpu_baseline(layers, xs, ids, ws, args.cpu_seconds)
+    if not args.only_decode:
+        del layers, graph
+        torch.cuda.empty_cache()
+        cpu_s = 0.0 if args.no_cpu_baseline else args.extra_cpu_seconds
+        result["workloads"] = {
+            "batched_decode": bench_batched_decode(dev, args.layers, args.steps // 4, cpu_s),
+            "prefill": bench_prefill(dev, 8, 20, cpu_s),
+            "dequant": bench_dequant(dev, 10, cpu_s),
+        }
     print(json.dumps(result), flush=True)
     return 0
 

@@ -31,9 +31,33 @@ namespace mqh {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int PF_ROWS = 64;      // weight rows per workgroup: 4 waves x 16
-constexpr int PF_RING = 2;       // super-blocks of loads in flight per lane while one is computed
+constexpr int PF_WAVES = 8;      // waves per workgroup of the GEMM kernels
+constexpr int PF_ROWS_GU = 64;   // gate/up rows per workgroup: 4 waves on gate, 4 on up
+constexpr int PF_ROWS_DOWN = 128; // down rows per workgroup chunk: 8 waves x 16
+#ifndef PF_CPW_GU
+#define PF_CPW_GU 1              // gate/up row chunks per workgroup (one continuous load ring)
+#endif
+#ifndef PF_CPW_DOWN
+#define PF_CPW_DOWN 1            // down row chunks per workgroup
+#endif
+constexpr int PF_RING = 4;       // register ring of super-blocks per lane (R - 1 in flight)
 constexpr int PF_PAD = 8;        // LDS row padding (halves)
+
+// Waves per SIMD that the LDS footprint of one workgroup (PF_WAVES waves)
+// admits; the GEMM kernels ask the register allocator for that occupancy.
+constexpr int pf_lds_bytes(int K, bool split) {
+    return 2 * PREFILL_TILE * (K + PF_PAD) * (split ? 2 : 1) + PREFILL_TILE * (K / 256) * 32 + 2048;
+}
+constexpr int pf_occupancy(int lds_bytes) {
+    return (160 * 1024 / lds_bytes) * PF_WAVES / 4 < 8 ? (160 * 1024 / lds_bytes) * PF_WAVES / 4 : 8;
+}
+
+#ifndef PF_OCC_GU
+#define PF_OCC_GU
+#endif
+#ifndef PF_OCC_DOWN
+#define PF_OCC_DOWN
+#endif
 
 template <int... Ms, class F>
 __device__ __forceinline__ void pf_unroll(std::integer_sequence<int, Ms...>, F&& f) {
@@ -67,13 +91,14 @@ __device__ __forceinline__ float pf_wave_sum(float v) {
 //
 // One wave stages token row `row` of src (K values, FP32 or BF16) as LDS column
 // j of the B operand: high plane xh[j][K + PF_PAD], low plane xl (SPLIT only),
-// and the 32-column sub-block sums / 32 as [j][block][hi 0..7 | lo 0..7] in xs.
+// and the 32-column sub-block sums / 32 as [block][j][hi 0..7 | lo 0..7] in xs
+// (block-major, so the 16 token columns of one block sit in distinct banks).
 // A lane owns 8 consecutive values per 512-column pass.  With gvec set, the
 // wave also returns x_row . gvec (FP32, unscaled) in every lane.
 template <int K, bool BF16, bool SPLIT>
 __device__ __forceinline__ float pf_stage(const void* src, int64_t row, int j, _Float16* xh, _Float16* xl,
                                           _Float16* xs, int* s_exp, const float* gvec) {
-    constexpr int NIT = K >= 512 ? K / 512 : 1, KP = K + PF_PAD, NB = K / 256;
+    constexpr int NIT = K >= 512 ? K / 512 : 1, KP = K + PF_PAD;
     const int lane = threadIdx.x & 63;
     float v[NIT][8];
     float amax = 0.0f, gdot = 0.0f;
@@ -132,8 +157,8 @@ __device__ __forceinline__ float pf_stage(const void* src, int64_t row, int j, _
                 const int sb = c >> 5;   // sub-block: block sb / 8, slot sb % 8
                 _Float16 h, l;
                 frag_split(s, 5, h, l);
-                xs[(j * NB + (sb >> 3)) * 16 + (sb & 7)] = h;
-                xs[(j * NB + (sb >> 3)) * 16 + 8 + (sb & 7)] = l;
+                xs[((sb >> 3) * PREFILL_TILE + j) * 16 + (sb & 7)] = h;
+                xs[((sb >> 3) * PREFILL_TILE + j) * 16 + 8 + (sb & 7)] = l;
             }
         }
     }
@@ -143,83 +168,115 @@ __device__ __forceinline__ float pf_stage(const void* src, int64_t row, int j, _
 
 // ------------------------------------------------------------ the GEMM core
 //
-// acc[mt] += W_mt[16 rows of this wave] x B^T over K = NB * 256 columns for NMAT
-// weight matrices sharing the B operand.  prefetch() loads the first blocks
-// before the caller stages the tokens, so that the two overlap.  D layout:
-// lane l holds rows 4(l/16) + i, token column l % 16.
-template <int T, int NMAT, int NB>
+// A wave accumulates W[16 rows] x B^T over K = NB * 256 columns for NMAT weight
+// matrices sharing the B operand, for CPW row chunks in turn (the chunk stride
+// is given in bytes); one register ring of super-blocks runs across the chunks,
+// so the loads of the next chunk are in flight while one ends.  prefetch()
+// loads the first blocks before the caller stages the tokens, so that the two
+// overlap.  D layout: lane l holds rows 4(l/16) + i, token column l % 16.
+template <int T, int NMAT, int NB, int CPW>
 struct PfRows {
-    static constexpr int NW = FragGeo<T>::NW, BB = block_bytes(T);
-    static constexpr int D = NB < PF_RING ? NB : PF_RING;
-    static_assert(NB % D == 0, "blocks per row must be a multiple of the ring size");
-    uint32_t raw[D][NMAT][NW];
+    static constexpr int NW = FragGeo<T>::NW, BB = block_bytes(T), NBT = NB * CPW;
+    // R ring slots: block b lives in slot b % R; while block b is computed,
+    // blocks b+1 .. b+R-1 are in flight (all of them for short rows)
+    static constexpr bool UNROLLED = NBT <= PF_RING;
+    static constexpr int R = UNROLLED ? NBT + 1 : PF_RING;
+    static_assert(UNROLLED || NBT % R == 0, "blocks per wave must be a multiple of the ring size");
+    uint32_t raw[R][NMAT][NW];
+    const uint8_t* W[NMAT];
+    int64_t chunk_stride;
+    int q;
 
-    __device__ __forceinline__ void load(const uint8_t* const (&W)[NMAT], int b, int q, uint32_t (&dst)[NMAT][NW]) {
+    __device__ __forceinline__ void load(int b, uint32_t (&dst)[NMAT][NW]) {
+        const int64_t off = (int64_t)(b / NB) * chunk_stride + (b % NB) * BB;
 #pragma unroll
-        for (int mt = 0; mt < NMAT; ++mt) frag_load<T>(W[mt] + b * BB, q, dst[mt]);
+        for (int mt = 0; mt < NMAT; ++mt) frag_load<T>(W[mt] + off, q, dst[mt]);
     }
 
-    __device__ __forceinline__ void prefetch(const uint8_t* const (&W)[NMAT], int q) {
+    __device__ __forceinline__ void prefetch() {
 #pragma unroll
-        for (int b = 0; b < D; ++b) load(W, b, q, raw[b]);
+        for (int b = 0; b < (NBT < R - 1 ? NBT : R - 1); ++b) load(b, raw[b]);
     }
 
+    // one super-block (block kb of its row): P = sum over its 8 steps of the exact
+    // integer operands times the token planes, then acc += d * P (- dmin * min term)
     template <bool SPLIT>
-    __device__ __forceinline__ void run(const uint8_t* const (&W)[NMAT], int q, const _Float16* xh, const _Float16* xl,
-                                        const _Float16* xs, f32x4 (&acc)[NMAT]) {
+    __device__ __forceinline__ void block(const uint32_t (&cur)[NMAT][NW], int kb, const _Float16* xh,
+                                          const _Float16* xl, const _Float16* xs, f32x4 (&acc)[NMAT]) {
         constexpr int KP = NB * 256 + PF_PAD;
         const int lane = threadIdx.x & 63, tok = lane & 15;
-        // a runtime loop over groups of D blocks keeps one block's operands live at a
-        // time; the refill of a ring slot is unconditional (the tail re-reads the
-        // last block, in bounds and unused)
-#pragma unroll 1
-        for (int b0 = 0; b0 < NB; b0 += D)
+        const int brow = tok * KP + kb * 256 + frag_lane_col<T>((q + 3) & 3);
+        f32x4 P[NMAT];
+        FragPrep<T> sp[NMAT];
 #pragma unroll
-        for (int bi = 0; bi < D; ++bi) {
-            const int b = b0 + bi;
-            uint32_t cur[NMAT][NW];
+        for (int mt = 0; mt < NMAT; ++mt) {
+            P[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            frag_prep<T>(cur[mt], q, sp[mt]);
+        }
+        pf_unroll(std::make_integer_sequence<int, 8>{}, [&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+            const int off = brow + frag_col<T, m>();
+            const h8_t bh = *(const h8_t*)(xh + off);
+            h8_t bl;
+            if constexpr (SPLIT) bl = *(const h8_t*)(xl + off);
 #pragma unroll
-            for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-                for (int i = 0; i < NW; ++i) cur[mt][i] = raw[bi][mt][i];
-            load(W, min(b + D, NB - 1), q, raw[bi]);
-
-            f32x4 P[NMAT];
-#pragma unroll
-            for (int mt = 0; mt < NMAT; ++mt) P[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            pf_unroll(std::make_integer_sequence<int, 8>{}, [&](auto mc) {
-                constexpr int m = decltype(mc)::value;
-                const int off = tok * KP + b * 256 + 32 * m + 8 * q;
-                const h8_t bh = *(const h8_t*)(xh + off);
-                h8_t bl;
-                if constexpr (SPLIT) bl = *(const h8_t*)(xl + off);
-#pragma unroll
-                for (int mt = 0; mt < NMAT; ++mt) {
-                    h8_t a[2];
-                    frag_step<T, m>(cur[mt], q, a);
-                    P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], bh, P[mt], 0, 0, 0);
-                    if constexpr (FragGeo<T>::NA == 2) P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], bh, P[mt], 0, 0, 0);
-                    if constexpr (SPLIT)
-                        P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag_lo_operand<T>(a), bl, P[mt], 0, 0, 0);
-                }
-            });
-            f32x4 Mn[NMAT];
-            if constexpr (FragGeo<T>::MIN) {
-                const h4_t bs = *(const h4_t*)(xs + (tok * NB + b) * 16 + 4 * q);
-#pragma unroll
-                for (int mt = 0; mt < NMAT; ++mt)
-                    Mn[mt] = __builtin_amdgcn_mfma_f32_16x16x16f16(frag_mins<T>(cur[mt], q), bs,
-                                                                   f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            for (int mt = 0; mt < NMAT; ++mt) {
+                h8_t a[2];
+                frag_step<T, m>(cur[mt], sp[mt], q, a);
+                P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], bh, P[mt], 0, 0, 0);
+                if constexpr (FragGeo<T>::NA == 2) P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], bh, P[mt], 0, 0, 0);
+                if constexpr (SPLIT)
+                    P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag_lo_operand<T>(a), bl, P[mt], 0, 0, 0);
             }
-            // d (and dmin) of D row 4q + i live in the header word of A lane 4q + i
+        });
+        f32x4 Mn[NMAT];
+        if constexpr (FragGeo<T>::MIN) {
+            const h4_t bs = *(const h4_t*)(xs + (kb * PREFILL_TILE + tok) * 16 + 4 * q);
 #pragma unroll
             for (int mt = 0; mt < NMAT; ++mt)
+                Mn[mt] = __builtin_amdgcn_mfma_f32_16x16x16f16(frag_mins<T>(cur[mt], q), bs,
+                                                               f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        }
+        // d (and dmin) of D row 4q + i live in the header word of A lane 4q + i
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t hdr = (uint32_t)__shfl((int)cur[mt][FragGeo<T>::HDR], 4 * q + i, 64);
-                    acc[mt][i] = fmaf(frag_h2f(hdr), P[mt][i], acc[mt][i]);
-                    if constexpr (FragGeo<T>::MIN) acc[mt][i] = fmaf(-frag_h2f(hdr >> 16), Mn[mt][i], acc[mt][i]);
-                }
+        for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t hdr = (uint32_t)__shfl((int)cur[mt][FragGeo<T>::HDR], 4 * q + i, 64);
+                acc[mt][i] = fmaf(frag_d<T>(hdr), P[mt][i], acc[mt][i]);
+                if constexpr (FragGeo<T>::MIN) acc[mt][i] = fmaf(-frag_dmin(hdr), Mn[mt][i], acc[mt][i]);
+            }
+    }
+
+    // All NBT blocks; end(c, acc) runs after the last block of chunk c, with the
+    // ring already loading chunk c + 1, and must leave acc zeroed.  The refill
+    // of block b + R - 1 goes to the slot block b - 1 has just released, ahead
+    // of block b's arithmetic (the sched barrier stops the scheduler from
+    // sinking it to the end of the loop body, which would expose the memory
+    // latency once per iteration).
+    template <bool SPLIT, class End>
+    __device__ __forceinline__ void run(const _Float16* xh, const _Float16* xl, const _Float16* xs,
+                                        f32x4 (&acc)[NMAT], End&& end) {
+        if constexpr (UNROLLED) {
+#pragma unroll
+            for (int b = 0; b < NBT; ++b) {
+                if (b + R - 1 < NBT) load(b + R - 1, raw[(b + R - 1) % R]);
+                __builtin_amdgcn_sched_barrier(0);
+                block<SPLIT>(raw[b % R], b % NB, xh, xl, xs, acc);
+                if ((b + 1) % NB == 0) end(b / NB, acc);
+            }
+        } else {
+#pragma unroll 1
+            for (int b0 = 0; b0 < NBT; b0 += R)
+#pragma unroll
+            for (int bi = 0; bi < R; ++bi) {
+                const int b = b0 + bi;
+                // the tail re-reads the last block (in bounds, unused)
+                load(min(b + R - 1, NBT - 1), raw[(bi + R - 1) % R]);
+                __builtin_amdgcn_sched_barrier(0);
+                block<SPLIT>(raw[bi], b % NB, xh, xl, xs, acc);
+                if ((b + 1) % NB == 0) end(b / NB, acc);
+            }
         }
     }
 };
@@ -290,57 +347,67 @@ __global__ __launch_bounds__(1024) void k_prefill_route(PrefillParams p) {
 
 // ------------------------------------------------------------ P1
 
-template <int GT, int NBH, bool XBF16>
-__global__ __launch_bounds__(256) void k_prefill_gate_up(PrefillParams p) {
+template <int GT, int NBH, bool XBF16, int CPW>
+__global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(PrefillParams p) {
     constexpr int H = NBH * 256, KP = H + PF_PAD;
     constexpr bool SPLIT = !XBF16;   // BF16 tokens are exact in the high plane
     __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
     __shared__ __attribute__((aligned(16))) _Float16 xl[SPLIT ? PREFILL_TILE * KP : 8];
     __shared__ __attribute__((aligned(16))) _Float16 xs[PREFILL_TILE * NBH * 16];
+    __shared__ __attribute__((aligned(16))) float s_up[PF_WAVES / 2][64][4];
     __shared__ int s_exp[PREFILL_TILE];
     const int tile = blockIdx.y;
     if (tile >= *p.n_tiles) return;
     const int4 td = pf_tile(p, tile);
     const int e = td.x, first = td.y, cnt = td.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
-    const int r0 = blockIdx.x * PF_ROWS + wave * 16;
+    // waves 0..3: gate rows, waves 4..7: the same up rows; CPW chunks of 64 rows
+    const int mat = wave / (PF_WAVES / 2), wsub = wave % (PF_WAVES / 2);
+    const int rbase = blockIdx.x * PF_ROWS_GU * CPW + wsub * 16;
     const int64_t row_bytes = (int64_t)NBH * block_bytes(GT);
-    const uint8_t* W[2];
-    if (e < 0) { W[0] = p.sh_gate; W[1] = p.sh_up; }
-    else { W[0] = p.gate + (int64_t)e * p.gate_eb; W[1] = p.up + (int64_t)e * p.up_eb; }
-    W[0] += (int64_t)(r0 + (lane & 15)) * row_bytes;
-    W[1] += (int64_t)(r0 + (lane & 15)) * row_bytes;
 
-    PfRows<GT, 2, NBH> g;
-    g.prefetch(W, q);
+    PfRows<GT, 1, NBH, CPW> g;
+    if (e < 0) g.W[0] = mat ? p.sh_up : p.sh_gate;
+    else g.W[0] = mat ? p.up + (int64_t)e * p.up_eb : p.gate + (int64_t)e * p.gate_eb;
+    g.W[0] += (int64_t)(rbase + (lane & 15)) * row_bytes;
+    g.chunk_stride = PF_ROWS_GU * row_bytes;
+    g.q = q;
+    g.prefetch();
     const bool gate_out = e < 0 && blockIdx.x == 0;
-    for (int j = wave; j < cnt; j += 4) {
+    for (int j = wave; j < cnt; j += PF_WAVES) {
         const int t = p.pair_tok[first + j];
         const float gd = pf_stage<H, XBF16, SPLIT>(p.x, t, j, xh, xl, xs, s_exp, gate_out ? p.sh_gate_inp : nullptr);
         if (gate_out && lane == 0) p.sh_scale[t] = p.sh_gate_inp != nullptr ? pf_sigmoid(gd) : 1.0f;
     }
     __syncthreads();
 
-    f32x4 acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-    g.template run<SPLIT>(W, q, xh, xl, xs, acc);
-
-    // columns at or past cnt hold stale LDS; their results are never stored
     const int col = lane & 15;
-    if (col < cnt) {
-        const float sc = ldexpf(1.0f, s_exp[col]);
-        float4 a;
-        a.x = pf_silu_mul(acc[0][0] * sc, acc[1][0] * sc);
-        a.y = pf_silu_mul(acc[0][1] * sc, acc[1][1] * sc);
-        a.z = pf_silu_mul(acc[0][2] * sc, acc[1][2] * sc);
-        a.w = pf_silu_mul(acc[0][3] * sc, acc[1][3] * sc);
-        *(float4*)(p.act + (int64_t)(first + col) * p.inter + r0 + 4 * q) = a;
-    }
+    const float sc = col < cnt ? ldexpf(1.0f, s_exp[col]) : 0.0f;
+    f32x4 acc[1] = {{0, 0, 0, 0}};
+    g.template run<SPLIT>(xh, xl, xs, acc, [&](int c, f32x4 (&a)[1]) {
+        // the up waves hand their results to the gate waves of the same rows
+        // (same D layout, so no transposition); columns at or past cnt hold stale
+        // LDS and are never stored
+        if (mat) *(float4*)s_up[wsub][lane] = make_float4(a[0][0], a[0][1], a[0][2], a[0][3]);
+        __syncthreads();
+        if (!mat && col < cnt) {
+            const float4 u = *(const float4*)s_up[wsub][lane];
+            float4 o;
+            o.x = pf_silu_mul(a[0][0] * sc, u.x * sc);
+            o.y = pf_silu_mul(a[0][1] * sc, u.y * sc);
+            o.z = pf_silu_mul(a[0][2] * sc, u.z * sc);
+            o.w = pf_silu_mul(a[0][3] * sc, u.w * sc);
+            *(float4*)(p.act + (int64_t)(first + col) * p.inter + rbase + PF_ROWS_GU * c + 4 * q) = o;
+        }
+        __syncthreads();
+        a[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    });
 }
 
 // ------------------------------------------------------------ P2
 
-template <int DT, int NBI>
-__global__ __launch_bounds__(256) void k_prefill_down(PrefillParams p) {
+template <int DT, int NBI, int CPW>
+__global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(PrefillParams p) {
     constexpr int I = NBI * 256, KP = I + PF_PAD;
     __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
     __shared__ __attribute__((aligned(16))) _Float16 xl[PREFILL_TILE * KP];
@@ -351,24 +418,26 @@ __global__ __launch_bounds__(256) void k_prefill_down(PrefillParams p) {
     const int4 td = pf_tile(p, tile);
     const int e = td.x, first = td.y, cnt = td.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
-    const int r0 = blockIdx.x * PF_ROWS + wave * 16;
+    const int rbase = blockIdx.x * PF_ROWS_DOWN * CPW + wave * 16;
     const int64_t row_bytes = (int64_t)NBI * block_bytes(DT);
-    const uint8_t* W[1] = {(e < 0 ? p.sh_down : p.down + (int64_t)e * p.down_eb) + (int64_t)(r0 + (lane & 15)) * row_bytes};
 
-    PfRows<DT, 1, NBI> g;
-    g.prefetch(W, q);
-    for (int j = wave; j < cnt; j += 4) pf_stage<I, false, true>(p.act, first + j, j, xh, xl, xs, s_exp, nullptr);
+    PfRows<DT, 1, NBI, CPW> g;
+    g.W[0] = (e < 0 ? p.sh_down : p.down + (int64_t)e * p.down_eb) + (int64_t)(rbase + (lane & 15)) * row_bytes;
+    g.chunk_stride = PF_ROWS_DOWN * row_bytes;
+    g.q = q;
+    g.prefetch();
+    for (int j = wave; j < cnt; j += PF_WAVES) pf_stage<I, false, true>(p.act, first + j, j, xh, xl, xs, s_exp, nullptr);
     __syncthreads();
 
-    f32x4 acc[1] = {{0, 0, 0, 0}};
-    g.template run<true>(W, q, xh, xl, xs, acc);
-
     const int col = lane & 15;
-    if (col < cnt) {
-        const float sc = ldexpf(1.0f, s_exp[col]);
-        *(float4*)(p.ypair + (int64_t)(first + col) * p.hidden + r0 + 4 * q) =
-            make_float4(acc[0][0] * sc, acc[0][1] * sc, acc[0][2] * sc, acc[0][3] * sc);
-    }
+    const float sc = col < cnt ? ldexpf(1.0f, s_exp[col]) : 0.0f;
+    f32x4 acc[1] = {{0, 0, 0, 0}};
+    g.template run<true>(xh, xl, xs, acc, [&](int c, f32x4 (&a)[1]) {
+        if (col < cnt)
+            *(float4*)(p.ypair + (int64_t)(first + col) * p.hidden + rbase + PF_ROWS_DOWN * c + 4 * q) =
+                make_float4(a[0][0] * sc, a[0][1] * sc, a[0][2] * sc, a[0][3] * sc);
+        a[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    });
 }
 
 // ------------------------------------------------------------ P3
@@ -423,40 +492,56 @@ PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden,
 // a kernel launch, bracketed by the profiling events when they are armed
 #define PF_LAUNCH(kernel, grid, armed, e0, e1, s, p)                                    \
     do {                                                                                \
-        if (armed) hipExtLaunchKernelGGL(kernel, grid, dim3(256), 0, s, e0, e1, 0, p); \
-        else hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, p);                      \
+        if (armed) hipExtLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, e0, e1, 0, p); \
+        else hipLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, p);                      \
     } while (0)
 
-template <int GT, int NBH>
+// chunks per workgroup: gate/up rows CPW x 64, down rows CPW x 128
+constexpr int pf_cpw_gu(int inter) { return inter / PF_ROWS_GU < PF_CPW_GU ? inter / PF_ROWS_GU : PF_CPW_GU; }
+constexpr int pf_cpw_down(int hidden) { return hidden / PF_ROWS_DOWN < PF_CPW_DOWN ? hidden / PF_ROWS_DOWN : PF_CPW_DOWN; }
+
+template <int GT, int NBH, int CPW>
 static void launch_p1(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
-    const dim3 grid(p.inter / PF_ROWS, p.max_tiles);
-    if (p.x_bf16) PF_LAUNCH((k_prefill_gate_up<GT, NBH, true>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p);
-    else PF_LAUNCH((k_prefill_gate_up<GT, NBH, false>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p);
+    const dim3 grid(p.inter / (PF_ROWS_GU * CPW), p.max_tiles);
+    if (p.x_bf16) PF_LAUNCH((k_prefill_gate_up<GT, NBH, true, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p);
+    else PF_LAUNCH((k_prefill_gate_up<GT, NBH, false, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p);
+}
+
+template <int GT, int NBH>
+static void launch_p1_i(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
+    if (p.inter == 256) launch_p1<GT, NBH, pf_cpw_gu(256)>(p, s, ev);
+    else launch_p1<GT, NBH, PF_CPW_GU>(p, s, ev);
 }
 
 template <int GT>
 static void launch_p1_h(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
     switch (p.hidden) {
-        case 256: launch_p1<GT, 1>(p, s, ev); break;
-        case 512: launch_p1<GT, 2>(p, s, ev); break;
-        case 1024: launch_p1<GT, 4>(p, s, ev); break;
-        default: launch_p1<GT, 8>(p, s, ev); break;
+        case 256: launch_p1_i<GT, 1>(p, s, ev); break;
+        case 512: launch_p1_i<GT, 2>(p, s, ev); break;
+        case 1024: launch_p1_i<GT, 4>(p, s, ev); break;
+        default: launch_p1_i<GT, 8>(p, s, ev); break;
     }
 }
 
-template <int DT, int NBI>
+template <int DT, int NBI, int CPW>
 static void launch_p2(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
-    const dim3 grid(p.hidden / PF_ROWS, p.max_tiles);
-    PF_LAUNCH((k_prefill_down<DT, NBI>), grid, ev.armed_b(), ev.b_start, ev.b_stop, s, p);
+    const dim3 grid(p.hidden / (PF_ROWS_DOWN * CPW), p.max_tiles);
+    PF_LAUNCH((k_prefill_down<DT, NBI, CPW>), grid, ev.armed_b(), ev.b_start, ev.b_stop, s, p);
+}
+
+template <int DT, int NBI>
+static void launch_p2_h(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
+    if (p.hidden == 256) launch_p2<DT, NBI, pf_cpw_down(256)>(p, s, ev);
+    else launch_p2<DT, NBI, PF_CPW_DOWN>(p, s, ev);
 }
 
 template <int DT>
 static void launch_p2_i(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
     switch (p.inter) {
-        case 256: launch_p2<DT, 1>(p, s, ev); break;
-        case 512: launch_p2<DT, 2>(p, s, ev); break;
-        case 1024: launch_p2<DT, 4>(p, s, ev); break;
-        default: launch_p2<DT, 8>(p, s, ev); break;
+        case 256: launch_p2_h<DT, 1>(p, s, ev); break;
+        case 512: launch_p2_h<DT, 2>(p, s, ev); break;
+        case 1024: launch_p2_h<DT, 4>(p, s, ev); break;
+        default: launch_p2_h<DT, 8>(p, s, ev); break;
     }
 }
 

@@ -1,6 +1,7 @@
 // Host build of the prefill GEMM's operand math (kquant_frag.h): a 64-lane wave
 // emulated lane by lane, with the MFMA layouts of v_mfma_f32_16x16x32_f16
-// (A: row l%16, k = 8(l/16) + i; B: column l%16, same k) and
+// (A: row l%16, k = 8(l/16) + i; B: column l%16, same k, the lane's k-slots
+// holding the 8 consecutive columns frag_col + frag_lane_col) and
 // v_mfma_f32_16x16x16_f16 (k = 4(l/16) + i), for checking the integer-operand
 // decomposition against the oracle without a GPU.  Test helper only.
 #include <math.h>
@@ -58,10 +59,13 @@ Tile stage(const float* x, int ntok, int K, int split) {
 template <int T, int M>
 void step(const uint32_t* r, int row, int q, int b, const Tile& t, int split, std::vector<double>& P) {
     h8_t a[2];
-    frag_step<T, M>(r, q, a);
+    FragPrep<T> sp;
+    frag_prep<T>(r, q, sp);
+    frag_step<T, M>(r, sp, q, a);
     const h8_t alo = frag_lo_operand<T>(a);
+    const int col = frag_col<T, M>() + frag_lane_col<T>((q + 3) & 3);
     for (int j = 0; j < t.ntok; ++j) {
-        const size_t base = (size_t)j * t.K + 256 * b + 32 * M + 8 * q;
+        const size_t base = (size_t)j * t.K + 256 * b + col;
         double s = 0.0;
         for (int e = 0; e < 8; ++e) {
             for (int n = 0; n < FragGeo<T>::NA; ++n) s += (double)(float)a[n][e] * t.xh[base + e];
@@ -92,8 +96,8 @@ void gemm(const uint8_t* w, int K, const Tile& t, int split, float* out) {
             step<T, 6>(r, row, q, b, t, split, P);
             step<T, 7>(r, row, q, b, t, split, P);
             const uint32_t hdr = r[FragGeo<T>::HDR];
-            d[row] = frag_h2f(hdr);
-            dmin[row] = frag_h2f(hdr >> 16);
+            d[row] = frag_d<T>(hdr);
+            dmin[row] = frag_dmin(hdr);
             if constexpr (FragGeo<T>::MIN) {
                 const h4_t mm = frag_mins<T>(r, q);
                 for (int j = 0; j < t.ntok; ++j)
@@ -126,5 +130,28 @@ extern "C" void mqh_cpu_frag_gemm(int type, const uint8_t* w, int K, const float
         case T_Q5_K: gemm<T_Q5_K>(w, K, t, split, out); break;
         case T_Q6_K: gemm<T_Q6_K>(w, K, t, split, out); break;
         default: gemm<T_Q3_K>(w, K, t, split, out); break;
+    }
+}
+
+// How often each of a super-block's 256 columns is dealt to a (lane, step,
+// slot): every column must be owned exactly once.
+template <int T>
+static void cover(int* count) {
+    for (int q = 0; q < 4; ++q) {
+        const int lc = frag_lane_col<T>((q + 3) & 3);
+        const int c[8] = {frag_col<T, 0>(), frag_col<T, 1>(), frag_col<T, 2>(), frag_col<T, 3>(),
+                          frag_col<T, 4>(), frag_col<T, 5>(), frag_col<T, 6>(), frag_col<T, 7>()};
+        for (int m = 0; m < 8; ++m)
+            for (int e = 0; e < 8; ++e) count[c[m] + lc + e]++;
+    }
+}
+
+extern "C" void mqh_cpu_frag_cover(int type, int* count) {
+    for (int c = 0; c < 256; ++c) count[c] = 0;
+    switch (type) {
+        case T_Q4_K: cover<T_Q4_K>(count); break;
+        case T_Q5_K: cover<T_Q5_K>(count); break;
+        case T_Q6_K: cover<T_Q6_K>(count); break;
+        default: cover<T_Q3_K>(count); break;
     }
 }

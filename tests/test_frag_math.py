@@ -2,10 +2,12 @@
 
 tests/cpu/frag_check.cpp compiles kquant_frag.h -- the same __host__ __device__
 code the gfx950 prefill kernels run -- and emulates one wave lane by lane with
-the documented MFMA register layouts: each lane unpacks its 8 columns of a
-32-column step as exact FP16 integers sc*q (Q6_K: a split pair), the token
-rows enter as power-of-two-scaled FP16 high (+ low) planes, the Q4_K/Q5_K min
-term goes through the sub-block sums, and d / dmin are applied per super-block.
+the documented MFMA register layouts: each lane loads its contiguous byte runs
+of a super-block, unpacks the 8 consecutive columns it owns in each of the 8
+steps as exact FP16 integers sc*q (Q6_K: a split pair), the token rows enter as
+power-of-two-scaled FP16 high (+ low) planes read at the same columns, the
+Q4_K/Q5_K min term goes through the sub-block sums, and d / dmin are applied
+per super-block.  Every column of a super-block must be dealt exactly once.
 The result must match the FP64 product of the oracle-dequantized rows to FP32
 rounding: the decomposition itself is exact, unlike FP16-rounded weights
 (which miss the 1e-3 bar on Q4_K through cancellation of the min offsets).
@@ -34,6 +36,7 @@ def chk():
     L = C.CDLL(str(OUT))
     L.mqh_cpu_frag_gemm.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
     L.mqh_cpu_frag_gemm.restype = None
+    L.mqh_cpu_frag_cover.argtypes = [C.c_int, C.c_void_p]
     return L
 
 
@@ -105,3 +108,10 @@ def test_all_zero_rows(chk):
     rows = np.zeros(16 * 144, np.uint8)
     out = frag_gemm(chk, 12, rows, 256, x, 1)
     assert np.all(out == 0.0)
+
+
+@pytest.mark.parametrize("t", [11, 12, 13, 14])
+def test_lanes_cover_each_column_once(chk, t):
+    count = np.zeros(256, np.int32)
+    chk.mqh_cpu_frag_cover(t, count.ctypes.data)
+    assert np.all(count == 1)

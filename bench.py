@@ -81,6 +81,18 @@ def step_bytes(layer) -> int:
     return (K + 1) * layer.bytes_per_expert()
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "kernel_traffic.json"
+
+
+def measured_traffic(instance: str):
+    """HBM bytes per dispatch of a kernel instance from the committed counter
+    runs (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), or None."""
+    try:
+        return json.loads(TRAFFIC_FILE.read_text())["kernels"][instance]["hbm_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def roofline(kern: dict, layer) -> dict:
     """The dominant kernel (the larger average duration) against HBM peak.
     Algorithmic bytes per launch: the quantized weight bytes it must read --
@@ -89,13 +101,10 @@ def roofline(kern: dict, layer) -> dict:
     a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
     b_bytes = (K + 1) * layer.expert_bytes("down")
     if kern["a_us"] >= kern["b_us"]:
-        name, nbytes, us = "k_fast_gate_up", a_bytes, kern["a_us"]
+        name, nbytes, us = "mqh::k_fast_gate_up<12, 32>", a_bytes, kern["a_us"]
     else:
-        name, nbytes, us = "k_fast_down", b_bytes, kern["b_us"]
-    gbs = nbytes / (us * 1e-6) / 1e9
-    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
-            "algorithmic_bytes": nbytes, "kernel_us": round(us, 3)}
+        name, nbytes, us = "mqh::k_fast_down<14, 8>", b_bytes, kern["b_us"]
+    return _hbm_roofline(name, nbytes, us)
 
 
 def parity_check(layer, x, ids, ws, y_gpu) -> float:
@@ -277,9 +286,10 @@ def _kernel_pair_times(calls, reps: int) -> dict:
 
 
 def _hbm_roofline(name: str, nbytes: float, us: float) -> dict:
+    """name: the kernel instance as the profiler names it."""
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name), "kernel": name,
             "algorithmic_bytes": int(nbytes), "kernel_us": round(us, 3)}
 
 
@@ -374,8 +384,8 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
     kb = res[best]["kernels_us"]
     frac_a = (layers[0].expert_bytes("gate") + layers[0].expert_bytes("up")) / layers[0].bytes_per_expert()
     dom = "A" if kb["A"] >= kb["B"] else "B"
-    kname = {"prefill": {"A": "k_prefill_gate_up", "B": "k_prefill_down"},
-             "decode": {"A": "k_fast_gate_up", "B": "k_fast_down"}}[best][dom]
+    kname = {"prefill": {"A": "mqh::k_prefill_gate_up<11, 8, false, 1>", "B": "mqh::k_prefill_down<11, 2, 1>"},
+             "decode": {"A": "mqh::k_fast_gate_up<11, 32>", "B": "mqh::k_fast_down<11, 8>"}}[best][dom]
     out = {
         "workload": f"batched decode: {T} tokens, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
                     f"logits + shared, all Q3_K, {n_layers} resident layers rotated",
@@ -443,7 +453,7 @@ def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
     gu = float(np.mean([(u + 1) * (layers[0].expert_bytes("gate") + layers[0].expert_bytes("up")) for u in U]))
     tflops = flop / (ms * 1e-3) / 1e12
     dom = "A" if kern["a_us"] >= kern["b_us"] else "B"
-    roof = _hbm_roofline("k_prefill_gate_up" if dom == "A" else "k_prefill_down",
+    roof = _hbm_roofline("mqh::k_prefill_gate_up<12, 8, true, 1>" if dom == "A" else "mqh::k_prefill_down<14, 2, 1>",
                          gu if dom == "A" else nbytes - gu, kern["a_us"] if dom == "A" else kern["b_us"])
     log(f"prefill: {ms * 1e3:.1f} us/layer, {tflops:.1f} TFLOP/s, parity {err:.2e}; "
         f"gate/up {kern['a_us']:.1f} us, down {kern['b_us']:.1f} us")
@@ -510,7 +520,7 @@ def bench_dequant(dev, reps: int, cpu_seconds: float) -> dict:
                     "types Q3_K (11), Q4_K (12), Q6_K (14), Q8_0 (8)",
         "metric": "GB/s (quantized bytes read + FP16 bytes written)", "per_type": res,
         "value": res[worst]["gbs"], "unit": "GB/s",
-        "roofline": _hbm_roofline("k_dequant (slowest type %s)" % worst, res[worst]["bytes"], res[worst]["us"]),
+        "roofline": _hbm_roofline("mqh::k_dequant<%s, true>" % worst, res[worst]["bytes"], res[worst]["us"]),
     }
     if cpu_seconds > 0:
         t = 12

@@ -96,8 +96,11 @@ def measured_traffic(instance: str):
 def roofline(kern: dict, layer) -> dict:
     """The dominant kernel (the larger average duration) against HBM peak.
     Algorithmic bytes per launch: the quantized weight bytes it must read --
-    kernel A the gate and up slices of the 9 experts, kernel B their down
-    slices -- plus activations in and out (a few KB)."""
+    the single-launch kernel all three matrices of the 9 experts, else kernel
+    A the gate and up slices, kernel B the down slices -- plus activations in
+    and out (a few KB)."""
+    if kern["kernels"] == 1:
+        return _hbm_roofline("mqh::k_fast_layer<12, 14, 32, 8>", step_bytes(layer), kern["a_us"])
     a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
     b_bytes = (K + 1) * layer.expert_bytes("down")
     if kern["a_us"] >= kern["b_us"]:
@@ -207,8 +210,10 @@ def kernel_times(runner, layers, X, IDS, WS, Y, reps: int) -> dict:
     b = [ms(ev[4 * i + 2], ev[4 * i + 3]) * 1e3 for i in range(n)]
     for h in ev:
         rt.hipEventDestroy(h)
+    # 1: one kernel did both halves (its duration is a_us, b_us is empty)
     return {"a_us": float(np.mean(a)), "b_us": float(np.mean(b)), "launches": n,
-            "a_us_median": float(np.median(a)), "b_us_median": float(np.median(b))}
+            "a_us_median": float(np.median(a)), "b_us_median": float(np.median(b)),
+            "kernels": int(lib.mqh_last_decode_kernels())}
 
 
 # ---------------------------------------------------------------- other workloads
@@ -282,7 +287,8 @@ def _kernel_pair_times(calls, reps: int) -> dict:
     b = [us(ev[4 * i + 2], ev[4 * i + 3]) for i in range(n)]
     for h in ev:
         rt.hipEventDestroy(h)
-    return {"a_us": float(np.mean(a)), "b_us": float(np.mean(b)), "launches": n}
+    return {"a_us": float(np.mean(a)), "b_us": float(np.mean(b)), "launches": n,
+            "kernels": int(lib.mqh_last_decode_kernels())}
 
 
 def _hbm_roofline(name: str, nbytes: float, us: float) -> dict:
@@ -376,16 +382,23 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
         replay = _graph(lambda: [call(l) for l in range(n_layers)], dev)
         ms = _time(replay, max(1, steps // n_layers)) / n_layers
         kern = _kernel_pair_times([lambda l=l: call(l) for l in range(n_layers)], 2)
+        single = name == "decode" and kern["kernels"] == 1
         res[name] = {"us_per_layer": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                      "parity_max_rel_err": float(f"{err:.3e}"),
-                     "kernels_us": {"A": round(kern["a_us"], 2), "B": round(kern["b_us"], 2)}}
+                     "kernels_us": {"AB": round(kern["a_us"], 2)} if single else
+                     {"A": round(kern["a_us"], 2), "B": round(kern["b_us"], 2)}}
         log(f"batched decode via {name}: {ms * 1e3:.2f} us/layer, parity {err:.2e}")
     best = min(res, key=lambda k: res[k]["us_per_layer"])
     kb = res[best]["kernels_us"]
     frac_a = (layers[0].expert_bytes("gate") + layers[0].expert_bytes("up")) / layers[0].bytes_per_expert()
-    dom = "A" if kb["A"] >= kb["B"] else "B"
+    if "AB" in kb:
+        dom, frac = "AB", 1.0
+    else:
+        dom = "A" if kb["A"] >= kb["B"] else "B"
+        frac = frac_a if dom == "A" else 1 - frac_a
     kname = {"prefill": {"A": "mqh::k_prefill_gate_up<11, 8, false, 1>", "B": "mqh::k_prefill_down<11, 2, 1>"},
-             "decode": {"A": "mqh::k_fast_gate_up<11, 32>", "B": "mqh::k_fast_down<11, 8>"}}[best][dom]
+             "decode": {"A": "mqh::k_fast_gate_up<11, 32>", "B": "mqh::k_fast_down<11, 8>",
+                        "AB": "mqh::k_fast_layer<11, 11, 32, 8>"}}[best][dom]
     out = {
         "workload": f"batched decode: {T} tokens, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
                     f"logits + shared, all Q3_K, {n_layers} resident layers rotated",
@@ -393,7 +406,7 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
         "value": res[best]["gbs"], "unit": "GB/s", "us_per_layer": res[best]["us_per_layer"],
         "path": best, "paths": res, "distinct_experts_mean": float(np.mean(U)),
         "weight_bytes_per_step": int(nbytes),
-        "roofline": _hbm_roofline(kname, nbytes * (frac_a if dom == "A" else 1 - frac_a), kb[dom]),
+        "roofline": _hbm_roofline(kname, nbytes * frac, kb[dom]),
     }
     if cpu_seconds > 0:
         L0 = layers[0]
@@ -643,7 +656,34 @@ def main() -> int:
     # each kernel bracketed by HIP events recorded by the runtime at its
     # start and end (mqh_profile_next_decode), on the stream it runs on
     kern = kernel_times(runner, layers, X, IDS, WS, Y, reps=max(1, min(reps, 10)))
-    log(f"kernel A (gate/up) {kern['a_us']:.3f} us, kernel B (down+combine) {kern['b_us']:.3f} us per launch")
+    if kern["kernels"] == 1:
+        log(f"single-launch kernel {kern['a_us']:.3f} us per launch")
+        kernels_us = {"k_fast_layer": round(kern["a_us"], 3), "launches_each": kern["launches"]}
+    else:
+        log(f"kernel A (gate/up) {kern['a_us']:.3f} us, kernel B (down+combine) {kern['b_us']:.3f} us per launch")
+        kernels_us = {"k_fast_gate_up": round(kern["a_us"], 3), "k_fast_down": round(kern["b_us"], 3),
+                      "launches_each": kern["launches"]}
+
+    # the single-launch kernel on the same layers, for comparison
+    alt = None
+    if not args.eager and kern["kernels"] == 2:
+        from flash_moe_hip import _lib
+
+        lib = _lib.load()
+        old_path = lib.mqh_set_decode_path(2)
+        try:
+            sweep()
+            torch.cuda.synchronize()
+            g2 = _graph(sweep, dev)
+            ms2 = _time(g2, reps) / args.layers
+            k2 = kernel_times(runner, layers, X, IDS, WS, Y, reps=max(1, min(reps, 10)))
+            assert runner.status() == 0
+            if k2["kernels"] == 1:
+                alt = {"us_per_layer": round(ms2 * 1e3, 3), "k_fast_layer": round(k2["a_us"], 3)}
+                log(f"single-launch path: {ms2 * 1e3:.2f} us/layer (kernel {k2['a_us']:.3f} us)")
+            del g2
+        finally:
+            lib.mqh_set_decode_path(old_path)
 
     result = {
         "metric": METRIC,
@@ -667,10 +707,11 @@ def main() -> int:
         },
         "us_per_layer": round(ms_step * 1e3, 3),
         "parity_max_rel_err": float(f"{max(err, err_graph):.3e}"),
-        "kernels_us": {"k_fast_gate_up": round(kern["a_us"], 3), "k_fast_down": round(kern["b_us"], 3),
-                       "launches_each": kern["launches"]},
+        "kernels_us": kernels_us,
         "roofline": roofline(kern, layers[0]),
     }
+    if alt is not None:
+        result["single_launch_path"] = alt
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle, 4 threads)")
         result["cpu_baseline"] = cpu_baseline(layers, xs, ids, ws, args.cpu_seconds)

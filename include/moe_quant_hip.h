@@ -130,11 +130,20 @@ int mqh_moe_prefill(int gate_type, const void* gate, int up_type, const void* up
                     int top_k, float* y, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Select the kernels behind mqh_moe_decode and moe_quant_expert: 0 (default)
- * = the integer-digit fast kernels whenever the shapes and types allow it
- * (FP32 graph, K-quant types, hidden and intermediate in 256..2048), else the
- * generic kernels; 1 = always the generic kernels.  Process-wide; returns the
- * previous setting, or -1 for another value. */
+ * = the two integer-digit fast kernels (gate/up + SwiGLU, then down +
+ * combine) whenever the shapes and types allow it (FP32 graph, K-quant types,
+ * hidden and intermediate in 256..2048), else the generic kernels; 1 = always
+ * the generic kernels; 2 = one kernel launch per call (gate/up and down
+ * workgroups of the same launch hand the activations over through the
+ * workspace) when the shapes allow it (as for 0, plus hidden 1024 or 2048,
+ * intermediate 256 to 1024, at most 16384 gate/up workgroups), else as 0.
+ * Process-wide; returns the previous setting, or -1 for another value. */
 int mqh_set_decode_path(int path);
+
+/* Number of kernels (1 or 2) the calling thread's last mqh_moe_decode or
+ * moe_quant_expert launched; 0 before the first.  No counterpart in the
+ * reference (a profiling aid). */
+int mqh_last_decode_kernels(void);
 
 /* Profiling: record HIP events (hipEvent_t, any may be NULL) at the start and
  * end of the two GEMM kernels of the calling thread's next mqh_moe_decode,
@@ -144,11 +153,13 @@ int mqh_set_decode_path(int path);
  * (its timers are host wall clocks, bench_phases.py:45-56). */
 int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_stop);
 
-/* Zero a workspace (flags and counters) on `stream`. */
+/* Zero a workspace's flags and handoff words on `stream` (once, before first use). */
 int mqh_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Synchronize `stream`, then read and clear the fault flags latched in
- * `workspace`: 0, -4 (non-finite output), -9 (bad expert id) or -5. */
+ * `workspace`: 0, -4 (non-finite output), -7 (a single-launch decode's
+ * activation handoff did not complete; results invalid), -9 (bad expert id)
+ * or -5. */
 int mqh_status(void* workspace, void* stream);
 
 #ifdef __cplusplus

@@ -15,23 +15,34 @@ using namespace mqh;
 namespace {
 
 constexpr int ST_OK = 0, ST_ARG = -1, ST_TYPE = -2, ST_BYTES = -3, ST_NONFINITE = -4, ST_HIP = -5,
-              ST_WORKSPACE = -6, ST_BAD_ID = -9;
+              ST_WORKSPACE = -6, ST_TIMEOUT = -7, ST_BAD_ID = -9;
 
 bool supported(int t) { return block_size(t) != 0; }
 
-// 0: the integer-digit fast kernels when the shapes allow it, 1: always the
-// generic kernels
+// 0: the two integer-digit kernels when the shapes allow them, else the
+// generic kernels; 1: always the generic kernels; 2: the single-launch kernel
+// when the shapes allow it, else as 0
 int g_decode_path = 0;
 
-// events armed by mqh_profile_next_decode for this thread's next decode
+// events armed by mqh_profile_next_decode for this thread's next decode, and
+// the number of kernels this thread's last decode launched
 thread_local KernelEvents t_events;
+thread_local int t_last_kernels = 0;
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s) {
     const KernelEvents ev = t_events;
     t_events = KernelEvents();
-    if (g_decode_path == 0 && fast_supported(p)) return launch_decode_fast(p, s, ev);
+    if (g_decode_path == 2 && fused_supported(p)) {
+        t_last_kernels = 1;
+        return launch_decode_fused(p, s, ev);
+    }
+    t_last_kernels = 2;
+    if (g_decode_path != 1 && fast_supported(p)) return launch_decode_fast(p, s, ev);
     return launch_decode_generic(p, s, ev);
 }
+
+// words to zero in a fresh workspace: the flags and the handoff words
+constexpr int64_t WS_INIT_WORDS = WS_HEAD_BYTES / 4;
 
 // Expected bytes of a [rows x cols] matrix, or a negative status.
 int64_t matrix_bytes(int type, int rows, int cols) {
@@ -108,7 +119,7 @@ void release_ctx(Ctx* c) {
 }
 
 int read_and_clear_flags(int* flags_dev, hipStream_t s) {
-    int h[3] = {0, 0, 0};
+    int h[3] = {0, 0, 0};   // FLAG_NONFINITE, FLAG_BAD_ID, FLAG_TIMEOUT
     if (hipStreamSynchronize(s) != hipSuccess) return ST_HIP;
     if (hipMemcpyAsync(h, flags_dev, sizeof(h), hipMemcpyDeviceToHost, s) != hipSuccess) return ST_HIP;
     if (hipStreamSynchronize(s) != hipSuccess) return ST_HIP;
@@ -116,6 +127,7 @@ int read_and_clear_flags(int* flags_dev, hipStream_t s) {
         if (zero_words(flags_dev, 3, s) != hipSuccess) return ST_HIP;
         if (hipStreamSynchronize(s) != hipSuccess) return ST_HIP;
     }
+    if (h[FLAG_TIMEOUT]) return ST_TIMEOUT;
     if (h[FLAG_BAD_ID]) return ST_BAD_ID;
     if (h[FLAG_NONFINITE]) return ST_NONFINITE;
     return ST_OK;
@@ -204,10 +216,11 @@ int moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes, int
     p.x = (const float*)IO; p.n_tokens = 1;
     p.ids = (const int32_t*)(IO + off_id); p.weights = (const float*)(IO + off_id + 4); p.top_k = 1;
     p.y = (float*)(IO + off_y); p.fp16 = fp16_graph;
-    p.flags = (int*)(WS + wl.flags_off); p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
+    p.flags = (int*)(WS + wl.flags_off); p.sync = (uint64_t*)(WS + wl.sync_off);
+    p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
     p.S = 1; p.Imax = intermediate;
 
-    if ((!fresh_ws || zero_words(WS, wl.flags_off / 4 + N_FLAGS, c->stream) == hipSuccess) &&
+    if ((!fresh_ws || zero_words(WS, WS_INIT_WORDS, c->stream) == hipSuccess) &&
         hipMemcpyAsync(W, gate, gate_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
         hipMemcpyAsync(W + off_up, up, up_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
         hipMemcpyAsync(W + off_down, down, down_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
@@ -235,8 +248,8 @@ int64_t mqh_moe_workspace_bytes(int n_tokens, int top_k, int intermediate, int s
 }
 
 int mqh_workspace_init(void* workspace, int64_t workspace_bytes, void* stream) {
-    if (!workspace || workspace_bytes < (int64_t)N_FLAGS * 4) return ST_ARG;
-    return zero_words(workspace, N_FLAGS, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
+    if (!workspace || workspace_bytes < WS_HEAD_BYTES) return ST_ARG;
+    return zero_words(workspace, WS_INIT_WORDS, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
 }
 
 int mqh_status(void* workspace, void* stream) {
@@ -289,7 +302,8 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
     }
     p.x = x; p.n_tokens = n_tokens; p.ids = ids; p.weights = weights; p.top_k = top_k;
     p.y = y; p.fp16 = fp16_graph;
-    p.flags = (int*)(WS + wl.flags_off); p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
+    p.flags = (int*)(WS + wl.flags_off); p.sync = (uint64_t*)(WS + wl.sync_off);
+    p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
     p.S = top_k + (has_shared ? 1 : 0);
     p.Imax = std::max(intermediate, has_shared ? sh_intermediate : 0);
     return launch_decode(p, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
@@ -354,8 +368,10 @@ int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_
     return ST_OK;
 }
 
+int mqh_last_decode_kernels(void) { return t_last_kernels; }
+
 int mqh_set_decode_path(int path) {
-    if (path != 0 && path != 1) return ST_ARG;
+    if (path < 0 || path > 2) return ST_ARG;
     const int old = g_decode_path;
     g_decode_path = path;
     return old;

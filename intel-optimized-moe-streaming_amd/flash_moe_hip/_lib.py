@@ -26,6 +26,7 @@ EXPORTS = (
     "mqh_moe_prefill_workspace_bytes",
     "mqh_moe_prefill",
     "mqh_set_decode_path",
+    "mqh_last_decode_kernels",
     "mqh_profile_next_decode",
     "mqh_workspace_init",
     "mqh_status",
@@ -39,6 +40,7 @@ STATUS_TEXT = {
     -4: "non-finite output",
     -5: "HIP runtime failure",
     -6: "workspace too small",
+    -7: "decode activation handoff timed out",
     -9: "expert id out of range",
 }
 
@@ -87,6 +89,8 @@ def _declare(lib: C.CDLL) -> C.CDLL:
     lib.mqh_profile_next_decode.restype = _I
     lib.mqh_set_decode_path.argtypes = [_I]
     lib.mqh_set_decode_path.restype = _I
+    lib.mqh_last_decode_kernels.argtypes = []
+    lib.mqh_last_decode_kernels.restype = _I
     lib.mqh_workspace_init.argtypes = [_P, _I64, _P]
     lib.mqh_workspace_init.restype = _I
     lib.mqh_status.argtypes = [_P, _P]

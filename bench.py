@@ -93,21 +93,22 @@ def measured_traffic(instance: str):
         return None
 
 
-def roofline(kern: dict, layer) -> dict:
+def roofline(kern: dict, layer, floor=None) -> dict:
     """The dominant kernel (the larger average duration) against HBM peak.
     Algorithmic bytes per launch: the quantized weight bytes it must read --
     the single-launch kernel all three matrices of the 9 experts, else kernel
     A the gate and up slices, kernel B the down slices -- plus activations in
     and out (a few KB)."""
     if kern["kernels"] == 1:
-        return _hbm_roofline("mqh::k_fast_layer<12, 14, 32, 8>", step_bytes(layer), kern["a_us"])
-    a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
-    b_bytes = (K + 1) * layer.expert_bytes("down")
-    if kern["a_us"] >= kern["b_us"]:
-        name, nbytes, us = "mqh::k_fast_gate_up<12, 32>", a_bytes, kern["a_us"]
+        name, nbytes, us = "mqh::k_fast_layer<12, 14, 32, 8>", step_bytes(layer), kern["a_us"]
     else:
-        name, nbytes, us = "mqh::k_fast_down<14, 8>", b_bytes, kern["b_us"]
-    return _hbm_roofline(name, nbytes, us)
+        a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
+        b_bytes = (K + 1) * layer.expert_bytes("down")
+        if kern["a_us"] >= kern["b_us"]:
+            name, nbytes, us = "mqh::k_fast_gate_up<12, 32>", a_bytes, kern["a_us"]
+        else:
+            name, nbytes, us = "mqh::k_fast_down<14, 8>", b_bytes, kern["b_us"]
+    return _hbm_roofline(name, nbytes, us, floor(nbytes) if floor else None)
 
 
 def parity_check(layer, x, ids, ws, y_gpu) -> float:
@@ -291,12 +292,56 @@ def _kernel_pair_times(calls, reps: int) -> dict:
             "kernels": int(lib.mqh_last_decode_kernels())}
 
 
-def _hbm_roofline(name: str, nbytes: float, us: float) -> dict:
-    """name: the kernel instance as the profiler names it."""
+def read_floor_us(nbytes: int, reps: int = 40) -> float:
+    """Average duration of a plain streaming read of nbytes (mqh_read_floor),
+    rotated over regions of a scratch buffer larger than the 256 MB MALL,
+    timed like the kernels: HIP events recorded at the kernel's own start and
+    end, on the current stream."""
+    import ctypes as C
+
+    import torch
+
+    from flash_moe_hip import _lib
+
+    lib, rt = _lib.load(), _hip_runtime()
+    nbytes = nbytes // 256 * 256
+    n_reg = max(2, -(-(512 << 20) // nbytes))
+    buf = torch.empty(n_reg * nbytes, dtype=torch.uint8, device="cuda")
+    ev = []
+    for _ in range(2 * reps):
+        h = C.c_void_p()
+        if rt.hipEventCreate(C.byref(h)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        ev.append(h)
+    stream = torch.cuda.current_stream().cuda_stream
+    torch.cuda.synchronize()
+    for i in range(reps):
+        _lib.check(lib.mqh_read_floor(buf.data_ptr() + (i % n_reg) * nbytes, nbytes, None, ev[2 * i], ev[2 * i + 1],
+                                      stream), "mqh_read_floor")
+    torch.cuda.synchronize()
+    del buf
+    vals = []
+    for i in range(reps):
+        v = C.c_float()
+        if rt.hipEventElapsedTime(C.byref(v), ev[2 * i], ev[2 * i + 1]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        vals.append(v.value * 1e3)
+    for h in ev:
+        rt.hipEventDestroy(h)
+    return float(np.mean(vals[reps // 4:]))
+
+
+def _hbm_roofline(name: str, nbytes: float, us: float, floor_us: float | None = None) -> dict:
+    """name: the kernel instance as the profiler names it; floor_us: the
+    streaming-read time of the same byte count (read_floor_us)."""
     gbs = nbytes / (us * 1e-6) / 1e9
-    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name), "kernel": name,
-            "algorithmic_bytes": int(nbytes), "kernel_us": round(us, 3)}
+    out = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name), "kernel": name,
+           "algorithmic_bytes": int(nbytes), "kernel_us": round(us, 3)}
+    if floor_us is not None:
+        out["read_floor_us"] = round(floor_us, 3)
+        out["frac_of_read_floor"] = round(floor_us / us, 4)
+    return out
 
 
 def _topk_routing(rng, T: int, k: int):
@@ -406,7 +451,7 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
         "value": res[best]["gbs"], "unit": "GB/s", "us_per_layer": res[best]["us_per_layer"],
         "path": best, "paths": res, "distinct_experts_mean": float(np.mean(U)),
         "weight_bytes_per_step": int(nbytes),
-        "roofline": _hbm_roofline(kname, nbytes * frac, kb[dom]),
+        "roofline": _hbm_roofline(kname, nbytes * frac, kb[dom], read_floor_us(int(nbytes * frac))),
     }
     if cpu_seconds > 0:
         L0 = layers[0]
@@ -466,8 +511,10 @@ def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
     gu = float(np.mean([(u + 1) * (layers[0].expert_bytes("gate") + layers[0].expert_bytes("up")) for u in U]))
     tflops = flop / (ms * 1e-3) / 1e12
     dom = "A" if kern["a_us"] >= kern["b_us"] else "B"
+    dom_bytes = gu if dom == "A" else nbytes - gu
     roof = _hbm_roofline("mqh::k_prefill_gate_up<12, 8, true, 1>" if dom == "A" else "mqh::k_prefill_down<14, 2, 1>",
-                         gu if dom == "A" else nbytes - gu, kern["a_us"] if dom == "A" else kern["b_us"])
+                         dom_bytes, kern["a_us"] if dom == "A" else kern["b_us"],
+                         read_floor_us(int(dom_bytes)))
     log(f"prefill: {ms * 1e3:.1f} us/layer, {tflops:.1f} TFLOP/s, parity {err:.2e}; "
         f"gate/up {kern['a_us']:.1f} us, down {kern['b_us']:.1f} us")
     out = {
@@ -708,7 +755,7 @@ def main() -> int:
         "us_per_layer": round(ms_step * 1e3, 3),
         "parity_max_rel_err": float(f"{max(err, err_graph):.3e}"),
         "kernels_us": kernels_us,
-        "roofline": roofline(kern, layers[0]),
+        "roofline": roofline(kern, layers[0], floor=read_floor_us),
     }
     if alt is not None:
         result["single_launch_path"] = alt

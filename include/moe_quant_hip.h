@@ -145,6 +145,15 @@ int mqh_set_decode_path(int path);
  * reference (a profiling aid). */
 int mqh_last_decode_kernels(void);
 
+/* Read `bytes` (a multiple of 16) at `src` (device memory, 16-byte aligned)
+ * once with a plain streaming kernel on `stream`, between the optional HIP
+ * events start_event / stop_event (recorded at the kernel's own start and
+ * end).  Timed on the same byte count as a decode or prefill kernel it gives
+ * the read time this GPU achieves for a launch of that size.  `sink` (may be
+ * NULL) is a device word the kernel practically never writes.  No
+ * counterpart in the reference (a measurement aid).  Returns 0, -1 or -5. */
+int mqh_read_floor(const void* src, int64_t bytes, void* sink, void* start_event, void* stop_event, void* stream);
+
 /* Profiling: record HIP events (hipEvent_t, any may be NULL) at the start and
  * end of the two GEMM kernels of the calling thread's next mqh_moe_decode,
  * moe_quant_expert or mqh_moe_prefill -- A: gate/up and SwiGLU, B: down

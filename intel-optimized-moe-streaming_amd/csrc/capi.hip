@@ -370,6 +370,14 @@ int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_
 
 int mqh_last_decode_kernels(void) { return t_last_kernels; }
 
+int mqh_read_floor(const void* src, int64_t bytes, void* sink, void* start_event, void* stop_event, void* stream) {
+    if (!src || bytes <= 0 || bytes % 16 || ((uintptr_t)src & 15)) return ST_ARG;
+    return launch_read_floor(src, bytes, (uint32_t*)sink, (hipStream_t)stream, (hipEvent_t)start_event,
+                             (hipEvent_t)stop_event) == hipSuccess
+               ? ST_OK
+               : ST_HIP;
+}
+
 int mqh_set_decode_path(int path) {
     if (path < 0 || path > 2) return ST_ARG;
     const int old = g_decode_path;

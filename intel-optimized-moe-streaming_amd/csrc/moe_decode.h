@@ -146,5 +146,7 @@ bool fused_supported(const DecodeParams& p);
 hipError_t launch_decode_fused(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev);
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream, const KernelEvents& ev);
 hipError_t launch_dequant(int type, const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream);
+hipError_t launch_read_floor(const void* src, int64_t bytes, uint32_t* sink, hipStream_t stream, hipEvent_t start,
+                             hipEvent_t stop);
 
 }  // namespace mqh

@@ -27,6 +27,7 @@ EXPORTS = (
     "mqh_moe_prefill",
     "mqh_set_decode_path",
     "mqh_last_decode_kernels",
+    "mqh_read_floor",
     "mqh_profile_next_decode",
     "mqh_workspace_init",
     "mqh_status",
@@ -91,6 +92,8 @@ def _declare(lib: C.CDLL) -> C.CDLL:
     lib.mqh_set_decode_path.restype = _I
     lib.mqh_last_decode_kernels.argtypes = []
     lib.mqh_last_decode_kernels.restype = _I
+    lib.mqh_read_floor.argtypes = [_P, C.c_int64, _P, _P, _P, _P]
+    lib.mqh_read_floor.restype = _I
     lib.mqh_workspace_init.argtypes = [_P, _I64, _P]
     lib.mqh_workspace_init.restype = _I
     lib.mqh_status.argtypes = [_P, _P]

@@ -96,3 +96,25 @@ def test_full_workload_every_value(hip, oracle_mod, t):
         bad = int(np.count_nonzero(got != want))
         assert bad == 0, f"{role}: {bad} of {got.size} values differ"
         del stack, out
+
+
+def test_read_floor_kernel(hip):
+    """The streaming-read reference kernel (a measurement aid): runs between
+    its events on the given stream, rejects misaligned or ragged sizes, and
+    leaves the source untouched."""
+    import torch
+
+    buf = torch.arange(1 << 20, dtype=torch.int32, device="cuda")
+    before = buf.clone()
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    assert hip.mqh_read_floor(buf.data_ptr(), buf.numel() * 4, sink.data_ptr(), None, None, stream) == 0
+    stop.record()
+    torch.cuda.synchronize()
+    assert start.elapsed_time(stop) > 0.0
+    assert torch.equal(buf, before)
+    assert hip.mqh_read_floor(buf.data_ptr() + 4, 1 << 12, None, None, None, stream) == -1
+    assert hip.mqh_read_floor(buf.data_ptr(), 1000, None, None, None, stream) == -1
+    assert hip.mqh_read_floor(None, 1 << 12, None, None, None, stream) == -1

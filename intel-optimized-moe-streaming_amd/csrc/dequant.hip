@@ -21,22 +21,38 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src
     constexpr int G = block_size(T) / 8;
     constexpr int PB = block_bytes(T);
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gi < n_groups; gi += stride) {
-        const int64_t b = gi / G;
-        const int t = (int)(gi - b * G);
-        float v[8];
-        decode8<T>(src + b * PB, t, v);
-        if constexpr (F16) {
-            uint4 o;
-            o.x = f2h_rn(v[0]) | (f2h_rn(v[1]) << 16);
-            o.y = f2h_rn(v[2]) | (f2h_rn(v[3]) << 16);
-            o.z = f2h_rn(v[4]) | (f2h_rn(v[5]) << 16);
-            o.w = f2h_rn(v[6]) | (f2h_rn(v[7]) << 16);
-            ((uint4*)dst)[gi] = o;
-        } else {
-            float4* o = (float4*)dst + 2 * gi;
-            o[0] = make_float4(v[0], v[1], v[2], v[3]);
-            o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    // two groups per pass, stride apart, both decoded before either is stored,
+    // so each thread has two groups' loads in flight
+    for (int64_t g0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g0 < n_groups; g0 += 2 * stride) {
+        float v[2][8];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            // a second group past the end decodes the last group again (in
+            // bounds, not stored), so both loads issue without a branch
+            const int64_t gi = min(g0 + u * stride, n_groups - 1);
+            const int64_t b = gi / G;
+            decode8<T>(src + b * PB, (int)(gi - b * G), v[u]);
+        }
+        // pin both groups' values here: otherwise the second decode (and its
+        // loads) sinks into the conditional store below, behind the first store
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[1][k] = opaque(v[1][k]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t gi = g0 + u * stride;
+            if (gi >= n_groups) break;
+            if constexpr (F16) {
+                uint4 o;
+                o.x = f2h_rn(v[u][0]) | (f2h_rn(v[u][1]) << 16);
+                o.y = f2h_rn(v[u][2]) | (f2h_rn(v[u][3]) << 16);
+                o.z = f2h_rn(v[u][4]) | (f2h_rn(v[u][5]) << 16);
+                o.w = f2h_rn(v[u][6]) | (f2h_rn(v[u][7]) << 16);
+                ((uint4*)dst)[gi] = o;
+            } else {
+                float4* o = (float4*)dst + 2 * gi;
+                o[0] = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+                o[1] = make_float4(v[u][4], v[u][5], v[u][6], v[u][7]);
+            }
         }
     }
 }

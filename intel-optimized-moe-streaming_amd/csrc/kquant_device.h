@@ -52,6 +52,13 @@ __device__ __forceinline__ uint64_t ld_u64(const uint8_t* p) {
     return v;
 }
 
+// 16 bytes from any byte address, as four dwords
+__device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+
 __device__ __forceinline__ float h2f(uint32_t bits) {
     return __half2float(__ushort_as_half((unsigned short)bits));
 }
@@ -73,24 +80,6 @@ __device__ __forceinline__ float round16(float f) { return __half2float(__float2
 // byte k of a 64-bit word
 __device__ __forceinline__ uint32_t byte_of(uint64_t w, int k) { return (uint32_t)(w >> (8 * k)) & 0xFFu; }
 
-// 6-bit scale and min j (0..7) of Q4_K/Q5_K from the 12 packed bytes at s.
-__device__ __forceinline__ void scale_min_k4(const uint8_t* s, int j, int& sc, int& mn) {
-    if (j < 4) {
-        sc = s[j] & 63;
-        mn = s[j + 4] & 63;
-    } else {
-        sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
-        mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-    }
-}
-
-// signed 6-bit scale j (0..15) of Q3_K from the 12 packed bytes at s
-__device__ __forceinline__ int q3_scale(const uint8_t* s, int j) {
-    const int lo = (j < 8) ? (s[j] & 15) : ((s[j - 8] >> 4) & 15);
-    const int hi = (s[8 + (j & 3)] >> (2 * (j >> 2))) & 3;
-    return (lo | (hi << 4)) - 32;
-}
-
 // ---------------------------------------------------- 8 consecutive values
 //
 // decode8<T>(blk, t, out): values 8t .. 8t+7 of the block at blk, as FP32,
@@ -107,13 +96,23 @@ __device__ __forceinline__ void decode8<T_Q8_0>(const uint8_t* blk, int t, float
     for (int k = 0; k < 8; ++k) out[k] = __fmul_rn((float)(int8_t)byte_of(w, k), d);
 }
 
+// Scale and min j (0..7) of Q4_K/Q5_K from header dwords h1..h3 (scale bytes
+// 0..11), the same bits as scale_min_k4, without per-byte loads.
+__device__ __forceinline__ void scale_min_k4_regs(uint32_t h1, uint32_t h2, uint32_t h3, int j, int& sc, int& mn) {
+    const int sh = 8 * (j & 3);
+    const uint32_t a = (h1 >> sh) & 0xFFu, b = (h2 >> sh) & 0xFFu, c = (h3 >> sh) & 0xFFu;
+    sc = j < 4 ? (int)(a & 63u) : (int)((c & 0x0Fu) | ((a >> 6) << 4));
+    mn = j < 4 ? (int)(b & 63u) : (int)((c >> 4) | ((b >> 6) << 4));
+}
+
 template <>
 __device__ __forceinline__ void decode8<T_Q4_K>(const uint8_t* blk, int t, float out[8]) {
     const int j = t >> 2;                       // sub-block 0..7
     const int g = t >> 3, hi = (t >> 2) & 1, lq = 8 * (t & 3);
-    const float d = h2f(ld_u16(blk)), dmin = h2f(ld_u16(blk + 2));
+    const uint4 h = ld_u128(blk);               // d, dmin, 12 scale bytes: one load
+    const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
     int sc, mn;
-    scale_min_k4(blk + 4, j, sc, mn);
+    scale_min_k4_regs(h.y, h.z, h.w, j, sc, mn);
     const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
     const uint64_t w = ld_u64(blk + 16 + 32 * g + lq) >> (4 * hi);
 #pragma unroll
@@ -124,9 +123,10 @@ template <>
 __device__ __forceinline__ void decode8<T_Q5_K>(const uint8_t* blk, int t, float out[8]) {
     const int j = t >> 2;
     const int g = t >> 3, hi = (t >> 2) & 1, lq = 8 * (t & 3);
-    const float d = h2f(ld_u16(blk)), dmin = h2f(ld_u16(blk + 2));
+    const uint4 h = ld_u128(blk);
+    const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
     int sc, mn;
-    scale_min_k4(blk + 4, j, sc, mn);
+    scale_min_k4_regs(h.y, h.z, h.w, j, sc, mn);
     const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
     const uint64_t lo = ld_u64(blk + 48 + 32 * g + lq) >> (4 * hi);
     const uint64_t hb = ld_u64(blk + 16 + lq) >> j;
@@ -154,8 +154,18 @@ __device__ __forceinline__ void decode8<T_Q6_K>(const uint8_t* blk, int t, float
 template <>
 __device__ __forceinline__ void decode8<T_Q3_K>(const uint8_t* blk, int t, float out[8]) {
     const int h = t >> 4, s = (t >> 2) & 3, lq = 8 * (t & 3);
-    const float d = h2f(ld_u16(blk + 108));
-    const float ds = __fmul_rn(d, (float)q3_scale(blk + 96, t >> 1));
+    // bytes 94..109: two quant bytes, the 12 scale bytes, d (one load that ends
+    // inside the block)
+    const uint4 v = ld_u128(blk + 94);
+    const uint32_t s0 = __builtin_amdgcn_alignbit(v.y, v.x, 16);   // scale bytes 0..3
+    const uint32_t s1 = __builtin_amdgcn_alignbit(v.z, v.y, 16);   // 4..7
+    const uint32_t s2 = __builtin_amdgcn_alignbit(v.w, v.z, 16);   // 8..11
+    const float d = h2f(v.w >> 16);
+    const int j = t >> 1;
+    const uint64_t lo64 = (uint64_t)s0 | ((uint64_t)s1 << 32);
+    const int sc = (int)(((lo64 >> (8 * (j & 7) + 4 * (j >> 3))) & 15u) |
+                         (((s2 >> (8 * (j & 3) + 2 * (j >> 2))) & 3u) << 4)) - 32;
+    const float ds = __fmul_rn(d, (float)sc);
     const uint64_t lo = ld_u64(blk + 32 + 32 * h + lq) >> (2 * s);
     const uint64_t hm = ld_u64(blk + lq) >> (t >> 2);
 #pragma unroll

@@ -485,10 +485,10 @@ __device__ __forceinline__ void down_body(const DecodeParams& p, const FastLayou
     }
 }
 
-template <int DT, int LPR>
+template <int DT, int LPR, int NPB>
 __global__ __launch_bounds__(1024) void k_fast_down(DecodeParams p, FastLayout L) {
-    __shared__ SharedB<GeoB<LPR>::RB> sh;
-    down_body<DT, LPR, false>(p, L, blockIdx.x, blockIdx.y, sh, 0, 0);
+    __shared__ SharedB<GeoB<LPR, NPB>::RB> sh;
+    down_body<DT, LPR, false, NPB>(p, L, blockIdx.x, blockIdx.y, sh, 0, 0);
 }
 
 // ------------------------------------------------------------------ launch
@@ -541,13 +541,31 @@ static void launch_a_t(const DecodeParams& p, const FastLayout& L, hipStream_t s
     }
 }
 
+#ifndef FAST_DOWN_WG_TARGET
+#define FAST_DOWN_WG_TARGET 1024   // kernel B workgroups above which rows per workgroup grow
+#endif
+
+template <int DT, int LPR, int NPB>
+static void launch_b_n(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
+    dim3 grid(p.hidden / GeoB<LPR, NPB>::RB, p.n_tokens);
+    if (ev.armed_b())
+        hipExtLaunchKernelGGL((k_fast_down<DT, LPR, NPB>), grid, dim3(64 * p.S), 0, stream, ev.b_start, ev.b_stop, 0,
+                              p, L);
+    else
+        hipLaunchKernelGGL((k_fast_down<DT, LPR, NPB>), grid, dim3(64 * p.S), 0, stream, p, L);
+}
+
+// Row groups per wave: one while the grid is small (a single token: every
+// workgroup on its own CU), more when many tokens would otherwise make many
+// short workgroups.
 template <int DT, int LPR>
 static void launch_b(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
-    dim3 grid(p.hidden / GeoB<LPR>::RB, p.n_tokens);
-    if (ev.armed_b())
-        hipExtLaunchKernelGGL((k_fast_down<DT, LPR>), grid, dim3(64 * p.S), 0, stream, ev.b_start, ev.b_stop, 0, p, L);
-    else
-        hipLaunchKernelGGL((k_fast_down<DT, LPR>), grid, dim3(64 * p.S), 0, stream, p, L);
+    const int64_t wg1 = (int64_t)(p.hidden / GeoB<LPR, 1>::RB) * p.n_tokens;
+    constexpr bool wide = LaneGeo<DT>::NRAW > 12;   // four row groups would spill
+    if (!wide && wg1 >= 4 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 4>::RB >= 1)
+        launch_b_n<DT, LPR, wide ? 2 : 4>(p, L, stream, ev);
+    else if (wg1 >= 2 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 2>::RB >= 1) launch_b_n<DT, LPR, 2>(p, L, stream, ev);
+    else launch_b_n<DT, LPR, 1>(p, L, stream, ev);
 }
 
 template <int DT>

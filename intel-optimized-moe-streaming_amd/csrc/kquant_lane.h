@@ -211,12 +211,32 @@ __host__ __device__ inline void k4_scale_min_pair(const uint32_t* hdr, int k, ui
     mn = k < 2 ? mn_lo : mn_hi;
 }
 
-// Q3_K signed 6-bit scale j (0..15) from the 12 scale bytes.
-__host__ __device__ inline int k3_scale(const uint32_t* sc, int j) {
-    const uint64_t lo64 = (uint64_t)sc[0] | ((uint64_t)sc[1] << 32);
-    const int lo = (int)((lo64 >> (8 * (j & 7) + 4 * (j >> 3))) & 15);
-    const int hi = (int)((sc[2] >> (8 * (j & 3) + 2 * (j >> 2))) & 3);
-    return (lo | (hi << 4)) - 32;
+// Bit field of `width` bits of x at `off` (v_bfe_u32 on the device).
+__host__ __device__ inline uint32_t bfe(uint32_t x, int off, int width) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_ubfe(x, (uint32_t)off, (uint32_t)width);
+#else
+    return (x >> off) & ((1u << width) - 1u);
+#endif
+}
+
+// x rotated right by r (0..31) (v_alignbit_b32 on the device).
+__host__ __device__ inline uint32_t rotr(uint32_t x, int r) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_alignbit(x, x, (uint32_t)r);
+#else
+    return r ? (x >> r) | (x << (32 - r)) : x;
+#endif
+}
+
+// Q3_K signed 6-bit scale 8h + 2s + odd (the scale of run s of lane k = 2h +
+// odd) from the 12 scale bytes sc[0..2]: its low nibble is nibble h of byte
+// 2s + odd, its high two bits are bits 2(s/2) of byte 8 + 2(s%2) + odd, so both
+// sit at the lane constant sh = 8 odd + 4h plus a per-run constant.
+__host__ __device__ inline int k3_scale_run(const uint32_t* sc, int sh, int s) {
+    const uint32_t lo = bfe(sc[s >> 1], sh + 16 * (s & 1), 4);
+    const uint32_t hi = bfe(sc[2], sh + 16 * (s & 1) + 2 * (s >> 1), 2);
+    return (int)(lo | (hi << 4)) - 32;
 }
 
 // ---------------------------------------------------------------- lane dots
@@ -254,13 +274,15 @@ __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const Lane
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             const int s = j + 2 * r;
+            // qh bits 2s, 2s + 1 of every byte moved to bits 4, 5 by one rotation
+            const int rq = (2 * s - 4) & 31;
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
                 uint32_t q[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     q[i] = ((raw[4 * p + i] >> (4 * r)) & 0x0F0F0F0Fu) |
-                           (((raw[8 + 4 * p + i] >> (2 * s)) & 0x03030303u) << 4);   // 0..63; -32 below
+                           (rotr(raw[8 + 4 * p + i], rq) & 0x30303030u);   // 0..63; -32 below
                 // int8 scale of the 16-column sub-block 8h + 2s + p (byte 2s + p of the 8 loaded)
                 const int sb = 2 * s + p;
                 const int sc = (int)(int8_t)(uint8_t)((sb < 4 ? raw[16] >> (8 * sb) : raw[17] >> (8 * (sb - 4))) & 0xFFu);
@@ -271,15 +293,19 @@ __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const Lane
         return d * acc;
     } else {  // Q3_K
         const float d = f16_bits_to_f32(raw[11] & 0xFFFFu);
-        const int h = k >> 1, odd = k & 1;
+        const int h = k >> 1, odd = k & 1, sh = 8 * odd + 4 * h;
         float acc = 0.0f;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
+            // hmask bit 4h + s of every byte moved to bit 2 by one rotation
+            // (rotating right by 4h + s - 2 mod 32 takes byte k's bit 4h + s to
+            // bit 8k + 2 without crossing the word's top)
+            const int r = (4 * h + s - 2) & 31;
             uint32_t q[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                q[i] = ((raw[4 + i] >> (2 * s)) & 0x03030303u) | (((raw[i] >> (4 * h + s)) & 0x01010101u) << 2);
-            const int sc = k3_scale(raw + 8, 8 * h + 2 * s + odd);
+                q[i] = ((raw[4 + i] >> (2 * s)) & 0x03030303u) | (rotr(raw[i], r) & 0x04040404u);
+            const int sc = k3_scale_run(raw + 8, sh, s);
             acc = fmaf((float)sc, fmaf(x.xs[s], (float)piece_dot(q, x, s), -4.0f * x.sum[s]), acc);
         }
         return d * acc;

@@ -280,6 +280,18 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
     const bool active = threadIdx.x < NT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
+    // 1. the token's values first: their address needs no expert id, so the
+    // load goes out while the id is still being read
+    const float* xt = p.x + (int64_t)t * H;
+    const bool gate_wg = shared && bx == 0 && p.sh_gate_inp != nullptr;
+    float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f), gi = xv;
+    if (active) {
+        xv = x_load<H, NT>(xt);
+        // the shared expert's sigmoid gate vector, same columns (one workgroup per token)
+        if (gate_wg) gi = x_load<H, NT>(p.sh_gate_inp);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     const uint8_t *Gm, *Um;
     bool bad = false;
     if (shared) {
@@ -293,17 +305,9 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
     const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
     const int row = bx * RA + wave * RPI + rr;
 
-    // 1. the token's values, then every weight load of this lane (issued in
-    // this order, so waiting for x does not wait for the weights)
-    const float* xt = p.x + (int64_t)t * H;
-    const bool gate_wg = shared && bx == 0 && p.sh_gate_inp != nullptr;
-    float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f), gi = xv;
+    // then every weight load of this lane (waiting for x does not wait for them)
     uint32_t rg[N], ru[N];
     if (active) {
-        xv = x_load<H, NT>(xt);
-        // the shared expert's sigmoid gate vector, same columns (one workgroup per token)
-        if (gate_wg) gi = x_load<H, NT>(p.sh_gate_inp);
-        __builtin_amdgcn_sched_barrier(0);
         const int64_t off = (int64_t)row * ROW_BYTES + blk * BB;
         lane_load<GT>(Gm + off, k, rg);
         lane_load<GT>(Um + off, k, ru);
@@ -406,6 +410,14 @@ __device__ __forceinline__ void down_body(const DecodeParams& p, const FastLayou
     const int r0 = bx * RB;
     const bool shared = p.has_shared && s == p.top_k;
 
+    LaneX X;
+    // the activation digits first: their address needs no expert id, so the
+    // loads go out while the id is still being read
+    if constexpr (!FUSED) {
+        if (active) lane_x<DT>(act_digits(L, (const uint8_t*)p.act, t, s, p.S), blk, k, X);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
     const uint8_t* D = p.sh_down;
     bool bad = false;
     float w = 0.0f;
@@ -416,7 +428,6 @@ __device__ __forceinline__ void down_body(const DecodeParams& p, const FastLayou
         w = bad ? 0.0f : p.weights[t * p.top_k + s];
     }
 
-    LaneX X;
     uint32_t raw[NPB][N];
     if constexpr (FUSED) {
         // every weight load first (it does not depend on the producers) ...
@@ -445,9 +456,7 @@ __device__ __forceinline__ void down_body(const DecodeParams& p, const FastLayou
         __syncthreads();
         if (active) lane_x_dev<DT>(act_digits(L, (const uint8_t*)p.act, t, s, p.S), blk, k, X);
     } else {
-        // activation digits first (small, in L2), then every weight load
-        if (active) lane_x<DT>(act_digits(L, (const uint8_t*)p.act, t, s, p.S), blk, k, X);
-        __builtin_amdgcn_sched_barrier(0);
+        // then every weight load
         if (active) {
 #pragma unroll
             for (int q = 0; q < NPB; ++q)

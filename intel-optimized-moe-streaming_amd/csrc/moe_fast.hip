@@ -127,11 +127,12 @@ __device__ __forceinline__ void x_digits(float4 v, int8_t* planes, float* xs16, 
     const int i0 = threadIdx.x * 4;
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     float s = (v.x + v.y) + (v.z + v.w);
-#pragma unroll
-    for (int off = 1; off < RUN / 4; off <<= 1) {   // 4 threads per 16-column run
-        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-        s += __shfl_xor(s, off, 64);
-    }
+    // 4 threads per 16-column run (lane-xor swizzles: no address arithmetic)
+    amax = fmaxf(amax, swz_xor<1>(amax));
+    s += swz_xor<1>(s);
+    amax = fmaxf(amax, swz_xor<2>(amax));
+    s += swz_xor<2>(s);
+    static_assert(RUN / 4 == 4, "two swizzle steps cover a run");
     const float inv = digit_inv(amax);
     const uint32_t a = split2(v.x, inv), b = split2(v.y, inv), c = split2(v.z, inv), d = split2(v.w, inv);
     *(uint32_t*)(planes + i0) = (a & 0xFFu) | ((b & 0xFFu) << 8) | ((c & 0xFFu) << 16) | ((d & 0xFFu) << 24);

@@ -367,9 +367,16 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
     }
 }
 
-template <int GT, int LPR>
+// SGT: the shared expert's gate/up type (its workgroups take that code path).
+template <int GT, int SGT, int LPR>
 __global__ __launch_bounds__(GeoA<LPR>::NT) void k_fast_gate_up(DecodeParams p, FastLayout L) {
     __shared__ SharedA<64 * LPR, GeoA<LPR>::WPG> sh;
+    if constexpr (SGT != GT) {
+        if (p.has_shared && (int)blockIdx.y == p.top_k) {
+            gate_up_body<SGT, LPR, false>(p, L, blockIdx.x, blockIdx.y, blockIdx.z, sh, nullptr, 0);
+            return;
+        }
+    }
     gate_up_body<GT, LPR, false>(p, L, blockIdx.x, blockIdx.y, blockIdx.z, sh, nullptr, 0);
 }
 
@@ -393,11 +400,13 @@ struct SharedB {
 
 // Workgroup (bx, t) of kernel B: RB down rows of token t for every slot (wave
 // s = slot s; waves at or past S only join the barriers), combined in top-k
-// order.  FUSED: the weights are requested first, then the workgroup waits
-// until the n_ready ready words of token t's producers (sync[t * n_ready ...])
-// hold `stamp`, and reads the activations with device-scope loads.
+// order.  down_slot is the calling wave's part (its slot's rows into LDS, with
+// the slot's weight type DT), down_combine the workgroup's.  FUSED: the weights
+// are requested first, then the workgroup waits until the n_ready ready words
+// of token t's producers (sync[t * n_ready ...]) hold `stamp`, and reads the
+// activations with device-scope loads (every wave takes part in that wait).
 template <int DT, int LPR, bool FUSED, int NPB_ = 1>
-__device__ __forceinline__ void down_body(const DecodeParams& p, const FastLayout& L, int bx, int t,
+__device__ __forceinline__ void down_slot(const DecodeParams& p, const FastLayout& L, int bx, int t,
                                           SharedB<GeoB<LPR, NPB_>::RB>& sh, int n_ready, uint64_t stamp) {
     constexpr int N = LaneGeo<DT>::NRAW;
     constexpr int BB = block_bytes(DT);
@@ -482,23 +491,42 @@ __device__ __forceinline__ void down_body(const DecodeParams& p, const FastLayou
             sh.s_w[s] = sc;
         }
     }
-    __syncthreads();
+}
 
+template <int LPR, int NPB_>
+__device__ __forceinline__ void down_combine(const DecodeParams& p, int bx, int t, SharedB<GeoB<LPR, NPB_>::RB>& sh) {
+    constexpr int RB = GeoB<LPR, NPB_>::RB;
+    __syncthreads();
     // combine in top-k order, then the shared expert (moe_layer.py:70-106)
     if (threadIdx.x < RB) {
         const int r = threadIdx.x;
         float acc = 0.0f;
         for (int j = 0; j < p.top_k; ++j) acc = __fadd_rn(acc, __fmul_rn(sh.s_w[j], sh.s_y[j][r]));
         if (p.has_shared) acc = __fadd_rn(acc, __fmul_rn(sh.s_w[p.top_k], sh.s_y[p.top_k][r]));
-        p.y[(int64_t)t * p.hidden + r0 + r] = acc;
+        p.y[(int64_t)t * p.hidden + bx * RB + r] = acc;
         if (!isfinite(acc)) atomicOr(&p.flags[FLAG_NONFINITE], 1);
     }
 }
 
-template <int DT, int LPR, int NPB>
+template <int DT, int LPR, bool FUSED, int NPB_ = 1>
+__device__ __forceinline__ void down_body(const DecodeParams& p, const FastLayout& L, int bx, int t,
+                                          SharedB<GeoB<LPR, NPB_>::RB>& sh, int n_ready, uint64_t stamp) {
+    down_slot<DT, LPR, FUSED, NPB_>(p, L, bx, t, sh, n_ready, stamp);
+    down_combine<LPR, NPB_>(p, bx, t, sh);
+}
+
+// SDT: the shared expert's down type (its wave takes that code path).
+template <int DT, int SDT, int LPR, int NPB>
 __global__ __launch_bounds__(1024) void k_fast_down(DecodeParams p, FastLayout L) {
     __shared__ SharedB<GeoB<LPR, NPB>::RB> sh;
-    down_body<DT, LPR, false, NPB>(p, L, blockIdx.x, blockIdx.y, sh, 0, 0);
+    if constexpr (SDT != DT) {
+        const int s = uniform(threadIdx.x >> 6);
+        if (p.has_shared && s == p.top_k) down_slot<SDT, LPR, false, NPB>(p, L, blockIdx.x, blockIdx.y, sh, 0, 0);
+        else down_slot<DT, LPR, false, NPB>(p, L, blockIdx.x, blockIdx.y, sh, 0, 0);
+    } else {
+        down_slot<DT, LPR, false, NPB>(p, L, blockIdx.x, blockIdx.y, sh, 0, 0);
+    }
+    down_combine<LPR, NPB>(p, blockIdx.x, blockIdx.y, sh);
 }
 
 // ------------------------------------------------------------------ launch
@@ -516,7 +544,11 @@ bool fast_supported(const DecodeParams& p) {
     }
     if (p.has_shared) {
         if (!(fast_type(p.sh_gate_type) && p.sh_up_type == p.sh_gate_type && fast_type(p.sh_down_type))) return false;
-        if (gt >= 0 && (p.sh_gate_type != gt || p.sh_down_type != dt || p.sh_inter != I)) return false;
+        // the shared expert shares the routed geometry; its types are the routed
+        // ones or Q6_K (the layout of the reference model's shared experts)
+        if (gt >= 0 && (p.sh_inter != I || (p.sh_gate_type != gt && p.sh_gate_type != T_Q6_K) ||
+                        (p.sh_down_type != dt && p.sh_down_type != T_Q6_K)))
+            return false;
     }
     const int inter = p.top_k > 0 ? p.inter : p.sh_inter;
     return fast_dim(inter);
@@ -531,51 +563,67 @@ FastLayout fast_layout(int inter) {
     return L;
 }
 
-template <int GT, int LPR>
+template <int GT, int SGT, int LPR>
 static void launch_a(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
     dim3 grid(p.inter / GeoA<LPR>::RA, p.S, p.n_tokens);
     if (ev.armed_a())
-        hipExtLaunchKernelGGL((k_fast_gate_up<GT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, ev.a_start, ev.a_stop, 0,
-                              p, L);
+        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, ev.a_start,
+                              ev.a_stop, 0, p, L);
     else
-        hipLaunchKernelGGL((k_fast_gate_up<GT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, p, L);
+        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, p, L);
 }
 
+template <int GT, int SGT>
+static void launch_a_h(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
+    switch (p.hidden) {
+        case 256: launch_a<GT, SGT, 4>(p, L, stream, ev); break;
+        case 512: launch_a<GT, SGT, 8>(p, L, stream, ev); break;
+        case 1024: launch_a<GT, SGT, 16>(p, L, stream, ev); break;
+        default: launch_a<GT, SGT, 32>(p, L, stream, ev); break;
+    }
+}
+
+// a shared expert of another type is Q6_K (fast_supported admits no other)
 template <int GT>
 static void launch_a_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
-    switch (p.hidden) {
-        case 256: launch_a<GT, 4>(p, L, stream, ev); break;
-        case 512: launch_a<GT, 8>(p, L, stream, ev); break;
-        case 1024: launch_a<GT, 16>(p, L, stream, ev); break;
-        default: launch_a<GT, 32>(p, L, stream, ev); break;
-    }
+    if (p.has_shared && p.top_k > 0 && p.sh_gate_type != GT) launch_a_h<GT, T_Q6_K>(p, L, stream, ev);
+    else launch_a_h<GT, GT>(p, L, stream, ev);
 }
 
 #ifndef FAST_DOWN_WG_TARGET
 #define FAST_DOWN_WG_TARGET 1024   // kernel B workgroups above which rows per workgroup grow
 #endif
 
-template <int DT, int LPR, int NPB>
+template <int DT, int SDT, int LPR, int NPB>
 static void launch_b_n(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
     dim3 grid(p.hidden / GeoB<LPR, NPB>::RB, p.n_tokens);
     if (ev.armed_b())
-        hipExtLaunchKernelGGL((k_fast_down<DT, LPR, NPB>), grid, dim3(64 * p.S), 0, stream, ev.b_start, ev.b_stop, 0,
-                              p, L);
+        hipExtLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), 0, stream, ev.b_start,
+                              ev.b_stop, 0, p, L);
     else
-        hipLaunchKernelGGL((k_fast_down<DT, LPR, NPB>), grid, dim3(64 * p.S), 0, stream, p, L);
+        hipLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), 0, stream, p, L);
 }
 
 // Row groups per wave: one while the grid is small (a single token: every
 // workgroup on its own CU), more when many tokens would otherwise make many
 // short workgroups.
+template <int DT, int SDT, int LPR>
+static void launch_b_s(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
+    const int64_t wg1 = (int64_t)(p.hidden / GeoB<LPR, 1>::RB) * p.n_tokens;
+    constexpr bool wide = LaneGeo<DT>::NRAW > 12 || LaneGeo<SDT>::NRAW > 12;   // four row groups would spill
+    if (!wide && wg1 >= 4 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 4>::RB >= 1)
+        launch_b_n<DT, SDT, LPR, wide ? 2 : 4>(p, L, stream, ev);
+    else if (wg1 >= 2 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 2>::RB >= 1)
+        launch_b_n<DT, SDT, LPR, 2>(p, L, stream, ev);
+    else
+        launch_b_n<DT, SDT, LPR, 1>(p, L, stream, ev);
+}
+
+// a shared expert of another type is Q6_K (fast_supported admits no other)
 template <int DT, int LPR>
 static void launch_b(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
-    const int64_t wg1 = (int64_t)(p.hidden / GeoB<LPR, 1>::RB) * p.n_tokens;
-    constexpr bool wide = LaneGeo<DT>::NRAW > 12;   // four row groups would spill
-    if (!wide && wg1 >= 4 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 4>::RB >= 1)
-        launch_b_n<DT, LPR, wide ? 2 : 4>(p, L, stream, ev);
-    else if (wg1 >= 2 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 2>::RB >= 1) launch_b_n<DT, LPR, 2>(p, L, stream, ev);
-    else launch_b_n<DT, LPR, 1>(p, L, stream, ev);
+    if (p.has_shared && p.top_k > 0 && p.sh_down_type != DT) launch_b_s<DT, T_Q6_K, LPR>(p, L, stream, ev);
+    else launch_b_s<DT, DT, LPR>(p, L, stream, ev);
 }
 
 template <int DT>
@@ -618,6 +666,7 @@ static bool fused_dims(int h, int i) { return (h == 2048 || h == 1024) && (i == 
 
 bool fused_supported(const DecodeParams& p) {
     if (!fast_supported(p) || p.sync == nullptr) return false;
+    if (p.has_shared && p.top_k > 0 && (p.sh_gate_type != p.gate_type || p.sh_down_type != p.down_type)) return false;
     const int inter = p.top_k > 0 ? p.inter : p.sh_inter;
     if (!fused_dims(p.hidden, inter)) return false;
     const int64_t n_prod = (int64_t)(inter / 16) * p.S * p.n_tokens;

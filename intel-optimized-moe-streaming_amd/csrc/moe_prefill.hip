@@ -40,7 +40,9 @@ constexpr int PF_ROWS_DOWN = 128; // down rows per workgroup chunk: 8 waves x 16
 #ifndef PF_CPW_DOWN
 #define PF_CPW_DOWN 1            // down row chunks per workgroup
 #endif
-constexpr int PF_RING = 4;       // register ring of super-blocks per lane (R - 1 in flight)
+#ifndef PF_RING
+#define PF_RING 4                // register ring of super-blocks per lane (R - 1 in flight)
+#endif
 constexpr int PF_PAD = 8;        // LDS row padding (halves)
 
 // Waves per SIMD that the LDS footprint of one workgroup (PF_WAVES waves)

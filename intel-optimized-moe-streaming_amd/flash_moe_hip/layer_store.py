@@ -122,8 +122,8 @@ class ExpertLayer:
                 *(_to_device_bytes(shared[r], device) for r in ROLES),
                 types={r: int(shared["types"][r]) for r in ROLES},
                 intermediate=int(shared["intermediate"]),
-                gate_inp=None if gi is None else torch.as_tensor(
-                    np.ascontiguousarray(gi, dtype=np.float32).reshape(-1)).to(device))
+                gate_inp=None if gi is None else torch.from_numpy(
+                    np.array(gi, dtype=np.float32).reshape(-1)).to(device))   # a copy: sources may be read-only maps
         return cls(dev["gate"], dev["up"], dev["down"], types, n_experts, hidden, intermediate, sh,
                    router_weights)
 

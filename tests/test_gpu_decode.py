@@ -260,3 +260,33 @@ def test_fast_repeated_launches_share_workspace(decode_layer, oracle_mod, hip, d
     for k in range(5):
         want = oracle_layer(oracle_mod, layer, host, shared, xs[k][0], ids[k][0].tolist(), ws[k][0].tolist())
         assert oracle_mod.max_relative_error(ys[k].cpu().numpy()[0], want) <= TOL
+
+
+@pytest.mark.parametrize("routed", [(12, 14), (11, 11), (13, 12), (14, 14)])
+def test_shared_expert_q6k_with_other_routed_types(hip, oracle_mod, routed):
+    """The reference model's layout: routed experts Q4_K/Q3_K (down Q6_K, Q3_K),
+    the shared expert all Q6_K.  The fast kernels run the shared slot with its
+    own type; 3 tokens (one row group per wave in kernel B) and 16 tokens (four
+    or two), against the oracle and the generic kernels."""
+    gu, dn = routed
+    t = {"gate": gu, "up": gu, "down": dn}
+    sh = {"gate": 14, "up": 14, "down": 14}
+    layer, host, shared = make_layer(90 + gu + dn, 12, 2048, 512, t, shared_types=sh)
+    rng = np.random.default_rng(gu * 10 + dn)
+    for T in (3, 16):
+        X = rng.standard_normal((T, 2048)).astype(np.float32)
+        ids = np.stack([rng.permutation(12)[:8] for _ in range(T)])
+        ws = rng.dirichlet(np.ones(8), size=T).astype(np.float32)
+        print(f"mixed shared types routed={routed} T={T}", flush=True)
+        got, st = run(layer, X, ids, ws)
+        assert st == 0
+        old = hip.mqh_set_decode_path(1)
+        try:
+            gen, st = run(layer, X, ids, ws)
+        finally:
+            hip.mqh_set_decode_path(old)
+        assert st == 0
+        for tok in range(T):
+            want = oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist())
+            assert oracle_mod.max_relative_error(got[tok], want) <= TOL, (routed, T, tok)
+            assert oracle_mod.max_relative_error(got[tok], gen[tok]) <= TOL, (routed, T, tok)

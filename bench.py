@@ -59,9 +59,10 @@ def build_layers(n_layers: int, device):
     return layers
 
 
-def route_layers(n_layers: int, seed: int = 0):
+def route_layers(n_layers: int, seed: int = 0, layers=None):
     """Per layer: x ~ N(0,1) [H]; router W ~ N(0, 0.02) [H x E]; top-8 ids and
-    softmax weights with the reference router's semantics."""
+    softmax weights with the reference router's semantics.  W becomes the
+    router of layers[l] when layers are given."""
     from flash_moe_hip.router import ExpertRouter
 
     xs, ids, ws = [], [], []
@@ -74,7 +75,77 @@ def route_layers(n_layers: int, seed: int = 0):
         xs.append(x)
         ids.append(np.asarray(i, np.int32))
         ws.append(np.asarray(w, np.float32))
+        if layers is not None:
+            layers[l].router_weights = W
     return np.stack(xs), np.stack(ids), np.stack(ws)
+
+
+def bench_routed_decode(runner, layers, X, ids_host, ws_host, reps: int, dev) -> dict:
+    """The decode step with routing on the device (mqh_moe_decode_routed: the
+    router's scores kernel, then the gate/up kernel taking the top-8 and the
+    softmax in its prologue, then the down kernel), per layer, captured as one
+    graph over the resident layers; and the two-call form (mqh_route, then
+    mqh_moe_decode).  Also the router alone, for 1 and 16 tokens.  Parity: the
+    device's ids equal the host router's, weights within 2e-6."""
+    import torch
+
+    n = len(layers)
+    IDS = torch.empty((n, K), dtype=torch.int32, device=dev)
+    WS = torch.empty((n, K), dtype=torch.float32, device=dev)
+    SC = torch.empty((n, E), dtype=torch.float32, device=dev)
+    Y = torch.empty((n, H), dtype=torch.float32, device=dev)
+    for L in layers:
+        L.router_device()
+
+    def route_all():
+        for l in range(n):
+            runner.route(layers[l], X[l:l + 1], K, ids=IDS[l:l + 1], weights=WS[l:l + 1], scores=SC[l:l + 1])
+
+    def two_call_all():
+        for l in range(n):
+            runner.route(layers[l], X[l:l + 1], K, ids=IDS[l:l + 1], weights=WS[l:l + 1], scores=SC[l:l + 1])
+            runner.decode(layers[l], X[l:l + 1], IDS[l:l + 1], WS[l:l + 1], y=Y[l:l + 1])
+
+    def routed_all():
+        for l in range(n):
+            runner.decode_routed(layers[l], X[l:l + 1], K, ids=IDS[l:l + 1], weights=WS[l:l + 1],
+                                 scores=SC[l:l + 1], y=Y[l:l + 1])
+
+    from flash_moe_hip import _lib
+
+    routed_all()
+    torch.cuda.synchronize()
+    assert runner.status() == 0
+    prologue = _lib.load().mqh_last_route_kernels() == 1
+    ids_dev, ws_dev = IDS.cpu().numpy(), WS.cpu().numpy()
+    same_ids = int(np.sum(np.all(ids_dev == ids_host, axis=1)))
+    ok = ids_dev == ids_host
+    w_err = float(np.abs(ws_dev - ws_host)[np.all(ok, axis=1)].max()) if same_ids else None
+    ms_route = _time(_graph(route_all, dev), reps) / n
+    ms_layer = _time(_graph(routed_all, dev), reps) / n
+    ms_two = _time(_graph(two_call_all, dev), reps) / n
+    assert runner.status() == 0
+    X16 = torch.randn((16, H), dtype=torch.float32, device=dev, generator=torch.Generator(dev).manual_seed(3))
+    I16 = torch.empty((16, K), dtype=torch.int32, device=dev)
+    W16 = torch.empty((16, K), dtype=torch.float32, device=dev)
+    S16 = torch.empty((16, E), dtype=torch.float32, device=dev)
+    ms16 = _time(_graph(lambda: [runner.route(layers[l], X16, K, ids=I16, weights=W16, scores=S16)
+                                 for l in range(n)], dev), reps) / n
+    log(f"device router: {ms_route * 1e3:.2f} us (1 token), {ms16 * 1e3:.2f} us (16 tokens); routed decode "
+        f"{ms_layer * 1e3:.2f} us/layer (route then decode: {ms_two * 1e3:.2f}); ids equal to the host router's "
+        f"on {same_ids}/{n} layers")
+    return {
+        "workload": f"the headline decode step with routing on the device: x . W (FP32 [{E} x {H}] router, "
+                    f"row per expert), top-{K}, float64 softmax, then the fused experts; {n} layers rotated",
+        "us_per_layer": round(ms_layer * 1e3, 3),
+        "select_in_gate_up_prologue": bool(prologue),
+        "gbs": round(step_bytes(layers[0]) / (ms_layer * 1e-3) / 1e9, 1),
+        "us_per_layer_route_then_decode": round(ms_two * 1e3, 3),
+        "router_us": {"1_token": round(ms_route * 1e3, 3), "16_tokens": round(ms16 * 1e3, 3)},
+        "router_bytes_per_call": E * H * 4,
+        "ids_equal_layers": f"{same_ids}/{n}",
+        "weights_max_abs_err": w_err,
+    }
 
 
 def step_bytes(layer) -> int:
@@ -628,7 +699,7 @@ def main() -> int:
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}; building {args.layers} resident layers")
     layers = build_layers(args.layers, dev)
-    xs, ids, ws = route_layers(args.layers)
+    xs, ids, ws = route_layers(args.layers, layers=layers)
     resident_gb = sum(L.resident_bytes() for L in layers) / 1e9
     log(f"resident expert bytes {resident_gb:.2f} GB")
     X = torch.from_numpy(xs).to(dev)
@@ -759,6 +830,7 @@ def main() -> int:
     }
     if alt is not None:
         result["single_launch_path"] = alt
+    result["routed_decode"] = bench_routed_decode(runner, layers, X, ids, ws, max(1, min(reps, 20)), dev)
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle, 4 threads)")
         result["cpu_baseline"] = cpu_baseline(layers, xs, ids, ws, args.cpu_seconds)

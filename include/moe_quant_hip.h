@@ -105,6 +105,31 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
                    const float* x, int n_tokens, const int32_t* ids, const float* weights, int top_k,
                    float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* mqh_moe_decode with the routing on the device, for tokens whose router
+ * input is already in HBM (ExpertRouter.route, src/flash_moe/router.py:140-170,
+ * fused into the decode prologue): router_weights [n_experts x hidden] FP32
+ * (ffn_gate_inp as the GGUF file stores it, 16-byte aligned, hidden % 4 == 0);
+ * scores [n_tokens x n_experts], ids and weights [n_tokens x top_k] are
+ * written (the router's outputs, as mqh_route returns them), then the layer
+ * runs as mqh_moe_decode on those ids and weights.  With at most 256 experts
+ * and the two fast kernels (path 0), the top-k and softmax run inside the
+ * gate/up kernel; otherwise (or on paths 1 and 2) a select kernel of their own
+ * runs first.  n_experts <=
+ * 1024, 1 <= top_k <= min(64, n_experts).  Returns as mqh_moe_decode. */
+int mqh_moe_decode_routed(int gate_type, const void* gate, int up_type, const void* up,
+                          int down_type, const void* down, int n_experts, int hidden, int intermediate,
+                          int sh_gate_type, const void* sh_gate, int sh_up_type, const void* sh_up,
+                          int sh_down_type, const void* sh_down, int sh_intermediate,
+                          const float* sh_gate_inp, const float* x, int n_tokens,
+                          const float* router_weights, int top_k, float* scores, int32_t* ids,
+                          float* weights, float* y, int fp16_graph, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
+/* Router kernels of the calling thread's last mqh_moe_decode_routed: 1 (the
+ * select step ran inside the gate/up kernel) or 2; 0 before the first.  No
+ * counterpart in the reference (a profiling aid). */
+int mqh_last_route_kernels(void);
+
 /* Bytes of workspace mqh_moe_prefill needs (has_shared: 0 or 1). */
 int64_t mqh_moe_prefill_workspace_bytes(int n_tokens, int top_k, int n_experts, int hidden, int intermediate,
                                         int has_shared);
@@ -144,6 +169,23 @@ int mqh_set_decode_path(int path);
  * moe_quant_expert launched; 0 before the first.  No counterpart in the
  * reference (a profiling aid). */
 int mqh_last_decode_kernels(void);
+
+/* Top-k routing of n_tokens tokens on `stream` (replaces ExpertRouter.route,
+ * src/flash_moe/router.py:140-170).  All pointers are device memory:
+ *   x            [n_tokens x hidden] FP32
+ *   gate_weights [n_experts x hidden] FP32: ffn_gate_inp as the GGUF file
+ *                stores it (the transpose of the reference's gate_weights)
+ *   scores       [n_tokens x n_experts] FP32 out: x . W, summed in FP32
+ *   ids          [n_tokens x top_k] int32 out, descending score order
+ *   weights      [n_tokens x top_k] FP32 out: the float64 softmax over the
+ *                selected scores (1/top_k each when its sum is not finite
+ *                and positive), rounded to FP32.
+ * NaN scores rank above every number (np.argsort puts NaN last); equal scores,
+ * and NaNs, go in ascending expert order.  hidden % 4 == 0, x and
+ * gate_weights 16-byte aligned, n_experts <= 1024,
+ * 1 <= top_k <= min(64, n_experts).  Returns 0, -1 or -5. */
+int mqh_route(const float* x, int n_tokens, int hidden, const float* gate_weights, int n_experts, int top_k,
+              float* scores, int32_t* ids, float* weights, void* stream);
 
 /* Read `bytes` (a multiple of 16) at `src` (device memory, 16-byte aligned)
  * once with a plain streaming kernel on `stream`, between the optional HIP

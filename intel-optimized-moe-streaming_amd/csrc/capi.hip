@@ -28,6 +28,9 @@ int g_decode_path = 0;
 // the number of kernels this thread's last decode launched
 thread_local KernelEvents t_events;
 thread_local int t_last_kernels = 0;
+// router kernels of this thread's last routed decode (1: the select step ran
+// inside the gate/up kernel, 2: a select kernel of its own)
+thread_local int t_last_route_kernels = 0;
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s) {
     const KernelEvents ev = t_events;
@@ -257,11 +260,17 @@ int mqh_status(void* workspace, void* stream) {
     return read_and_clear_flags((int*)workspace, (hipStream_t)stream);
 }
 
-int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up, int down_type, const void* down,
-                   int n_experts, int hidden, int intermediate, int sh_gate_type, const void* sh_gate,
-                   int sh_up_type, const void* sh_up, int sh_down_type, const void* sh_down, int sh_intermediate,
-                   const float* sh_gate_inp, const float* x, int n_tokens, const int32_t* ids, const float* weights,
-                   int top_k, float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, void* stream) {
+}  // extern "C" (reopened below)
+
+namespace {
+
+// Validate the arguments of a decode call and fill p (ids/weights may be
+// outputs of the routed call).  Returns a status.
+int decode_params(int gate_type, const void* gate, int up_type, const void* up, int down_type, const void* down,
+                  int n_experts, int hidden, int intermediate, int sh_gate_type, const void* sh_gate, int sh_up_type,
+                  const void* sh_up, int sh_down_type, const void* sh_down, int sh_intermediate,
+                  const float* sh_gate_inp, const float* x, int n_tokens, const int32_t* ids, const float* weights,
+                  int top_k, float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, DecodeParams& p) {
     const bool has_shared = sh_gate != nullptr;
     if (!x || !y || !workspace) return ST_ARG;
     if (hidden <= 0 || hidden > 65536 || n_tokens <= 0 || top_k < 0 || top_k > 64 ||
@@ -285,7 +294,7 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
     if (workspace_bytes < wl.total) return ST_WORKSPACE;
 
     uint8_t* WS = (uint8_t*)workspace;
-    DecodeParams p{};
+    p = DecodeParams{};
     p.gate = (const uint8_t*)gate; p.up = (const uint8_t*)up; p.down = (const uint8_t*)down;
     p.gate_type = gate_type; p.up_type = up_type; p.down_type = down_type;
     if (top_k > 0) {
@@ -306,8 +315,60 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
     p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
     p.S = top_k + (has_shared ? 1 : 0);
     p.Imax = std::max(intermediate, has_shared ? sh_intermediate : 0);
+    return ST_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up, int down_type, const void* down,
+                   int n_experts, int hidden, int intermediate, int sh_gate_type, const void* sh_gate,
+                   int sh_up_type, const void* sh_up, int sh_down_type, const void* sh_down, int sh_intermediate,
+                   const float* sh_gate_inp, const float* x, int n_tokens, const int32_t* ids, const float* weights,
+                   int top_k, float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, void* stream) {
+    DecodeParams p;
+    const int st = decode_params(gate_type, gate, up_type, up, down_type, down, n_experts, hidden, intermediate,
+                                 sh_gate_type, sh_gate, sh_up_type, sh_up, sh_down_type, sh_down, sh_intermediate,
+                                 sh_gate_inp, x, n_tokens, ids, weights, top_k, y, fp16_graph, workspace,
+                                 workspace_bytes, p);
+    if (st) return st;
     return launch_decode(p, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
 }
+
+int mqh_moe_decode_routed(int gate_type, const void* gate, int up_type, const void* up, int down_type,
+                          const void* down, int n_experts, int hidden, int intermediate, int sh_gate_type,
+                          const void* sh_gate, int sh_up_type, const void* sh_up, int sh_down_type,
+                          const void* sh_down, int sh_intermediate, const float* sh_gate_inp, const float* x,
+                          int n_tokens, const float* router_weights, int top_k, float* scores, int32_t* ids,
+                          float* weights, float* y, int fp16_graph, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
+    if (!router_weights || !scores || !ids || !weights || top_k < 1 || n_experts > 1024 || top_k > n_experts ||
+        hidden % 4 || ((uintptr_t)x | (uintptr_t)router_weights) % 16)
+        return ST_ARG;
+    DecodeParams p;
+    const int st = decode_params(gate_type, gate, up_type, up, down_type, down, n_experts, hidden, intermediate,
+                                 sh_gate_type, sh_gate, sh_up_type, sh_up, sh_down_type, sh_down, sh_intermediate,
+                                 sh_gate_inp, x, n_tokens, ids, weights, top_k, y, fp16_graph, workspace,
+                                 workspace_bytes, p);
+    if (st) return st;
+    const hipStream_t s = (hipStream_t)stream;
+    if (launch_route_scores(x, n_tokens, hidden, router_weights, n_experts, scores, s) != hipSuccess) return ST_HIP;
+    if (g_decode_path == 0 && n_experts <= ROUTE_PROLOGUE_MAX_EXPERTS && fast_supported(p)) {
+        // the select step inside the gate/up kernel; the two-kernel fast path
+        p.route_scores = scores; p.route_ids = ids; p.route_weights = weights;
+        const KernelEvents ev = t_events;
+        t_events = KernelEvents();
+        t_last_kernels = 2;
+        t_last_route_kernels = 1;
+        return launch_decode_fast(p, s, ev) == hipSuccess ? ST_OK : ST_HIP;
+    }
+    if (launch_route_select(scores, n_tokens, n_experts, top_k, ids, weights, s) != hipSuccess) return ST_HIP;
+    t_last_route_kernels = 2;
+    return launch_decode(p, s) == hipSuccess ? ST_OK : ST_HIP;
+}
+
+int mqh_last_route_kernels(void) { return t_last_route_kernels; }
 
 int64_t mqh_moe_prefill_workspace_bytes(int n_tokens, int top_k, int n_experts, int hidden, int intermediate,
                                         int has_shared) {
@@ -369,6 +430,18 @@ int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_
 }
 
 int mqh_last_decode_kernels(void) { return t_last_kernels; }
+
+int mqh_route(const float* x, int n_tokens, int hidden, const float* gate_weights, int n_experts, int top_k,
+              float* scores, int32_t* ids, float* weights, void* stream) {
+    if (!x || !gate_weights || !scores || !ids || !weights || n_tokens <= 0 || hidden <= 0 || hidden % 4 ||
+        n_experts <= 0 || n_experts > 1024 || top_k < 1 || top_k > 64 || top_k > n_experts ||
+        ((uintptr_t)x | (uintptr_t)gate_weights) % 16)
+        return ST_ARG;
+    return launch_route(x, n_tokens, hidden, gate_weights, n_experts, top_k, scores, ids, weights,
+                        (hipStream_t)stream) == hipSuccess
+               ? ST_OK
+               : ST_HIP;
+}
 
 int mqh_read_floor(const void* src, int64_t bytes, void* sink, void* start_event, void* stop_event, void* stream) {
     if (!src || bytes <= 0 || bytes % 16 || ((uintptr_t)src & 15)) return ST_ARG;

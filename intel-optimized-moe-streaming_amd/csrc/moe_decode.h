@@ -19,6 +19,8 @@ enum : int { FLAG_NONFINITE = 0, FLAG_BAD_ID = 1, FLAG_TIMEOUT = 2, N_FLAGS = 64
 constexpr int SYNC_MAX_PRODUCERS = 16384;
 constexpr int64_t WS_HEAD_BYTES = (int64_t)N_FLAGS * 4 + (int64_t)SYNC_MAX_PRODUCERS * 8;   // flags + handoff words
 
+constexpr int ROUTE_PROLOGUE_MAX_EXPERTS = 256;   // 4 router scores per lane
+
 constexpr int ROWS_A = 8;    // intermediate rows per workgroup, kernel A
 constexpr int ROWS_W = 4;    // hidden rows per wavefront, kernel B
 constexpr int ROWS_B = 4 * ROWS_W;
@@ -46,6 +48,13 @@ struct DecodeParams {
     const int32_t* ids;     // [n_tokens x top_k]
     const float* weights;   // [n_tokens x top_k]
     int top_k;
+    // routing in the gate/up prologue (route_scores != nullptr, fast path,
+    // n_experts <= ROUTE_PROLOGUE_MAX_EXPERTS): router scores [n_tokens x
+    // n_experts] in; the top-k ids and weights are written to route_ids /
+    // route_weights (the same memory as ids / weights, read by the down kernel)
+    const float* route_scores;
+    int32_t* route_ids;
+    float* route_weights;
     float* y;               // [n_tokens x hidden]
     int fp16;
     // workspace views
@@ -146,6 +155,12 @@ bool fused_supported(const DecodeParams& p);
 hipError_t launch_decode_fused(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev);
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream, const KernelEvents& ev);
 hipError_t launch_dequant(int type, const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream);
+hipError_t launch_route(const float* x, int n_tokens, int hidden, const float* w, int n_experts, int top_k,
+                        float* scores, int32_t* ids, float* weights, hipStream_t stream);
+hipError_t launch_route_scores(const float* x, int n_tokens, int hidden, const float* w, int n_experts, float* scores,
+                               hipStream_t stream);
+hipError_t launch_route_select(const float* scores, int n_tokens, int n_experts, int top_k, int32_t* ids,
+                               float* weights, hipStream_t stream);
 hipError_t launch_read_floor(const void* src, int64_t bytes, uint32_t* sink, hipStream_t stream, hipEvent_t start,
                              hipEvent_t stop);
 

@@ -27,6 +27,7 @@
 
 #include "kquant_lane.h"
 #include "moe_decode.h"
+#include "route_topk.h"
 
 namespace mqh {
 
@@ -297,6 +298,28 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
     bool bad = false;
     if (shared) {
         Gm = p.sh_gate; Um = p.sh_up;
+    } else if (p.route_scores != nullptr) {
+        // routing in the prologue (router.py:140-170): every wave takes the
+        // top s+1 of token t's router scores (the x load above is in flight
+        // meanwhile); one workgroup per token takes all top_k and writes the
+        // ids and softmax weights for the down kernel and the caller
+        const bool publish = bx == 0 && s == 0;
+        uint64_t key[ROUTE_PROLOGUE_MAX_EXPERTS / 64];
+        route_keys(p.route_scores + (int64_t)t * p.n_experts, p.n_experts, lane, key);
+        const int rounds = publish ? p.top_k : s + 1;
+        float mine = 0.0f;
+        int e = 0;
+        for (int r = 0; r < rounds; ++r) {
+            const uint64_t win = route_next(key);
+            if (r == s) e = key_expert(win);
+            if (lane == r) mine = key_score(win);
+            if (publish && threadIdx.x == 0) p.route_ids[t * p.top_k + r] = key_expert(win);
+        }
+        if (publish && wave == 0) {
+            const float w = route_weight(mine, p.top_k, lane);
+            if (lane < p.top_k) p.route_weights[t * p.top_k + lane] = w;
+        }
+        Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
     } else {
         int e = p.ids[t * p.top_k + s];
         if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }

@@ -23,11 +23,14 @@ EXPORTS = (
     "mqh_dequant",
     "mqh_moe_workspace_bytes",
     "mqh_moe_decode",
+    "mqh_moe_decode_routed",
+    "mqh_last_route_kernels",
     "mqh_moe_prefill_workspace_bytes",
     "mqh_moe_prefill",
     "mqh_set_decode_path",
     "mqh_last_decode_kernels",
     "mqh_read_floor",
+    "mqh_route",
     "mqh_profile_next_decode",
     "mqh_workspace_init",
     "mqh_status",
@@ -77,6 +80,15 @@ def _declare(lib: C.CDLL) -> C.CDLL:
         _P, _I, _P, _I64, _P,                    # y, fp16_graph, workspace, ws bytes, stream
     ]
     lib.mqh_moe_decode.restype = _I
+    lib.mqh_moe_decode_routed.argtypes = [
+        _I, _P, _I, _P, _I, _P, _I, _I, _I,      # routed types/tensors, n_experts, hidden, inter
+        _I, _P, _I, _P, _I, _P, _I, _P,          # shared types/tensors, sh_inter, sh_gate_inp
+        _P, _I, _P, _I, _P, _P, _P,              # x, n_tokens, router weights, top_k, scores, ids, weights
+        _P, _I, _P, _I64, _P,                    # y, fp16_graph, workspace, ws bytes, stream
+    ]
+    lib.mqh_moe_decode_routed.restype = _I
+    lib.mqh_last_route_kernels.argtypes = []
+    lib.mqh_last_route_kernels.restype = _I
     lib.mqh_moe_prefill_workspace_bytes.argtypes = [_I, _I, _I, _I, _I, _I]
     lib.mqh_moe_prefill_workspace_bytes.restype = _I64
     lib.mqh_moe_prefill.argtypes = [
@@ -94,6 +106,8 @@ def _declare(lib: C.CDLL) -> C.CDLL:
     lib.mqh_last_decode_kernels.restype = _I
     lib.mqh_read_floor.argtypes = [_P, C.c_int64, _P, _P, _P, _P]
     lib.mqh_read_floor.restype = _I
+    lib.mqh_route.argtypes = [_P, _I, _I, _P, _I, _I, _P, _P, _P, _P]
+    lib.mqh_route.restype = _I
     lib.mqh_workspace_init.argtypes = [_P, _I64, _P]
     lib.mqh_workspace_init.restype = _I
     lib.mqh_status.argtypes = [_P, _P]

@@ -80,6 +80,20 @@ class ExpertLayer:
                 raise ValueError("shared gate_inp must be FP32 [hidden]")
         # FP32 router weights [hidden x n_experts] (host, NumPy) when known
         self.router_weights = router_weights
+        self._router_dev = None
+
+    def router_device(self):
+        """The router weights on the layer's device as the GGUF file stores
+        ffn_gate_inp: a contiguous FP32 [n_experts x hidden] tensor, one row per
+        expert (uploaded once)."""
+        import torch
+
+        if self.router_weights is None:
+            raise ValueError("this layer has no router weights")
+        if self._router_dev is None:
+            w = np.asarray(self.router_weights, dtype=np.float32).reshape(self.hidden, self.n_experts)
+            self._router_dev = torch.from_numpy(np.ascontiguousarray(w.T)).to(self.device)
+        return self._router_dev
 
     # ------------------------------------------------------------- geometry
     def expert_bytes(self, role: str) -> int:

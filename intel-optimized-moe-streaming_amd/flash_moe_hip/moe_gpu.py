@@ -88,6 +88,79 @@ class MoeRunner:
         _lib.check(rc, "mqh_moe_decode")
         return y
 
+    def route(self, layer: ExpertLayer, x, top_k: int, *, router_w=None, ids=None, weights=None, scores=None,
+              stream=None):
+        """Top-k routing on the device (``ExpertRouter.route``, router.py:140-170):
+        x [T,H] FP32; router_w [E,H] FP32, one row per expert as the GGUF file
+        stores ffn_gate_inp (default: the layer's router weights).  Returns
+        (ids [T,k] int32, weights [T,k] FP32) in descending score order; the
+        FP32 scores [T,E] land in ``scores`` when given."""
+        import torch
+
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        w = layer.router_device() if router_w is None else router_w
+        x = x.reshape(-1, layer.hidden)
+        T = x.shape[0]
+        if x.dtype != torch.float32 or not x.is_contiguous():
+            raise ValueError("x must be contiguous FP32")
+        if w.dtype != torch.float32 or not w.is_contiguous() or tuple(w.shape) != (layer.n_experts, layer.hidden):
+            raise ValueError(f"router weights must be contiguous FP32 [{layer.n_experts}, {layer.hidden}]")
+        if ids is None:
+            ids = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
+        if weights is None:
+            weights = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
+        if scores is None:
+            scores = torch.empty((T, layer.n_experts), dtype=torch.float32, device=x.device)
+        if T == 0:
+            return ids, weights
+        rc = self.lib.mqh_route(x.data_ptr(), T, layer.hidden, w.data_ptr(), layer.n_experts, int(top_k),
+                                scores.data_ptr(), ids.data_ptr(), weights.data_ptr(), stream.cuda_stream)
+        _lib.check(rc, "mqh_route")
+        return ids, weights
+
+    def decode_routed(self, layer: ExpertLayer, x, top_k: int, *, router_w=None, y=None, ids=None, weights=None,
+                      scores=None, use_shared: bool = True, stream=None):
+        """The layer with its routing on the device (mqh_moe_decode_routed): the
+        router scores, top-k and softmax of ``route`` followed by ``decode``, in
+        one call; with at most 256 experts and the fast kernels the top-k runs
+        inside the gate/up kernel.  Returns (y, ids, weights)."""
+        import torch
+
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        w = layer.router_device() if router_w is None else router_w
+        x = x.reshape(-1, layer.hidden)
+        T = x.shape[0]
+        if x.dtype != torch.float32 or not x.is_contiguous():
+            raise ValueError("x must be contiguous FP32")
+        if w.dtype != torch.float32 or not w.is_contiguous() or tuple(w.shape) != (layer.n_experts, layer.hidden):
+            raise ValueError(f"router weights must be contiguous FP32 [{layer.n_experts}, {layer.hidden}]")
+        dev = x.device
+        if ids is None:
+            ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+        if weights is None:
+            weights = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+        if scores is None:
+            scores = torch.empty((T, layer.n_experts), dtype=torch.float32, device=dev)
+        if y is None:
+            y = torch.empty((T, layer.hidden), dtype=torch.float32, device=dev)
+        sh = layer.shared if use_shared else None
+        ws = self._workspace(T, top_k, layer.intermediate, sh.intermediate if sh else 0, stream)
+        t = layer.tensors
+        rc = self.lib.mqh_moe_decode_routed(
+            layer.types["gate"], t["gate"].data_ptr(), layer.types["up"], t["up"].data_ptr(),
+            layer.types["down"], t["down"].data_ptr(), layer.n_experts, layer.hidden, layer.intermediate,
+            sh.types["gate"] if sh else 0, sh.gate.data_ptr() if sh else _NULL,
+            sh.types["up"] if sh else 0, sh.up.data_ptr() if sh else _NULL,
+            sh.types["down"] if sh else 0, sh.down.data_ptr() if sh else _NULL,
+            sh.intermediate if sh else 0,
+            sh.gate_inp.data_ptr() if (sh is not None and sh.gate_inp is not None) else _NULL,
+            x.data_ptr(), T, w.data_ptr(), int(top_k), scores.data_ptr(), ids.data_ptr(), weights.data_ptr(),
+            y.data_ptr(), 0, ws.data_ptr(), self._ws_bytes, stream.cuda_stream)
+        _lib.check(rc, "mqh_moe_decode_routed")
+        return y, ids, weights
+
     @staticmethod
     def prefill_supported(layer: ExpertLayer) -> bool:
         """Whether the grouped prefill kernels cover this layer's routed experts."""

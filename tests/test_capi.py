@@ -103,3 +103,27 @@ def test_device_entry_validation(lib):
     small_ws = list(args)
     small_ws[25] = 64
     assert lib.mqh_moe_decode(*small_ws) == -6
+
+
+def test_route_validation(lib):
+    p = C.c_void_p(256)
+    ok = dict(x=p, t=1, h=2048, w=p, e=128, k=8, s=p, ids=p, wts=p)
+
+    def call(**kw):
+        a = {**ok, **kw}
+        return lib.mqh_route(a["x"], a["t"], a["h"], a["w"], a["e"], a["k"], a["s"], a["ids"], a["wts"], None)
+
+    assert call(x=None) == -1
+    assert call(w=None) == -1
+    assert call(s=None) == -1
+    assert call(ids=None) == -1
+    assert call(wts=None) == -1
+    assert call(t=0) == -1
+    assert call(h=0) == -1
+    assert call(h=2046) == -1                 # rows are read 16 bytes at a time
+    assert call(x=C.c_void_p(264)) == -1      # x not 16-byte aligned
+    assert call(w=C.c_void_p(260)) == -1
+    assert call(e=1025) == -1                 # at most 16 scores per lane
+    assert call(k=0) == -1
+    assert call(k=65) == -1                   # one selected score per lane
+    assert call(e=4, k=5) == -1               # more slots than experts

@@ -267,7 +267,7 @@ struct SharedA {
 // Threads at or past NT (the single-launch kernel's wider workgroups) only join
 // the barriers.  FUSED: publish with device-scope stores, then write `stamp`
 // into ready word `ready` (else plain stores; the kernel boundary orders them).
-template <int GT, int LPR, bool FUSED>
+template <int GT, int LPR, bool FUSED, bool ROUTED = false>
 __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLayout& L, int bx, int s, int t,
                                              SharedA<64 * LPR, GeoA<LPR>::WPG>& sh, uint64_t* ready,
                                              uint64_t stamp) {
@@ -298,7 +298,7 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
     bool bad = false;
     if (shared) {
         Gm = p.sh_gate; Um = p.sh_up;
-    } else if (p.route_scores != nullptr) {
+    } else if constexpr (ROUTED) {
         // routing in the prologue (router.py:140-170): every wave takes the
         // top s+1 of token t's router scores (the x load above is in flight
         // meanwhile); one workgroup per token takes all top_k and writes the
@@ -401,6 +401,21 @@ __global__ __launch_bounds__(GeoA<LPR>::NT) void k_fast_gate_up(DecodeParams p, 
         }
     }
     gate_up_body<GT, LPR, false>(p, L, blockIdx.x, blockIdx.y, blockIdx.z, sh, nullptr, 0);
+}
+
+// Kernel A with the router's select step in its prologue (p.route_scores set,
+// at most ROUTE_PROLOGUE_MAX_EXPERTS experts): the same work as
+// k_fast_gate_up once each workgroup knows its expert.
+template <int GT, int SGT, int LPR>
+__global__ __launch_bounds__(GeoA<LPR>::NT) void k_fast_gate_up_routed(DecodeParams p, FastLayout L) {
+    __shared__ SharedA<64 * LPR, GeoA<LPR>::WPG> sh;
+    if constexpr (SGT != GT) {
+        if (p.has_shared && (int)blockIdx.y == p.top_k) {
+            gate_up_body<SGT, LPR, false>(p, L, blockIdx.x, blockIdx.y, blockIdx.z, sh, nullptr, 0);
+            return;
+        }
+    }
+    gate_up_body<GT, LPR, false, true>(p, L, blockIdx.x, blockIdx.y, blockIdx.z, sh, nullptr, 0);
 }
 
 // ---------------------------------------------------------------- kernel B
@@ -589,6 +604,14 @@ FastLayout fast_layout(int inter) {
 template <int GT, int SGT, int LPR>
 static void launch_a(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
     dim3 grid(p.inter / GeoA<LPR>::RA, p.S, p.n_tokens);
+    if (p.route_scores != nullptr) {
+        if (ev.armed_a())
+            hipExtLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream,
+                                  ev.a_start, ev.a_stop, 0, p, L);
+        else
+            hipLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, p, L);
+        return;
+    }
     if (ev.armed_a())
         hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, ev.a_start,
                               ev.a_stop, 0, p, L);

@@ -134,6 +134,60 @@ def test_route_nan_scores_rank_first_with_uniform_weights(oracle_mod):
     np.testing.assert_array_equal(wts[0], np.full(k, 0.25, np.float32))
 
 
+@pytest.mark.parametrize("T,E,k", [(4096, 256, 8), (1024, 1024, 16), (2048, 60, 4)])
+def test_route_select_is_the_top_k_of_its_scores_at_scale(T, E, k):
+    """Size-independent: every token's ids are exactly the top k of the scores
+    the kernel wrote (score descending, then expert ascending), and its weights
+    the float64 softmax of those scores; the scores are x . W within FP32
+    summation error."""
+    H = 2048
+    rng = np.random.default_rng(T + E)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    w = (rng.standard_normal((H, E)) * 0.02).astype(np.float32)
+    ids, wts, scores = gpu_route(x, w, k, with_scores=True)
+    s64 = x.astype(np.float64) @ w.astype(np.float64)
+    bound = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64)
+    assert np.all(np.abs(scores - s64) <= 4e-6 * bound)
+    order = np.lexsort((np.broadcast_to(np.arange(E), scores.shape), -scores), axis=1)[:, :k]
+    np.testing.assert_array_equal(ids, order)
+    sel = np.take_along_axis(scores, order, axis=1).astype(np.float64)
+    e = np.exp(sel - sel.max(axis=1, keepdims=True))
+    want = (e / e.sum(axis=1, keepdims=True)).astype(np.float32)
+    np.testing.assert_allclose(wts, want, rtol=0, atol=1e-7)
+
+
+def test_routed_decode_many_tokens_equals_route_then_decode():
+    """64 tokens: every gate/up workgroup's own top-k in the prologue picks the
+    same experts as the select kernel, so the outputs are bit-identical."""
+    import torch
+    from flash_moe_hip import _lib
+    from flash_moe_hip.moe_gpu import MoeRunner
+    from test_gpu_decode import make_layer
+
+    E, H, I, k, T = 256, 1024, 256, 8, 64
+    types = {"gate": 12, "up": 12, "down": 14}
+    layer, _, _ = make_layer(5, E, H, I, types, shared_types={"gate": 14, "up": 14, "down": 14})
+    rng = np.random.default_rng(6)
+    layer.router_weights = (rng.standard_normal((H, E)) * 0.03).astype(np.float32)
+    xd = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).cuda()
+    runner = MoeRunner()
+    lib = _lib.load()
+    outs = []
+    for _ in range(3):
+        y, ids, wts = runner.decode_routed(layer, xd, k)
+        torch.cuda.synchronize()
+        assert lib.mqh_last_route_kernels() == 1
+        outs.append((y.cpu().numpy(), ids.cpu().numpy(), wts.cpu().numpy()))
+    ids2, wts2 = runner.route(layer, xd, k)
+    y2 = runner.decode(layer, xd, ids2, wts2)
+    torch.cuda.synchronize()
+    assert runner.status() == 0
+    for y, ids, wts in outs:
+        np.testing.assert_array_equal(ids, ids2.cpu().numpy())
+        np.testing.assert_array_equal(wts, wts2.cpu().numpy())
+        np.testing.assert_array_equal(y, y2.cpu().numpy())
+
+
 @pytest.mark.parametrize("E,types,sh_types,T,path,route_kernels", [
     (256, (12, 12, 14), (14, 14, 14), 1, 0, 1),     # the headline layer: select in the gate/up prologue
     (256, (12, 12, 14), (14, 14, 14), 16, 0, 1),

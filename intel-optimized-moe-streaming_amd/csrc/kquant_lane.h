@@ -12,16 +12,19 @@
 //               bits 2 (j + 2r); int8 scales per 16 columns.
 //   Q3_K        qs bytes [32h + l0, +16) with h = k/2, l0 = 16 (k%2): run s (0..3) = bit pair s,
 //               columns 128h + 32s + l0 + [0,16); hmask bytes [l0, +16), bit 4h + s.
+//   Q8_0        a 256-column unit is 8 consecutive 34-byte blocks (272 bytes); lane k owns blocks
+//               2k and 2k+1 (bytes [68k, 68k+68)): run r = block 2k + r, columns 64k + 32r + [0,32),
+//               its FP16 scale then 32 int8 quants.
 //
-// These are the bit positions of the reference decoders (cpp/dequant_k.cpp: Q4_K :182-206,
-// Q5_K :221-240, Q6_K :254-268, Q3_K :278-298), regrouped so that 4 lanes cover one block
-// with contiguous 32-byte (Q3_K: 16-byte) quant loads.
+// These are the bit positions of the reference decoders (cpp/dequant_k.cpp: Q8_0 :146-154,
+// Q4_K :182-206, Q5_K :221-240, Q6_K :254-268, Q3_K :278-298), regrouped so that 4 lanes cover
+// one block with contiguous 32-byte (Q3_K: 16-byte) quant loads.
 //
 // Arithmetic.  Activations are split into two int8 "digits" per value with one scale per
 // aligned 16-column run:  s = max|x| / 127 over the run, X = x/s in [-127, 127],
 //   x0 = rint(X),  x1 = rint((X - x0) * 254)  (both in [-127, 127]),
 //   x = (s/254) * (254 x0 + x1) + r,   |r| <= s/508 (+ FP32 rounding) < 1.6e-5 * max|x|.
-// A run's dot product with the raw (unsigned) quants is then the exact integer
+// A run's dot product with the raw quants (unsigned; Q8_0's are signed) is then the exact integer
 //   I = 254 I0 + I1,  Id = sum_k q_k xd_k   (v_dot4_i32_i8, 4 MACs per instruction; |I| < 2^31)
 // times the run scale s/254.  Quant offsets (Q6_K's -32, Q3_K's -4, the -dmin*m of Q4_K/Q5_K)
 // use the FP32 column sums of 16-column pieces instead of more dot products.
@@ -99,11 +102,15 @@ template <> struct LaneGeo<T_Q4_K> { static constexpr int NR = 2, RL = 32, NRAW 
 template <> struct LaneGeo<T_Q5_K> { static constexpr int NR = 2, RL = 32, NRAW = 20; };
 template <> struct LaneGeo<T_Q6_K> { static constexpr int NR = 2, RL = 32, NRAW = 19; };
 template <> struct LaneGeo<T_Q3_K> { static constexpr int NR = 4, RL = 16, NRAW = 12; };
+template <> struct LaneGeo<T_Q8_0> { static constexpr int NR = 2, RL = 32, NRAW = 17; };
+
+// Bytes of one 256-column unit of a row: a K-quant super-block, or 8 Q8_0 blocks.
+__host__ __device__ constexpr int unit_bytes(int t) { return t == T_Q8_0 ? 8 * 34 : block_bytes(t); }
 
 // First column (within the super-block) of run r of lane k.
 template <int T>
 __host__ __device__ inline int lane_col(int k, int r) {
-    if constexpr (T == T_Q4_K || T == T_Q5_K) return 64 * k + 32 * r;
+    if constexpr (T == T_Q4_K || T == T_Q5_K || T == T_Q8_0) return 64 * k + 32 * r;
     else if constexpr (T == T_Q6_K) return 128 * (k >> 1) + 32 * ((k & 1) + 2 * r);
     else return 128 * (k >> 1) + 32 * r + 16 * (k & 1);
 }
@@ -160,10 +167,18 @@ __host__ __device__ inline int32_t piece_dot(const uint32_t* q, const LaneX& x, 
 __host__ __device__ inline void put4(uint32_t* w, const uint8_t* p) { __builtin_memcpy(w, p, 16); }
 __host__ __device__ inline void put2(uint32_t* w, const uint8_t* p) { __builtin_memcpy(w, p, 8); }
 
-// Raw bytes lane k needs from the block at blk, into raw[0 .. NRAW).
+// Raw bytes lane k needs from the block (Q8_0: the 256-column unit) at blk,
+// into raw[0 .. NRAW).
 template <int T>
 __host__ __device__ inline void lane_load(const uint8_t* blk, int k, uint32_t* raw) {
-    if constexpr (T == T_Q4_K) {
+    if constexpr (T == T_Q8_0) {
+        const uint8_t* b = blk + 68 * k;         // blocks 2k, 2k+1: d0 qs0[32] d1 qs1[32]
+        put4(raw, b);
+        put4(raw + 4, b + 16);
+        put4(raw + 8, b + 32);
+        put4(raw + 12, b + 48);
+        __builtin_memcpy(raw + 16, b + 64, 4);
+    } else if constexpr (T == T_Q4_K) {
         put4(raw, blk);                          // d, dmin, scales
         put4(raw + 4, blk + 16 + 32 * k);        // qs
         put4(raw + 8, blk + 32 + 32 * k);
@@ -229,6 +244,16 @@ __host__ __device__ inline uint32_t rotr(uint32_t x, int r) {
 #endif
 }
 
+// The 32 bits of the 64-bit value hi:lo starting at bit r (0..31)
+// (v_alignbit_b32 on the device).
+__host__ __device__ inline uint32_t rotr_pair(uint32_t hi, uint32_t lo, int r) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_alignbit(hi, lo, (uint32_t)r);
+#else
+    return r ? (lo >> r) | (hi << (32 - r)) : lo;
+#endif
+}
+
 // Q3_K signed 6-bit scale 8h + 2s + odd (the scale of run s of lane k = 2h +
 // odd) from the 12 scale bytes sc[0..2]: its low nibble is nibble h of byte
 // 2s + odd, its high two bits are bits 2(s/2) of byte 8 + 2(s%2) + odd, so both
@@ -244,7 +269,21 @@ __host__ __device__ inline int k3_scale_run(const uint32_t* sc, int sh, int s) {
 // Dot product of lane k's 64 weights (raw bytes from lane_load) with x.
 template <int T>
 __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const LaneX& x) {
-    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+    if constexpr (T == T_Q8_0) {
+        // block 0: d at bytes 0-1, quants at bytes 2..33 (dwords shifted by two
+        // bytes); block 1: d at bytes 34-35, quants at bytes 36..67 (dwords 9..16)
+        const float d0 = f16_bits_to_f32(raw[0] & 0xFFFFu), d1 = f16_bits_to_f32(raw[8] >> 16);
+        float run0 = 0.0f, run1 = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            uint32_t q[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = rotr_pair(raw[4 * p + i + 1], raw[4 * p + i], 16);
+            run0 = fmaf(x.xs[p], (float)piece_dot(q, x, p), run0);
+            run1 = fmaf(x.xs[2 + p], (float)piece_dot(raw + 9 + 4 * p, x, 2 + p), run1);
+        }
+        return fmaf(d0, run0, d1 * run1);
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         constexpr int QS = T == T_Q4_K ? 4 : 12;
         const float d = f16_bits_to_f32(raw[0] & 0xFFFFu), dmin = f16_bits_to_f32(raw[0] >> 16);
         uint32_t sc2, mn2;

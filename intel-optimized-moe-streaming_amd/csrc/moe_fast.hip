@@ -20,9 +20,10 @@
 // so a row of C columns is C/64 consecutive lanes and an instruction covers
 // 64/(C/64) rows.  Every weight byte is read once per (token, slot).
 //
-// Supported (checked by fast_supported): FP32 graph; types Q3_K/Q4_K/Q5_K/Q6_K
+// Supported (checked by fast_supported): FP32 graph; types Q3_K/Q4_K/Q5_K/Q6_K/Q8_0
 // with gate type == up type; hidden and intermediate in {256, 512, 1024, 2048};
-// at most 16 slots; a shared expert with the routed types and intermediate size.
+// at most 16 slots; a shared expert with the routed intermediate size and the
+// routed types or Q6_K.  The single-launch kernel takes the K-quant types only.
 #include <hip/hip_ext.h>
 
 #include "kquant_lane.h"
@@ -273,7 +274,7 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
                                              uint64_t stamp) {
     using G_ = GeoA<LPR>;
     constexpr int N = LaneGeo<GT>::NRAW;
-    constexpr int BB = block_bytes(GT);
+    constexpr int BB = unit_bytes(GT);
     constexpr int H = 64 * LPR;
     constexpr int RPI = G_::RPI, RA = G_::RA, NT = G_::NT, WPG = G_::WPG;
     constexpr int64_t ROW_BYTES = (int64_t)(H / 256) * BB;
@@ -447,7 +448,7 @@ template <int DT, int LPR, bool FUSED, int NPB_ = 1>
 __device__ __forceinline__ void down_slot(const DecodeParams& p, const FastLayout& L, int bx, int t,
                                           SharedB<GeoB<LPR, NPB_>::RB>& sh, int n_ready, uint64_t stamp) {
     constexpr int N = LaneGeo<DT>::NRAW;
-    constexpr int BB = block_bytes(DT);
+    constexpr int BB = unit_bytes(DT);
     constexpr int I = 64 * LPR;
     constexpr int RPI = GeoB<LPR, NPB_>::RPI, NPB = GeoB<LPR, NPB_>::NPB, RB = GeoB<LPR, NPB_>::RB;
     constexpr int64_t ROW_BYTES = (int64_t)(I / 256) * BB;
@@ -569,7 +570,9 @@ __global__ __launch_bounds__(1024) void k_fast_down(DecodeParams p, FastLayout L
 
 // ------------------------------------------------------------------ launch
 
-static bool fast_type(int t) { return t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+static bool fast_type(int t) {
+    return t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_0;
+}
 static bool fast_dim(int n) { return n == 256 || n == 512 || n == 1024 || n == 2048; }
 
 bool fast_supported(const DecodeParams& p) {
@@ -712,6 +715,9 @@ static bool fused_dims(int h, int i) { return (h == 2048 || h == 1024) && (i == 
 
 bool fused_supported(const DecodeParams& p) {
     if (!fast_supported(p) || p.sync == nullptr) return false;
+    // the single-launch kernel is built for the K-quant types
+    if (p.top_k > 0 && (p.gate_type == T_Q8_0 || p.down_type == T_Q8_0)) return false;
+    if (p.has_shared && (p.sh_gate_type == T_Q8_0 || p.sh_down_type == T_Q8_0)) return false;
     if (p.has_shared && p.top_k > 0 && (p.sh_gate_type != p.gate_type || p.sh_down_type != p.down_type)) return false;
     const int inter = p.top_k > 0 ? p.inter : p.sh_inter;
     if (!fused_dims(p.hidden, inter)) return false;
@@ -788,6 +794,7 @@ hipError_t launch_decode_fast(const DecodeParams& p0, hipStream_t stream, const 
         case T_Q4_K: launch_a_t<T_Q4_K>(p, L, stream, ev); break;
         case T_Q5_K: launch_a_t<T_Q5_K>(p, L, stream, ev); break;
         case T_Q6_K: launch_a_t<T_Q6_K>(p, L, stream, ev); break;
+        case T_Q8_0: launch_a_t<T_Q8_0>(p, L, stream, ev); break;
         default: launch_a_t<T_Q3_K>(p, L, stream, ev); break;
     }
     hipError_t err = hipGetLastError();
@@ -796,6 +803,7 @@ hipError_t launch_decode_fast(const DecodeParams& p0, hipStream_t stream, const 
         case T_Q4_K: launch_b_t<T_Q4_K>(p, L, stream, ev); break;
         case T_Q5_K: launch_b_t<T_Q5_K>(p, L, stream, ev); break;
         case T_Q6_K: launch_b_t<T_Q6_K>(p, L, stream, ev); break;
+        case T_Q8_0: launch_b_t<T_Q8_0>(p, L, stream, ev); break;
         default: launch_b_t<T_Q3_K>(p, L, stream, ev); break;
     }
     return hipGetLastError();

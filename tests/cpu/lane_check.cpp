@@ -50,7 +50,7 @@ static float row_dot(const uint8_t* row, int ncols, const HostDigits& hd) {
             uint32_t raw[LaneGeo<T>::NRAW];
             LaneX x;
             lane_x<T>(hd.ref(), b, k, x);
-            lane_load<T>(row + (int64_t)b * block_bytes(T), k, raw);
+            lane_load<T>(row + (int64_t)b * unit_bytes(T), k, raw);
             acc += lane_dot<T>(raw, k, x);
         }
     }
@@ -63,6 +63,7 @@ extern "C" float mqh_cpu_row_dot(int type, const uint8_t* row, int ncols, const 
         case T_Q4_K: return row_dot<T_Q4_K>(row, ncols, hd);
         case T_Q5_K: return row_dot<T_Q5_K>(row, ncols, hd);
         case T_Q6_K: return row_dot<T_Q6_K>(row, ncols, hd);
+        case T_Q8_0: return row_dot<T_Q8_0>(row, ncols, hd);
         default: return row_dot<T_Q3_K>(row, ncols, hd);
     }
 }
@@ -89,6 +90,7 @@ extern "C" void mqh_cpu_lane_cover(int type, int* count) {
         case T_Q3_K: cover<T_Q3_K>(count); break;
         case T_Q6_K: cover<T_Q6_K>(count); break;
         case T_Q5_K: cover<T_Q5_K>(count); break;
+        case T_Q8_0: cover<T_Q8_0>(count); break;
         default: cover<T_Q4_K>(count); break;
     }
 }

@@ -51,7 +51,7 @@ def activations(rng, n, kind):
     return (rng.standard_normal(n) * 1e4).astype(np.float32)
 
 
-@pytest.mark.parametrize("t", [11, 12, 13, 14])
+@pytest.mark.parametrize("t", [8, 11, 12, 13, 14])
 @pytest.mark.parametrize("kind", ["normal", "heavy", "sparse", "large"])
 def test_row_dot_matches_oracle(chk, oracle_mod, t, kind):
     from flash_moe_hip.synthetic import random_tensor
@@ -84,7 +84,7 @@ def test_digit_roundtrip_bound(chk):
     assert (err[nz] / gmax[nz]).max() > 0.3 * DIGIT_ERR
 
 
-@pytest.mark.parametrize("t", [11, 12, 13, 14])
+@pytest.mark.parametrize("t", [8, 11, 12, 13, 14])
 def test_lanes_cover_each_column_once(chk, t):
     count = np.zeros(256, np.int32)
     chk.mqh_cpu_lane_cover(t, count.ctypes.data)

@@ -207,6 +207,38 @@ def test_fast_type_pairs(hip, oracle_mod, types):
                 assert err <= TOL, (types, H, I, path, tok, err)
 
 
+@pytest.mark.parametrize("types,sh_types", [((12, 8), (14, 14)), ((8, 8), (8, 8)), ((8, 14), (14, 14)),
+                                            ((11, 8), (11, 8)), ((13, 8), None)])
+def test_fast_q8_0(hip, oracle_mod, types, sh_types):
+    """Q8_0 gate/up or down projections in the integer-digit kernels (the
+    reference model's first layer has a Q8_0 down projection), 3 tokens, against
+    the oracle and against the generic kernels."""
+    gu, dn = types
+    t = {"gate": gu, "up": gu, "down": dn}
+    st_ = None if sh_types is None else {"gate": sh_types[0], "up": sh_types[0], "down": sh_types[1]}
+    for H, I in ((256, 256), (2048, 512), (512, 1024), (1024, 2048)):
+        layer, host, shared = make_layer(31 + gu + dn, 6, H, I, t, shared_types=st_)
+        rng = np.random.default_rng(H + 3 * I)
+        X = rng.standard_normal((3, H)).astype(np.float32)
+        ids = np.array([[0, 5, 2], [3, 3, 1], [4, 0, 5]])
+        ws = np.array([[0.5, 0.3, 0.2], [0.6, 0.2, 0.2], [0.4, 0.4, 0.2]])
+        want = [oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist())
+                for tok in range(3)]
+        got = {}
+        for path in (0, 1):
+            print(f"q8_0 types={types} shared={sh_types} H={H} I={I} path={path}", flush=True)
+            old = hip.mqh_set_decode_path(path)
+            try:
+                got[path], st = run(layer, X, ids, ws)
+            finally:
+                hip.mqh_set_decode_path(old)
+            assert st == 0
+            for tok in range(3):
+                err = oracle_mod.max_relative_error(got[path][tok], want[tok])
+                assert err <= TOL, (types, H, I, path, tok, err)
+        assert not np.array_equal(got[0], got[1])   # the digit kernels ran, not the FP32 ones
+
+
 def test_single_launch_token_limit(hip, oracle_mod):
     """The single-launch kernel serves up to 16384 gate/up workgroups (tokens x
     slots x intermediate/16): 56 tokens of top-8 + shared at I=512 take it, 57

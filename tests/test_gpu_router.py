@@ -194,7 +194,7 @@ def test_routed_decode_many_tokens_equals_route_then_decode():
     (64, (11, 11, 11), (11, 11, 11), 5, 0, 1),
     (16, (13, 13, 12), None, 3, 0, 1),
     (300, (12, 12, 14), (14, 14, 14), 2, 0, 2),     # more experts than the prologue holds
-    (32, (12, 12, 8), None, 2, 0, 2),               # Q8_0 down: generic kernels
+    (32, (12, 12, 8), None, 2, 0, 1),               # Q8_0 down
     (32, (12, 12, 14), (12, 12, 14), 3, 1, 2),      # generic kernels forced
     (32, (12, 12, 14), (12, 12, 14), 3, 2, 2),      # single-launch path requested
 ], ids=["E256-T1", "E256-T16", "E64-q3k", "E16-noshared", "E300", "q8down", "generic", "single-launch"])

@@ -672,6 +672,110 @@ def bench_dequant(dev, reps: int, cpu_seconds: float) -> dict:
     return out_d
 
 
+def _delta_kernel_us(states, ins, outs, reps: int) -> float:
+    """Average duration of the DeltaNet kernel over reps eager passes of the
+    layers, from HIP events the runtime records at its start and end."""
+    import ctypes as C
+
+    import torch
+
+    from flash_moe_hip import _lib
+
+    lib, rt = _lib.load(), _hip_runtime()
+    n = reps * len(states)
+    ev = []
+    for _ in range(2 * n):
+        h = C.c_void_p()
+        if rt.hipEventCreate(C.byref(h)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        ev.append(h)
+    torch.cuda.synchronize()
+    for i in range(n):
+        l = i % len(states)
+        _lib.check(lib.mqh_profile_next_decode(ev[2 * i], ev[2 * i + 1], None, None), "mqh_profile_next_decode")
+        states[l].step(*ins[l], out=outs[l])
+    torch.cuda.synchronize()
+    us = []
+    for i in range(n):
+        v = C.c_float()
+        if rt.hipEventElapsedTime(C.byref(v), ev[2 * i], ev[2 * i + 1]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        us.append(v.value * 1e3)
+    for h in ev:
+        rt.hipEventDestroy(h)
+    return float(np.mean(us))
+
+
+def bench_deltanet(dev, reps: int, cpu_seconds: float) -> dict:
+    """The DeltaNet decode recurrence (moe_delta_heads) of the reference model's
+    recurrent layers: 30 layers, each a [32 heads x 128 x 128] FP32 state
+    (2 MiB) resident in HBM, one step per layer per token, all 30 captured as
+    one graph and replayed.  Bytes per step: the state read and written
+    (4 MiB); q, k, v, beta, gate are a few KiB."""
+    import torch
+
+    import oracle
+    from flash_moe_hip.native_expert import DeltaState
+
+    NL, NV, DV, DK = 30, 32, 128, 128
+    rng = np.random.default_rng(5)
+    host0 = (rng.standard_normal((NV, DV, DK)) * 0.01).astype(np.float32)
+    states = [DeltaState(NV, DV, DK, device=dev, state=host0 if l == 0 else
+                         (rng.standard_normal((NV, DV, DK)) * 0.01).astype(np.float32)) for l in range(NL)]
+    hins = []
+    for _ in range(NL):
+        hins.append(((rng.standard_normal((NV, DK)) * 0.05).astype(np.float32),
+                     (rng.standard_normal((NV, DK)) * 0.05).astype(np.float32),
+                     (rng.standard_normal((NV, DV)) * 0.1).astype(np.float32),
+                     rng.uniform(0.01, 0.99, NV).astype(np.float32),
+                     (-rng.uniform(0.001, 5, NV)).astype(np.float32)))
+    ins = [[torch.from_numpy(a).to(dev) for a in h] for h in hins]
+    outs = torch.empty((NL, NV, DV), dtype=torch.float32, device=dev)
+    # parity: one step of layer 0 against the oracle, bit for bit
+    states[0].step(*ins[0], out=outs[0])
+    torch.cuda.synchronize()
+    ref_state = host0.copy()
+    rc, want = oracle.delta_heads(ref_state, *hins[0])
+    exact = bool(rc == 0 and np.array_equal(outs[0].cpu().numpy(), want)
+                 and np.array_equal(states[0].state.cpu().numpy(), ref_state))
+
+    def sweep():
+        for l in range(NL):
+            states[l].step(*ins[l], out=outs[l])
+
+    ms = _time(_graph(sweep, dev), reps) / NL
+    kus = _delta_kernel_us(states, ins, outs, 4)
+    assert all(s.status() == 0 for s in states)
+    nbytes = 2 * NV * DV * DK * 4
+    log(f"deltanet: {ms * 1e3:.2f} us per layer step, kernel {kus:.2f} us, bit-exact {exact}")
+    out = {
+        "workload": f"DeltaNet decode step (moe_delta_heads): {NV} heads x {DV} x {DK} FP32 state per layer, "
+                    f"{NL} recurrent layers resident and rotated, one step per layer",
+        "metric": "state GB/s per layer step (state read + written)",
+        "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 3),
+        "bit_exact_vs_oracle": exact,
+        "roofline": _hbm_roofline("mqh::k_delta_heads<16>", nbytes, kus, read_floor_us(nbytes)),
+    }
+    if cpu_seconds > 0:
+        L = oracle.reference_delta_lib()
+        kind = "reference" if L is not None else "port"
+        fn = oracle.reference_delta_heads if L is not None else oracle.delta_heads
+        st = host0.copy()
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds:
+            fn(st, *hins[done % NL])
+            done += 1
+        dt = time.perf_counter() - t0
+        per = dt / done
+        out["cpu_baseline"] = {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+                               "us_per_layer": round(per * 1e6, 1),
+                               "sample": f"{done} steps of one [{NV}x{DV}x{DK}] state in {dt:.1f} s, one thread "
+                                         f"({'the reference kernel built from cpp/moe_delta.cpp' if L else 'the oracle'})"}
+    del states, ins, outs
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -682,6 +786,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch every step from Python instead of a graph")
     ap.add_argument("--only-decode", action="store_true", help="skip the batched-decode, prefill and dequant lines")
+    ap.add_argument("--workloads", default="batched_decode,prefill,dequant,deltanet",
+                    help="comma-separated workloads run after the headline decode")
     ap.add_argument("--extra-cpu-seconds", type=float, default=4.0)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (counter calibration)")
@@ -838,11 +944,14 @@ def main() -> int:
         del layers, graph
         torch.cuda.empty_cache()
         cpu_s = 0.0 if args.no_cpu_baseline else args.extra_cpu_seconds
-        result["workloads"] = {
-            "batched_decode": bench_batched_decode(dev, args.layers, args.steps // 4, cpu_s),
-            "prefill": bench_prefill(dev, 8, 20, cpu_s),
-            "dequant": bench_dequant(dev, 10, cpu_s),
+        wanted = set(args.workloads.split(","))
+        runs = {
+            "batched_decode": lambda: bench_batched_decode(dev, args.layers, args.steps // 4, cpu_s),
+            "prefill": lambda: bench_prefill(dev, 8, 20, cpu_s),
+            "dequant": lambda: bench_dequant(dev, 10, cpu_s),
+            "deltanet": lambda: bench_deltanet(dev, 50, cpu_s),
         }
+        result["workloads"] = {name: run() for name, run in runs.items() if name in wanted}
     print(json.dumps(result), flush=True)
     return 0
 

@@ -130,6 +130,27 @@ int mqh_moe_decode_routed(int gate_type, const void* gate, int up_type, const vo
  * counterpart in the reference (a profiling aid). */
 int mqh_last_route_kernels(void);
 
+/* One DeltaNet decode step for every head (replaces moe_delta_heads,
+ * cpp/moe_delta.cpp:18-69, bound by NativeDelta, src/flash_moe/native_expert.py:
+ * 76-97): state [heads x value_dim x key_dim] FP32 updated in place,
+ * q, k [heads x key_dim], v [heads x value_dim], beta, gate [heads],
+ * output [heads x value_dim].  Host pointers, same signature and codes: -1 for
+ * a null pointer or heads outside 1..256, key_dim or value_dim outside
+ * 1..1024; -2 when an output is not finite (every row's state is updated and
+ * every output written, where the reference stops at the first such row);
+ * -5 on a HIP failure.  The buffers are staged through HBM: the
+ * PCIe-inclusive compatibility path. */
+int moe_delta_heads(float* state, const float* q, const float* k, const float* v, const float* beta,
+                    const float* gate, float* output, int heads, int key_dim, int value_dim);
+
+/* moe_delta_heads on device pointers, enqueued on `stream`: the state stays
+ * resident in HBM across steps.  workspace (optional, zeroed once with
+ * mqh_workspace_init): a non-finite output latches, and mqh_status then
+ * returns -4.  Returns 0, -1 or -5. */
+int mqh_delta_heads(float* state, const float* q, const float* k, const float* v, const float* beta,
+                    const float* gate, float* output, int heads, int key_dim, int value_dim, void* workspace,
+                    void* stream);
+
 /* Bytes of workspace mqh_moe_prefill needs (has_shared: 0 or 1). */
 int64_t mqh_moe_prefill_workspace_bytes(int n_tokens, int top_k, int n_experts, int hidden, int intermediate,
                                         int has_shared);
@@ -199,7 +220,8 @@ int mqh_read_floor(const void* src, int64_t bytes, void* sink, void* start_event
 /* Profiling: record HIP events (hipEvent_t, any may be NULL) at the start and
  * end of the two GEMM kernels of the calling thread's next mqh_moe_decode,
  * moe_quant_expert or mqh_moe_prefill -- A: gate/up and SwiGLU, B: down
- * projection (with the weighted combine in decode).
+ * projection (with the weighted combine in decode) -- or of the one kernel of
+ * its next mqh_delta_heads (A; B is not recorded).
  * One-shot; the launch itself is unchanged.  No counterpart in the reference
  * (its timers are host wall clocks, bench_phases.py:45-56). */
 int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_stop);

@@ -236,6 +236,65 @@ int moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes, int
     return status;
 }
 
+int moe_delta_heads(float* state, const float* q, const float* k, const float* v, const float* beta,
+                    const float* gate, float* output, int heads, int key_dim, int value_dim) {
+    // validation of moe_delta.cpp:21-24
+    if (!state || !q || !k || !v || !beta || !gate || !output || heads < 1 || heads > 256 || key_dim < 1 ||
+        key_dim > 1024 || value_dim < 1 || value_dim > 1024)
+        return ST_ARG;
+    int status = ST_OK;
+    Ctx* c = acquire_ctx(status);
+    if (!c) return status;
+    // io: state | q | k | v | beta | gate | output | flags
+    const int64_t n_state = (int64_t)heads * value_dim * key_dim, n_qk = (int64_t)heads * key_dim;
+    const int64_t n_v = (int64_t)heads * value_dim;
+    const int64_t o_q = align256(n_state * 4), o_k = o_q + align256(n_qk * 4), o_v = o_k + align256(n_qk * 4);
+    const int64_t o_b = o_v + align256(n_v * 4), o_g = o_b + align256((int64_t)heads * 4);
+    const int64_t o_out = o_g + align256((int64_t)heads * 4), o_fl = o_out + align256(n_v * 4);
+    const int64_t total = o_fl + 256;
+    if (c->io.reserve(total) != hipSuccess) {
+        release_ctx(c);
+        return ST_HIP;
+    }
+    uint8_t* IO = (uint8_t*)c->io.ptr;
+    float* S = (float*)IO;
+    int* fl = (int*)(IO + o_fl);
+    const hipStream_t s = c->stream;
+    status = ST_HIP;
+    if (zero_words(fl, 3, s) == hipSuccess &&
+        hipMemcpyAsync(S, state, n_state * 4, hipMemcpyHostToDevice, s) == hipSuccess &&
+        hipMemcpyAsync(IO + o_q, q, n_qk * 4, hipMemcpyHostToDevice, s) == hipSuccess &&
+        hipMemcpyAsync(IO + o_k, k, n_qk * 4, hipMemcpyHostToDevice, s) == hipSuccess &&
+        hipMemcpyAsync(IO + o_v, v, n_v * 4, hipMemcpyHostToDevice, s) == hipSuccess &&
+        hipMemcpyAsync(IO + o_b, beta, (size_t)heads * 4, hipMemcpyHostToDevice, s) == hipSuccess &&
+        hipMemcpyAsync(IO + o_g, gate, (size_t)heads * 4, hipMemcpyHostToDevice, s) == hipSuccess &&
+        launch_delta_heads(S, (const float*)(IO + o_q), (const float*)(IO + o_k), (const float*)(IO + o_v),
+                           (const float*)(IO + o_b), (const float*)(IO + o_g), (float*)(IO + o_out), heads,
+                           key_dim, value_dim, fl, s, KernelEvents()) == hipSuccess &&
+        hipMemcpyAsync(state, S, n_state * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
+        hipMemcpyAsync(output, IO + o_out, n_v * 4, hipMemcpyDeviceToHost, s) == hipSuccess) {
+        status = read_and_clear_flags(fl, s);
+        if (status == ST_NONFINITE) status = -2;   // moe_delta.cpp:65
+    }
+    release_ctx(c);
+    return status;
+}
+
+int mqh_delta_heads(float* state, const float* q, const float* k, const float* v, const float* beta,
+                    const float* gate, float* output, int heads, int key_dim, int value_dim, void* workspace,
+                    void* stream) {
+    if (!state || !q || !k || !v || !beta || !gate || !output || heads < 1 || heads > 256 || key_dim < 1 ||
+        key_dim > 1024 || value_dim < 1 || value_dim > 1024)
+        return ST_ARG;
+    int* flags = workspace ? (int*)workspace : nullptr;   // the flag words lead every workspace
+    const KernelEvents ev = t_events;
+    t_events = KernelEvents();
+    return launch_delta_heads(state, q, k, v, beta, gate, output, heads, key_dim, value_dim, flags,
+                              (hipStream_t)stream, ev) == hipSuccess
+               ? ST_OK
+               : ST_HIP;
+}
+
 int mqh_dequant(int type, const void* src, void* dst, int64_t n, int want_f16, void* stream) {
     const int bs = block_size(type);
     if (bs == 0 || src == nullptr || dst == nullptr) return ST_ARG;

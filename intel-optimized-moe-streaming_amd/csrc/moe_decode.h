@@ -148,6 +148,9 @@ struct KernelEvents {
 };
 
 hipError_t launch_decode_generic(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev);
+hipError_t launch_delta_heads(float* state, const float* q, const float* k, const float* v, const float* beta,
+                              const float* gate, float* out, int heads, int key_dim, int value_dim, int* flags,
+                              hipStream_t stream, const KernelEvents& ev);
 bool fast_supported(const DecodeParams& p);
 FastLayout fast_layout(int inter);
 hipError_t launch_decode_fast(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev);

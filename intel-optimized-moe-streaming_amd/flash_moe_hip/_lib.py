@@ -20,6 +20,8 @@ EXPORTS = (
     "dequant_k_block_size",
     "dequant_k",
     "moe_quant_expert",
+    "moe_delta_heads",
+    "mqh_delta_heads",
     "mqh_dequant",
     "mqh_moe_workspace_bytes",
     "mqh_moe_decode",
@@ -69,6 +71,10 @@ def _declare(lib: C.CDLL) -> C.CDLL:
     lib.dequant_k.restype = _I
     lib.moe_quant_expert.argtypes = [_I, _P, _I64] * 3 + [_P, _I, _I, _P, _I]
     lib.moe_quant_expert.restype = _I
+    lib.moe_delta_heads.argtypes = [_P] * 7 + [_I] * 3
+    lib.moe_delta_heads.restype = _I
+    lib.mqh_delta_heads.argtypes = [_P] * 7 + [_I] * 3 + [_P, _P]
+    lib.mqh_delta_heads.restype = _I
     lib.mqh_dequant.argtypes = [_I, _P, _P, _I64, _I, _P]
     lib.mqh_dequant.restype = _I
     lib.mqh_moe_workspace_bytes.argtypes = [_I, _I, _I, _I]

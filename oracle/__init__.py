@@ -7,11 +7,15 @@ it and never falls back to it.
 
 Contents
 --------
-* ``liboracle_kquant.so`` (built from ``kquant_oracle.c`` by ``Makefile``): a C
-  restatement of the reference kernels ``cpp/dequant_k.cpp`` and
-  ``cpp/moe_quant_dot.cpp``.  Wrapped here as :func:`dequant_k` and
-  :func:`moe_quant_expert` with the reference's argument meaning and status
-  codes.
+* ``liboracle_kquant.so`` (built from ``kquant_oracle.c`` and ``delta_oracle.c``
+  by ``Makefile``): a C restatement of the reference kernels
+  ``cpp/dequant_k.cpp``, ``cpp/moe_quant_dot.cpp`` and ``cpp/moe_delta.cpp``.
+  Wrapped here as :func:`dequant_k`, :func:`moe_quant_expert` and
+  :func:`delta_heads` with the reference's argument meaning and status codes.
+* ``_ref/libref_delta.so`` (``make ref``, only where the reference tree is
+  present; never committed): the reference's own ``cpp/moe_delta.cpp`` compiled
+  from its source, the second check of :func:`delta_heads` and the CPU baseline
+  of the DeltaNet bench line (:func:`reference_delta_lib`).
 * NumPy restatements of the Python semantics around the kernels:
   :func:`route` (``src/flash_moe/router.py:140-170``), :func:`combine`
   (``src/flash_moe/moe_layer.py:70-106``), :func:`shared_expert_forward`
@@ -30,6 +34,8 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle_kquant.so"
+REF_DELTA_PATH = HERE / "_ref" / "libref_delta.so"
+REFERENCE_TREE = Path("/root/reference")
 
 BLOCK = {8: (32, 34), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
 
@@ -37,8 +43,11 @@ _lib = None
 
 
 def build() -> Path:
-    """Compile the C restatement (make -C oracle)."""
+    """Compile the C restatement (make -C oracle) and, where the reference tree
+    is present, the reference's DeltaNet kernel into _ref/ (make ref)."""
     subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    if (REFERENCE_TREE / "cpp" / "moe_delta.cpp").is_file():
+        subprocess.run(["make", "-s", "-C", str(HERE), "ref", f"REFERENCE={REFERENCE_TREE}"], check=True)
     return LIB_PATH
 
 
@@ -59,6 +68,8 @@ def lib() -> C.CDLL:
         L.oracle_f32_to_f16.restype = C.c_uint16
         L.oracle_f16_to_f32.argtypes = [C.c_uint16]
         L.oracle_f16_to_f32.restype = C.c_float
+        L.oracle_delta_heads.argtypes = [C.c_void_p] * 7 + [C.c_int] * 3
+        L.oracle_delta_heads.restype = C.c_int
         L.oracle_f32_to_f16_array.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
         L.oracle_f16_to_f32_array.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
         _lib = L
@@ -124,6 +135,53 @@ def expert_forward(tensors, kinds, x, hidden, intermediate, fp16_graph=0) -> np.
 
 
 # ------------------------------------------------------------ Python semantics
+
+def _delta_call(fn, state: np.ndarray, q, k, v, beta, gate):
+    if state.dtype != np.float32 or not state.flags.c_contiguous or state.ndim != 3:
+        raise ValueError("state must be a contiguous FP32 [heads, value_dim, key_dim] array")
+    nv, dv, dk = state.shape
+    arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v, beta, gate)]
+    shapes = [(nv, dk), (nv, dk), (nv, dv), (nv,), (nv,)]
+    if any(a.shape != s_ for a, s_ in zip(arrs, shapes)):
+        raise ValueError("DeltaNet input shape mismatch")
+    out = np.zeros((nv, dv), np.float32)
+    rc = fn(state.ctypes.data, *[a.ctypes.data for a in arrs], out.ctypes.data, nv, dk, dv)
+    return rc, out
+
+
+def delta_heads(state: np.ndarray, q, k, v, beta, gate):
+    """``moe_delta_heads`` (cpp/moe_delta.cpp:18-69): one delta-rule step of every
+    head, ``state`` [heads, value_dim, key_dim] FP32 updated in place.  Returns
+    (status, output [heads, value_dim])."""
+    return _delta_call(lib().oracle_delta_heads, state, q, k, v, beta, gate)
+
+
+def reference_delta_lib():
+    """The reference's moe_delta_heads built from its source (oracle/_ref), or None."""
+    if not REF_DELTA_PATH.exists():
+        return None
+    L = C.CDLL(str(REF_DELTA_PATH))
+    L.moe_delta_heads.argtypes = [C.c_void_p] * 7 + [C.c_int] * 3
+    L.moe_delta_heads.restype = C.c_int
+    return L
+
+
+def reference_delta_heads(state: np.ndarray, q, k, v, beta, gate):
+    """Like :func:`delta_heads`, through the reference's own compiled kernel."""
+    L = reference_delta_lib()
+    if L is None:
+        raise FileNotFoundError(f"{REF_DELTA_PATH} is not built (make -C oracle ref)")
+    return _delta_call(L.moe_delta_heads, state, q, k, v, beta, gate)
+
+
+def delta_step_numpy(S: np.ndarray, q, k, v, beta: float, gate: float) -> np.ndarray:
+    """The closed form of one head's step (gated_deltanet.py:264-298, arXiv
+    2412.06464 eq. 10) in float64: S <- exp(gate) S; S <- S + beta (v - S k) k^T;
+    out = S q.  Updates S (float64) in place and returns out."""
+    S *= np.exp(gate)
+    S += np.outer(beta * (v - S @ k), k)
+    return S @ q
+
 
 def route(x, router_w: np.ndarray, top_k: int):
     """``ExpertRouter.route`` (router.py:140-170): FP32 scores ``x @ W`` with W

@@ -127,3 +127,19 @@ def test_route_validation(lib):
     assert call(k=0) == -1
     assert call(k=65) == -1                   # one selected score per lane
     assert call(e=4, k=5) == -1               # more slots than experts
+
+
+def test_delta_heads_validation(lib):
+    p = C.c_void_p(256)
+    ok = dict(st=p, q=p, k=p, v=p, b=p, g=p, o=p, h=32, dk=128, dv=128)
+
+    def call(fn, **kw):
+        a = {**ok, **kw}
+        args = [a["st"], a["q"], a["k"], a["v"], a["b"], a["g"], a["o"], a["h"], a["dk"], a["dv"]]
+        return fn(*args) if fn is lib.moe_delta_heads else fn(*args, None, None)
+
+    for fn in (lib.moe_delta_heads, lib.mqh_delta_heads):
+        for key in ("st", "q", "k", "v", "b", "g", "o"):
+            assert call(fn, **{key: None}) == -1
+        for kw in (dict(h=0), dict(h=257), dict(dk=0), dict(dk=1025), dict(dv=0), dict(dv=1025)):
+            assert call(fn, **kw) == -1          # moe_delta.cpp:21-24

@@ -17,7 +17,8 @@
  *     out-of-range expert ids) are latched in the caller's workspace and
  *     reported by mqh_status().
  *
- * GGML type ids: Q8_0 = 8, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14.
+ * GGML type ids: Q8_0 = 8, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14
+ * (dequant_k, moe_quant_expert); the device entry points also IQ4_NL = 20.
  * Quantized matrices are GGUF row-major: rows = output features, each row a
  * run of (cols / block_size) blocks.  A stacked expert tensor holds
  * n_experts such matrices back to back, exactly as a GGUF *_exps tensor.
@@ -72,12 +73,25 @@ int moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes,
                      const float* input, int hidden, int intermediate,
                      float* output, int fp16_graph);
 
+/* IQ4_NL to FP32, replacing the reference's IQ4_NL library
+ * (cpp/fast_dequant.cpp:40-65 dequantize_iq4_nl_cpp and
+ * cpp/fast_dequant_avx2.cpp:100-116 dequantize_iq4_nl_avx2, bound by
+ * run_native_int4_openvino.py:35,98): rows x (cols / 32) 18-byte blocks (FP16
+ * scale, 16 bytes of 4-bit indices: low nibbles give values 0..15, high
+ * nibbles 16..31), value = scale * table[index] with the reference's own
+ * 16-entry table; output row r at dst + r * cols, columns past the last whole
+ * block untouched.  Host pointers, staged through HBM; no status, as in the
+ * reference (a call it cannot run leaves dst untouched). */
+void dequantize_iq4_nl_cpp(const uint8_t* src_bytes, float* dst, int rows, int cols);
+void dequantize_iq4_nl_avx2(const uint8_t* src_bytes, float* dst, int rows, int cols);
+
 /* ------------------------------------------------------------------------ */
 /* 2. Device-resident entry points                                           */
 /* ------------------------------------------------------------------------ */
 
 /* Device form of dequant_k for weights already in HBM (the conversion that
- * dequant_to_f16, src/run_q4k_f16_openvino.py:62-85, performs on the host).
+ * dequant_to_f16, src/run_q4k_f16_openvino.py:62-85, performs on the host),
+ * for the five types and IQ4_NL (FP16 output: RN_f16 of the FP32 value).
  * `dst` must be 16-byte aligned.  Returns 0, -1 or -5. */
 int mqh_dequant(int type, const void* src, void* dst, int64_t n, int want_f16, void* stream);
 
@@ -94,7 +108,9 @@ int64_t mqh_moe_workspace_bytes(int n_tokens, int top_k, int intermediate, int s
  * [n_tokens x top_k] (int32, FP32) in top-k order; x and y [n_tokens x
  * hidden] FP32.  The shared expert is optional (sh_gate == NULL: none;
  * sh_gate_inp == NULL: no sigmoid scale).  fp16_graph applies to the routed
- * experts.  The workspace must hold mqh_moe_workspace_bytes(...) bytes and be
+ * experts.  Types: the five of moe_quant_expert and IQ4_NL (the latter, like
+ * the FP16 graph, through the FP32 generic kernels).
+ * The workspace must hold mqh_moe_workspace_bytes(...) bytes and be
  * zeroed once (mqh_workspace_init) before first use.  Returns 0, -1, -2, -5
  * or -6; kernel-side faults are read with mqh_status. */
 int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,

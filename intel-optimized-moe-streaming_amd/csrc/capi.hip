@@ -17,7 +17,10 @@ namespace {
 constexpr int ST_OK = 0, ST_ARG = -1, ST_TYPE = -2, ST_BYTES = -3, ST_NONFINITE = -4, ST_HIP = -5,
               ST_WORKSPACE = -6, ST_TIMEOUT = -7, ST_BAD_ID = -9;
 
-bool supported(int t) { return block_size(t) != 0; }
+// dequant_k and moe_quant_expert accept the reference's five types; the
+// device entry points also IQ4_NL
+bool supported(int t) { return reference_type(t); }
+bool device_supported(int t) { return reference_type(t) || t == T_IQ4_NL; }
 
 // 0: the two integer-digit kernels when the shapes allow them, else the
 // generic kernels; 1: always the generic kernels; 2: the single-launch kernel
@@ -137,8 +140,10 @@ int read_and_clear_flags(int* flags_dev, hipStream_t s) {
 }
 
 // Validate shapes and types of one expert triple.  Returns 0 or a status.
-int check_expert_types(int gt, int ut, int dt, int hidden, int inter) {
-    if (!supported(gt) || !supported(ut) || !supported(dt)) return ST_TYPE;
+int check_expert_types(int gt, int ut, int dt, int hidden, int inter, bool device = false) {
+    if (device ? !(device_supported(gt) && device_supported(ut) && device_supported(dt))
+               : !(supported(gt) && supported(ut) && supported(dt)))
+        return ST_TYPE;
     if (hidden % block_size(gt) || hidden % block_size(ut) || inter % block_size(dt)) return ST_TYPE;
     return ST_OK;
 }
@@ -149,10 +154,10 @@ extern "C" {
 
 int dequant_k_supported(int type) { return supported(type) ? 1 : 0; }
 
-int dequant_k_block_size(int type) { return block_size(type); }
+int dequant_k_block_size(int type) { return supported(type) ? block_size(type) : 0; }
 
 int dequant_k(int type, const uint8_t* src, void* dst, int64_t n, int want_f16) {
-    const int bs = block_size(type);
+    const int bs = supported(type) ? block_size(type) : 0;
     if (bs == 0 || src == nullptr || dst == nullptr) return ST_ARG;
     if (n <= 0 || n % bs != 0) return ST_ARG;
     int status = ST_OK;
@@ -295,8 +300,37 @@ int mqh_delta_heads(float* state, const float* q, const float* k, const float* v
                : ST_HIP;
 }
 
+void dequantize_iq4_nl_cpp(const uint8_t* src_bytes, float* dst, int rows, int cols) {
+    // fast_dequant.cpp:40-65: rows x (cols / 32) blocks, row r of the output at
+    // dst + r * cols; no status (a call it cannot run leaves dst untouched)
+    if (!src_bytes || !dst || rows <= 0 || cols < 32) return;
+    const int bpr = cols / 32;
+    const int64_t n = (int64_t)rows * bpr * 32;
+    int status = ST_OK;
+    Ctx* c = acquire_ctx(status);
+    if (!c) return;
+    const size_t in_bytes = (size_t)rows * bpr * 18;
+    if (c->w.reserve(in_bytes) == hipSuccess && c->io.reserve((size_t)n * 4) == hipSuccess &&
+        hipMemcpyAsync(c->w.ptr, src_bytes, in_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
+        launch_dequant(T_IQ4_NL, (const uint8_t*)c->w.ptr, c->io.ptr, n, 0, c->stream) == hipSuccess) {
+        // rows land cols floats apart; the columns past bpr * 32 stay as they were
+        if (cols % 32 == 0)
+            (void)hipMemcpyAsync(dst, c->io.ptr, (size_t)n * 4, hipMemcpyDeviceToHost, c->stream);
+        else
+            (void)hipMemcpy2DAsync(dst, (size_t)cols * 4, c->io.ptr, (size_t)bpr * 128, (size_t)bpr * 128,
+                                   (size_t)rows, hipMemcpyDeviceToHost, c->stream);
+        (void)hipStreamSynchronize(c->stream);
+    }
+    release_ctx(c);
+}
+
+void dequantize_iq4_nl_avx2(const uint8_t* src_bytes, float* dst, int rows, int cols) {
+    // fast_dequant_avx2.cpp:100-116 computes the same values as the scalar export
+    dequantize_iq4_nl_cpp(src_bytes, dst, rows, cols);
+}
+
 int mqh_dequant(int type, const void* src, void* dst, int64_t n, int want_f16, void* stream) {
-    const int bs = block_size(type);
+    const int bs = device_supported(type) ? block_size(type) : 0;
     if (bs == 0 || src == nullptr || dst == nullptr) return ST_ARG;
     if (n <= 0 || n % bs != 0 || ((uintptr_t)dst & 15)) return ST_ARG;
     return launch_dequant(type, (const uint8_t*)src, dst, n, want_f16, (hipStream_t)stream) == hipSuccess ? ST_OK
@@ -339,14 +373,14 @@ int decode_params(int gate_type, const void* gate, int up_type, const void* up, 
     if (top_k > 0) {
         if (!gate || !up || !down || !ids || !weights) return ST_ARG;
         if (n_experts <= 0 || intermediate <= 0 || intermediate > 65536) return ST_ARG;
-        st = check_expert_types(gate_type, up_type, down_type, hidden, intermediate);
+        st = check_expert_types(gate_type, up_type, down_type, hidden, intermediate, true);
         if (st) return st;
     } else {
         intermediate = 0;
     }
     if (has_shared) {
         if (!sh_up || !sh_down || sh_intermediate <= 0 || sh_intermediate > 65536) return ST_ARG;
-        st = check_expert_types(sh_gate_type, sh_up_type, sh_down_type, hidden, sh_intermediate);
+        st = check_expert_types(sh_gate_type, sh_up_type, sh_down_type, hidden, sh_intermediate, true);
         if (st) return st;
     }
     const WorkspaceLayout wl = decode_workspace_layout(n_tokens, top_k, intermediate, has_shared ? sh_intermediate : 0);

@@ -75,6 +75,7 @@ static hipError_t launch_t(const uint8_t* src, void* dst, int64_t n, int want_f1
 hipError_t launch_dequant(int type, const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream) {
     switch (type) {
         case T_Q8_0: return launch_t<T_Q8_0>(src, dst, n, want_f16, stream);
+        case T_IQ4_NL: return launch_t<T_IQ4_NL>(src, dst, n, want_f16, stream);
         case T_Q3_K: return launch_t<T_Q3_K>(src, dst, n, want_f16, stream);
         case T_Q4_K: return launch_t<T_Q4_K>(src, dst, n, want_f16, stream);
         case T_Q5_K: return launch_t<T_Q5_K>(src, dst, n, want_f16, stream);

@@ -30,14 +30,22 @@
 
 namespace mqh {
 
-enum : int { T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
+enum : int { T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_NL = 20 };
 
 __host__ __device__ constexpr int block_size(int t) {
-    return t == T_Q8_0 ? 32 : (t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 256 : 0;
+    return (t == T_Q8_0 || t == T_IQ4_NL) ? 32 : (t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 256 : 0;
 }
 
 __host__ __device__ constexpr int block_bytes(int t) {
-    return t == T_Q8_0 ? 34 : t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : 0;
+    return t == T_Q8_0 ? 34 : t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210
+         : t == T_IQ4_NL ? 18 : 0;
+}
+
+// The five types of the reference's dequant_k and moe_quant_expert
+// (cpp/dequant_k.cpp:342-348); IQ4_NL is decoded by the device entry points
+// only, as the reference decodes it in a library of its own.
+__host__ __device__ constexpr bool reference_type(int t) {
+    return t == T_Q8_0 || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K;
 }
 
 // ------------------------------------------------------------------ loads
@@ -94,6 +102,32 @@ __device__ __forceinline__ void decode8<T_Q8_0>(const uint8_t* blk, int t, float
     const uint64_t w = ld_u64(blk + 2 + 8 * t);
 #pragma unroll
     for (int k = 0; k < 8; ++k) out[k] = __fmul_rn((float)(int8_t)byte_of(w, k), d);
+}
+
+// IQ4_NL: an FP16 scale, then 16 bytes of 4-bit indices into a 16-entry table;
+// values 0..15 are the low nibbles of bytes 0..15, values 16..31 the high
+// nibbles, each scale * table[index] rounded once (cpp/fast_dequant.cpp:40-65,
+// fast_dequant_avx2.cpp:80-97).  The table is the reference's own constants
+// (fast_dequant.cpp:4-9), which are not gguf's kvalues_iq4nl / 127: the output
+// follows the reference library this replaces.
+__host__ __device__ constexpr float IQ4NL_TABLE[16] = {
+    -1.0f, -0.6961914f, -0.515625f, -0.375f, -0.25390625f, -0.1484375f, -0.0546875f, 0.02734375f,
+    0.1015625f, 0.1796875f, 0.265625f, 0.359375f, 0.46875f, 0.59765625f, 0.7578125f, 1.0f};
+
+// table[i] for a 4-bit i, selected in registers (no memory access)
+__device__ __forceinline__ float iq4nl_value(uint32_t i) {
+    float r = IQ4NL_TABLE[0];
+#pragma unroll
+    for (uint32_t k = 1; k < 16; ++k) r = i == k ? IQ4NL_TABLE[k] : r;
+    return r;
+}
+
+template <>
+__device__ __forceinline__ void decode8<T_IQ4_NL>(const uint8_t* blk, int t, float out[8]) {
+    const float d = h2f(ld_u16(blk));
+    const uint64_t w = ld_u64(blk + 2 + 8 * (t & 1)) >> (4 * (t >> 1));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = __fmul_rn(d, iq4nl_value(byte_of(w, k) & 15u));
 }
 
 // Scale and min j (0..7) of Q4_K/Q5_K from header dwords h1..h3 (scale bytes
@@ -180,6 +214,7 @@ __device__ __forceinline__ void decode8<T_Q3_K>(const uint8_t* blk, int t, float
 __device__ __forceinline__ void decode8_any(int type, const uint8_t* blk, int t, float out[8]) {
     switch (type) {
         case T_Q8_0: decode8<T_Q8_0>(blk, t, out); break;
+        case T_IQ4_NL: decode8<T_IQ4_NL>(blk, t, out); break;
         case T_Q3_K: decode8<T_Q3_K>(blk, t, out); break;
         case T_Q4_K: decode8<T_Q4_K>(blk, t, out); break;
         case T_Q5_K: decode8<T_Q5_K>(blk, t, out); break;

@@ -54,7 +54,7 @@ __device__ __forceinline__ RowMap row_map(int cols) {
     return m;
 }
 
-__device__ __forceinline__ int ppb_of(int type) { return type == T_Q8_0 ? 1 : 8; }
+__device__ __forceinline__ int ppb_of(int type) { return block_size(type) / 32; }
 
 // Partial dot product of the parts a lane owns, against values in registers
 // (NK > 0) or read from `xmem` (NK == 0).

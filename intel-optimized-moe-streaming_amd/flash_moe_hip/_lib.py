@@ -22,6 +22,8 @@ EXPORTS = (
     "moe_quant_expert",
     "moe_delta_heads",
     "mqh_delta_heads",
+    "dequantize_iq4_nl_cpp",
+    "dequantize_iq4_nl_avx2",
     "mqh_dequant",
     "mqh_moe_workspace_bytes",
     "mqh_moe_decode",
@@ -75,6 +77,10 @@ def _declare(lib: C.CDLL) -> C.CDLL:
     lib.moe_delta_heads.restype = _I
     lib.mqh_delta_heads.argtypes = [_P] * 7 + [_I] * 3 + [_P, _P]
     lib.mqh_delta_heads.restype = _I
+    lib.dequantize_iq4_nl_cpp.argtypes = [_P, _P, _I, _I]
+    lib.dequantize_iq4_nl_cpp.restype = None
+    lib.dequantize_iq4_nl_avx2.argtypes = [_P, _P, _I, _I]
+    lib.dequantize_iq4_nl_avx2.restype = None
     lib.mqh_dequant.argtypes = [_I, _P, _P, _I64, _I, _P]
     lib.mqh_dequant.restype = _I
     lib.mqh_moe_workspace_bytes.argtypes = [_I, _I, _I, _I]

@@ -9,7 +9,12 @@ Host API, same names and meaning as the reference:
   * ``GGML_BLOCK_INFO``, ``name_of``, ``is_aligned``, ``max_relative_error``
     (``src/flash_moe/dequant.py:30-50,74-83,198-202``).
 
-Device API: ``dequant_device`` decodes a uint8 CUDA tensor already in HBM.
+``dequantize_iq4_nl(raw, rows, cols)`` is the reference's IQ4_NL library call
+(``dequantize_iq4_nl_avx2``, ``run_native_int4_openvino.py:94-99``): its
+16-entry table (``cpp/fast_dequant.cpp:4-9``), not gguf's.
+
+Device API: ``dequant_device`` decodes a uint8 CUDA tensor already in HBM
+(the five types above and IQ4_NL).
 """
 from __future__ import annotations
 
@@ -19,7 +24,7 @@ from . import _lib
 from .quant_types import GGML_BLOCK_INFO, block_info, name_of
 
 __all__ = ["GGML_BLOCK_INFO", "name_of", "is_aligned", "dequant_to_f16", "dequantize", "dequantize_to",
-           "dequant_device", "max_relative_error"]
+           "dequantize_iq4_nl", "dequant_device", "max_relative_error"]
 
 
 def is_aligned(ggml_type: int, nbytes: int) -> bool:
@@ -84,6 +89,16 @@ def dequantize_to(raw, ggml_type: int, dtype: str = "f16", shape: tuple[int, ...
     bs, pb = block_info(ggml_type)
     out = dequant_to_f16(data, ggml_type, data.nbytes // pb * bs)
     return out.reshape(*shape) if shape is not None else out
+
+
+def dequantize_iq4_nl(raw, rows: int, cols: int) -> np.ndarray:
+    """[rows x cols] FP32 from rows * (cols // 32) IQ4_NL blocks (18 bytes each)."""
+    src = _as_bytes(raw)
+    if rows <= 0 or cols <= 0 or cols % 32 or src.nbytes < rows * (cols // 32) * 18:
+        raise ValueError(f"{src.nbytes} bytes cannot hold [{rows} x {cols}] IQ4_NL values")
+    dst = np.empty((rows, cols), dtype=np.float32)
+    _lib.load().dequantize_iq4_nl_avx2(src.ctypes.data, dst.ctypes.data, int(rows), int(cols))
+    return dst
 
 
 def dequant_device(src, ggml_type: int, n_elements: int | None = None, dtype=None, out=None, stream=None):

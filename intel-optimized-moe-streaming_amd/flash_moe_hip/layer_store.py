@@ -16,7 +16,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from .quant_types import SUPPORTED_TYPES, name_of, tensor_bytes
+from .quant_types import DEVICE_TYPES, name_of, tensor_bytes
 
 ROLES = ("gate", "up", "down")
 
@@ -55,7 +55,7 @@ class ExpertLayer:
 
         self.types = {r: int(types[r]) for r in ROLES}
         for r in ROLES:
-            if self.types[r] not in SUPPORTED_TYPES:
+            if self.types[r] not in DEVICE_TYPES:
                 raise ValueError(f"{r}: unsupported ggml type {self.types[r]}")
         self.n_experts, self.hidden, self.intermediate = int(n_experts), int(hidden), int(intermediate)
         self.tensors = {"gate": gate, "up": up, "down": down}

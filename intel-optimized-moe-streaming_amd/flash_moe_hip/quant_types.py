@@ -7,10 +7,15 @@ they are the same numbers as ``src/flash_moe/dequant.py:30-50`` (by name) and
 from __future__ import annotations
 
 GGML_TYPE_IDS: dict[str, int] = {"Q8_0": 8, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
-TYPE_NAMES: dict[int, str] = {v: k for k, v in GGML_TYPE_IDS.items()}
+IQ4_NL = 20
+TYPE_NAMES: dict[int, str] = {**{v: k for k, v in GGML_TYPE_IDS.items()}, IQ4_NL: "IQ4_NL"}
 
-# The types the HIP kernels decode (native_expert.py:10 lists the same five).
+# The types of the reference's native expert (native_expert.py:10 lists the
+# same five): what NativeExpert / load_native_expert accept.
 SUPPORTED_TYPES = frozenset(GGML_TYPE_IDS.values())
+# What the device entry points decode: the five plus IQ4_NL (the reference's
+# fast_dequant library, cpp/fast_dequant.cpp:40-65).
+DEVICE_TYPES = SUPPORTED_TYPES | {IQ4_NL}
 
 # name -> (block_size, bytes_per_block) for every GGUF type the reference names.
 GGML_BLOCK_INFO: dict[str, tuple[int, int]] = {

@@ -19,7 +19,7 @@ import numpy as np
 from .quant_types import GGML_TYPE_IDS, block_info
 
 # byte offsets of the FP16 scale fields per type: (d, dmin or None)
-SCALE_FIELDS = {8: (0, None), 11: (108, None), 12: (0, 2), 13: (0, 2), 14: (208, None)}
+SCALE_FIELDS = {8: (0, None), 11: (108, None), 12: (0, 2), 13: (0, 2), 14: (208, None), 20: (0, None)}
 
 
 def tensor_nbytes(ggml_type: int, rows: int, cols: int) -> int:

@@ -37,7 +37,8 @@ LIB_PATH = HERE / "liboracle_kquant.so"
 REF_DELTA_PATH = HERE / "_ref" / "libref_delta.so"
 REFERENCE_TREE = Path("/root/reference")
 
-BLOCK = {8: (32, 34), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+BLOCK = {8: (32, 34), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18)}
+IQ4_NL = 20
 
 _lib = None
 
@@ -68,6 +69,8 @@ def lib() -> C.CDLL:
         L.oracle_f32_to_f16.restype = C.c_uint16
         L.oracle_f16_to_f32.argtypes = [C.c_uint16]
         L.oracle_f16_to_f32.restype = C.c_float
+        L.oracle_dequantize_iq4_nl.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+        L.oracle_dequantize_iq4_nl.restype = None
         L.oracle_delta_heads.argtypes = [C.c_void_p] * 7 + [C.c_int] * 3
         L.oracle_delta_heads.restype = C.c_int
         L.oracle_f32_to_f16_array.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
@@ -99,11 +102,26 @@ def dequant_k(ggml_type: int, raw, n: int, want_f16: bool = False):
     return rc, out
 
 
+def dequantize_iq4_nl(raw, rows: int, cols: int) -> np.ndarray:
+    """``dequantize_iq4_nl_cpp`` (cpp/fast_dequant.cpp:40-65): [rows x cols] FP32."""
+    src = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
+    if src.size < rows * (cols // 32) * 18:
+        raise ValueError("not enough IQ4_NL blocks")
+    out = np.zeros((rows, cols), np.float32)
+    lib().oracle_dequantize_iq4_nl(src.ctypes.data, out.ctypes.data, int(rows), int(cols))
+    return out
+
+
 def dequant(ggml_type: int, raw, n: int | None = None, want_f16: bool = False) -> np.ndarray:
+    """Values of a flat run of blocks, FP32 or RN_f16 (IQ4_NL through the
+    reference's IQ4_NL library semantics, the rest through dequant_k)."""
     src = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
     bs, pb = BLOCK[int(ggml_type)]
     if n is None:
         n = src.size // pb * bs
+    if int(ggml_type) == IQ4_NL:
+        vals = dequantize_iq4_nl(src, n // 32, 32).reshape(-1)
+        return f32_to_f16_bits(vals).view(np.float16) if want_f16 else vals
     rc, out = dequant_k(ggml_type, src, n, want_f16)
     if rc != 0:
         raise RuntimeError(f"oracle dequant_k failed with status {rc}")

@@ -327,3 +327,30 @@ int oracle_moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_byt
     free(act);
     return status;
 }
+
+/* ------------------------------------------ IQ4_NL (cpp/fast_dequant.cpp:40-65) */
+
+/* The reference library's 16-entry table, its own constants
+ * (fast_dequant.cpp:4-9, fast_dequant_avx2.cpp:34-39); not gguf's
+ * kvalues_iq4nl / 127. */
+static const float IQ4NL_TABLE[16] = {-1.0f,     -0.6961914f, -0.515625f, -0.375f,     -0.25390625f, -0.1484375f,
+                                      -0.0546875f, 0.02734375f, 0.1015625f, 0.1796875f, 0.265625f,    0.359375f,
+                                      0.46875f,    0.59765625f, 0.7578125f, 1.0f};
+
+/* rows x (cols / 32) 18-byte blocks: FP16 scale d, then qs[16]; value i
+ * (0..15) = d * table[qs[i] & 15], value 16 + i = d * table[qs[i] >> 4];
+ * output row r at dst + r * cols. */
+void oracle_dequantize_iq4_nl(const uint8_t* src, float* dst, int rows, int cols) {
+    const int bpr = cols / 32;
+    for (int r = 0; r < rows; ++r) {
+        for (int b = 0; b < bpr; ++b) {
+            const uint8_t* blk = src + ((int64_t)r * bpr + b) * 18;
+            const float d = ld_f16(blk);
+            float* out = dst + (int64_t)r * cols + 32 * b;
+            for (int i = 0; i < 16; ++i) {
+                out[i] = d * IQ4NL_TABLE[blk[2 + i] & 15];
+                out[i + 16] = d * IQ4NL_TABLE[blk[2 + i] >> 4];
+            }
+        }
+    }
+}

@@ -143,3 +143,13 @@ def test_delta_heads_validation(lib):
             assert call(fn, **{key: None}) == -1
         for kw in (dict(h=0), dict(h=257), dict(dk=0), dict(dk=1025), dict(dv=0), dict(dv=1025)):
             assert call(fn, **kw) == -1          # moe_delta.cpp:21-24
+
+
+def test_iq4_nl_stays_outside_the_reference_contracts(lib):
+    # dequant_k and moe_quant_expert keep the reference's five types
+    # (dequant_k.cpp:342-348); IQ4_NL has its own exports and the device paths
+    assert lib.dequant_k_supported(20) == 0
+    assert lib.dequant_k_block_size(20) == 0
+    buf = np.zeros(18, np.uint8)
+    out = np.zeros(32, np.float32)
+    assert lib.dequant_k(20, buf.ctypes.data, out.ctypes.data, 32, 0) == -1

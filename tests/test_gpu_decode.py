@@ -322,3 +322,47 @@ def test_shared_expert_q6k_with_other_routed_types(hip, oracle_mod, routed):
             want = oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist())
             assert oracle_mod.max_relative_error(got[tok], want) <= TOL, (routed, T, tok)
             assert oracle_mod.max_relative_error(got[tok], gen[tok]) <= TOL, (routed, T, tok)
+
+
+def _f64_expert(oracle_mod, tensors, types, x, H, I):
+    g = oracle_mod.dequant(types["gate"], tensors["gate"]).astype(np.float64).reshape(I, H)
+    u = oracle_mod.dequant(types["up"], tensors["up"]).astype(np.float64).reshape(I, H)
+    d = oracle_mod.dequant(types["down"], tensors["down"]).astype(np.float64).reshape(H, I)
+    gx, ux = g @ x.astype(np.float64), u @ x.astype(np.float64)
+    return d @ (gx / (1.0 + np.exp(-gx)) * ux)
+
+
+@pytest.mark.parametrize("types", [(20, 20), (12, 20), (20, 14)])
+def test_iq4_nl_layer(hip, oracle_mod, types):
+    """IQ4_NL experts (the reference decodes IQ4_NL in its fast_dequant library
+    and runs the matmuls elsewhere) through the fused decode, against the
+    float64 SwiGLU of the oracle-dequantized weights: routed and shared
+    experts, 3 tokens, and the routed-on-device form."""
+    import torch
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    gu, dn = types
+    t = {"gate": gu, "up": gu, "down": dn}
+    E, H, I = 6, 512, 256
+    layer, host, shared = make_layer(41 + gu + dn, E, H, I, t, shared_types=t)
+    rng = np.random.default_rng(43)
+    X = rng.standard_normal((3, H)).astype(np.float32)
+    ids = np.array([[0, 5, 2], [3, 3, 1], [4, 0, 5]])
+    ws = np.array([[0.5, 0.3, 0.2], [0.6, 0.2, 0.2], [0.4, 0.4, 0.2]])
+    print(f"iq4_nl types={types}", flush=True)
+    got, st = run(layer, X, ids, ws)
+    assert st == 0
+    sh_t = {r: shared[r] for r in ROLES}
+    for tok in range(3):
+        ys = [_f64_expert(oracle_mod, host_expert(host, layer, int(e)), t, X[tok], H, I) for e in ids[tok]]
+        gate = 1.0 / (1.0 + np.exp(-float(X[tok].astype(np.float64) @ shared["gate_inp"])))
+        want = sum(float(w) * y for w, y in zip(ws[tok], ys)) + gate * _f64_expert(oracle_mod, sh_t, t, X[tok], H, I)
+        err = oracle_mod.max_relative_error(got[tok], want.astype(np.float32))
+        assert err <= TOL, (types, tok, err)
+    layer.router_weights = (rng.standard_normal((H, E)) * 0.05).astype(np.float32)
+    runner = MoeRunner()
+    y, rid, rw = runner.decode_routed(layer, torch.from_numpy(X).cuda(), 3)
+    torch.cuda.synchronize()
+    assert runner.status() == 0
+    y2 = runner.decode(layer, torch.from_numpy(X).cuda(), rid, rw)
+    np.testing.assert_array_equal(y.cpu().numpy(), y2.cpu().numpy())

@@ -118,3 +118,55 @@ def test_read_floor_kernel(hip):
     assert hip.mqh_read_floor(buf.data_ptr() + 4, 1 << 12, None, None, None, stream) == -1
     assert hip.mqh_read_floor(buf.data_ptr(), 1000, None, None, None, stream) == -1
     assert hip.mqh_read_floor(None, 1 << 12, None, None, None, stream) == -1
+
+
+def _iq4nl_blocks(n, seed):
+    from flash_moe_hip.synthetic import random_blocks as bench_blocks
+
+    rng = np.random.default_rng(seed)
+    b = bench_blocks(rng, 20, n)
+    edge = np.zeros((6, 18), np.uint8)
+    edge[:, 2:] = rng.integers(0, 256, size=(6, 16), dtype=np.uint8)
+    for i, d in enumerate((0.0, -0.0, -1.5, 65504.0, 6e-8, 2.0 ** -14)):
+        edge[i, 0:2] = np.array([d], np.float16).view(np.uint8)
+    return np.concatenate([b, edge]).reshape(-1)
+
+
+def test_device_dequant_iq4_nl_bit_exact(hip, oracle_mod):
+    """IQ4_NL (type 20) through mqh_dequant, FP32 and FP16, against the oracle
+    of the reference's IQ4_NL library (cpp/fast_dequant.cpp:40-65)."""
+    import torch
+
+    from flash_moe_hip.dequant import dequant_device
+
+    data = _iq4nl_blocks(4096, 5)
+    src = torch.from_numpy(data).cuda()
+    for dtype, view in ((torch.float16, np.uint16), (torch.float32, np.uint32)):
+        got = dequant_device(src, 20, dtype=dtype).cpu().numpy().view(view)
+        want = oracle_mod.dequant(20, data, want_f16=dtype == torch.float16).view(view)
+        assert np.array_equal(got, want)
+
+
+def test_host_iq4_nl_exports(hip, oracle_mod):
+    """dequantize_iq4_nl_cpp / _avx2 (host pointers, the reference signature):
+    whole rows, and a column count that leaves a partial block whose output
+    columns stay untouched."""
+    from flash_moe_hip.dequant import dequantize_iq4_nl
+
+    rng = np.random.default_rng(6)
+    rows = 40
+    for cols in (64, 512, 70):
+        bpr = cols // 32
+        raw = _iq4nl_blocks(rows * bpr - 6, 7 + cols)
+        want = oracle_mod.dequantize_iq4_nl(raw, rows, cols)
+        for fn in (hip.dequantize_iq4_nl_cpp, hip.dequantize_iq4_nl_avx2):
+            dst = np.full((rows, cols), 7.0, np.float32)
+            fn(raw.ctypes.data, dst.ctypes.data, rows, cols)
+            np.testing.assert_array_equal(dst[:, :32 * bpr].view(np.uint32), want[:, :32 * bpr].view(np.uint32))
+            assert np.all(dst[:, 32 * bpr:] == 7.0)
+        if cols % 32 == 0:
+            got = dequantize_iq4_nl(raw, rows, cols)
+            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    dst = np.full((2, 64), 3.0, np.float32)
+    hip.dequantize_iq4_nl_avx2(None, dst.ctypes.data, 2, 64)        # nothing to run: dst untouched
+    assert np.all(dst == 3.0)

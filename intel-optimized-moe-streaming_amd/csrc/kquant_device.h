@@ -88,6 +88,17 @@ __device__ __forceinline__ float round16(float f) { return __half2float(__float2
 // byte k of a 64-bit word
 __device__ __forceinline__ uint32_t byte_of(uint64_t w, int k) { return (uint32_t)(w >> (8 * k)) & 0xFFu; }
 
+// byte k (a compile-time 0..3) of w as a float: one v_cvt_f32_ubyte<k>
+template <int k>
+__device__ __forceinline__ float ubyte_f(uint32_t w) { return (float)((w >> (8 * k)) & 0xFFu); }
+
+// out[4 * half + k] = f(byte k of w[half]) for the 8 bytes of two dwords
+template <class F>
+__device__ __forceinline__ void per_byte8(uint32_t w0, uint32_t w1, float out[8], F&& f) {
+    out[0] = f(ubyte_f<0>(w0)); out[1] = f(ubyte_f<1>(w0)); out[2] = f(ubyte_f<2>(w0)); out[3] = f(ubyte_f<3>(w0));
+    out[4] = f(ubyte_f<0>(w1)); out[5] = f(ubyte_f<1>(w1)); out[6] = f(ubyte_f<2>(w1)); out[7] = f(ubyte_f<3>(w1));
+}
+
 // ---------------------------------------------------- 8 consecutive values
 //
 // decode8<T>(blk, t, out): values 8t .. 8t+7 of the block at blk, as FP32,
@@ -148,9 +159,9 @@ __device__ __forceinline__ void decode8<T_Q4_K>(const uint8_t* blk, int t, float
     int sc, mn;
     scale_min_k4_regs(h.y, h.z, h.w, j, sc, mn);
     const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
-    const uint64_t w = ld_u64(blk + 16 + 32 * g + lq) >> (4 * hi);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) out[k] = __fsub_rn(__fmul_rn(d1, (float)(byte_of(w, k) & 15)), m1);
+    const uint64_t w = ld_u64(blk + 16 + 32 * g + lq);
+    const uint32_t u0 = ((uint32_t)w >> (4 * hi)) & 0x0F0F0F0Fu, u1 = ((uint32_t)(w >> 32) >> (4 * hi)) & 0x0F0F0F0Fu;
+    per_byte8(u0, u1, out, [&](float q) { return __fsub_rn(__fmul_rn(d1, q), m1); });
 }
 
 template <>
@@ -162,13 +173,12 @@ __device__ __forceinline__ void decode8<T_Q5_K>(const uint8_t* blk, int t, float
     int sc, mn;
     scale_min_k4_regs(h.y, h.z, h.w, j, sc, mn);
     const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
-    const uint64_t lo = ld_u64(blk + 48 + 32 * g + lq) >> (4 * hi);
-    const uint64_t hb = ld_u64(blk + 16 + lq) >> j;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t q = (byte_of(lo, k) & 15) | ((byte_of(hb, k) & 1) << 4);
-        out[k] = __fsub_rn(__fmul_rn(d1, (float)q), m1);
-    }
+    const uint64_t lo = ld_u64(blk + 48 + 32 * g + lq);
+    const uint64_t hb = ld_u64(blk + 16 + lq);
+    const uint32_t u0 = (((uint32_t)lo >> (4 * hi)) & 0x0F0F0F0Fu) | ((((uint32_t)hb >> j) & 0x01010101u) << 4);
+    const uint32_t u1 =
+        (((uint32_t)(lo >> 32) >> (4 * hi)) & 0x0F0F0F0Fu) | ((((uint32_t)(hb >> 32) >> j) & 0x01010101u) << 4);
+    per_byte8(u0, u1, out, [&](float q) { return __fsub_rn(__fmul_rn(d1, q), m1); });
 }
 
 template <>
@@ -176,21 +186,32 @@ __device__ __forceinline__ void decode8<T_Q6_K>(const uint8_t* blk, int t, float
     const int h = t >> 4, s = (t >> 2) & 3, lq = 8 * (t & 3);
     const float d = h2f(ld_u16(blk + 208));
     const float ds = __fmul_rn(d, (float)(int8_t)blk[192 + (t >> 1)]);
-    const uint64_t lo = ld_u64(blk + 64 * h + 32 * (s & 1) + lq) >> (4 * (s >> 1));
-    const uint64_t hq = ld_u64(blk + 128 + 32 * h + lq) >> (2 * s);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int q = (int)((byte_of(lo, k) & 15) | ((byte_of(hq, k) & 3) << 4)) - 32;
-        out[k] = __fmul_rn(ds, (float)q);
-    }
+    const uint64_t lo = ld_u64(blk + 64 * h + 32 * (s & 1) + lq);
+    const uint64_t hq = ld_u64(blk + 128 + 32 * h + lq);
+    const int sl = 4 * (s >> 1), sh = 2 * s;
+    // q + 32 in each byte (0..63); q = that - 32, exact in FP32
+    const uint32_t u0 = (((uint32_t)lo >> sl) & 0x0F0F0F0Fu) | ((((uint32_t)hq >> sh) & 0x03030303u) << 4);
+    const uint32_t u1 = (((uint32_t)(lo >> 32) >> sl) & 0x0F0F0F0Fu) | ((((uint32_t)(hq >> 32) >> sh) & 0x03030303u) << 4);
+    per_byte8(u0, u1, out, [&](float u) { return __fmul_rn(ds, u - 32.0f); });
 }
 
 template <>
 __device__ __forceinline__ void decode8<T_Q3_K>(const uint8_t* blk, int t, float out[8]) {
     const int h = t >> 4, s = (t >> 2) & 3, lq = 8 * (t & 3);
-    // bytes 94..109: two quant bytes, the 12 scale bytes, d (one load that ends
-    // inside the block)
-    const uint4 v = ld_u128(blk + 94);
+    // bytes 94..109: two quant bytes, the 12 scale bytes, d.  A 16-byte load
+    // that is not dword aligned is slow, and every other block starts 2 bytes
+    // off a dword: read the 16 bytes at the dword at or below byte 94 (from
+    // byte 92 at the latest, inside the block) and bytes 108..109 on their own,
+    // then shift down by 0 or 16 bits.
+    const uintptr_t a = (uintptr_t)(blk + 94);
+    const uint4 w = *(const uint4*)(a & ~(uintptr_t)3);
+    const uint32_t d16 = ld_u16(blk + 108);
+    const bool mis = (a & 3) != 0;
+    uint4 v;
+    v.x = mis ? __builtin_amdgcn_alignbit(w.y, w.x, 16) : w.x;
+    v.y = mis ? __builtin_amdgcn_alignbit(w.z, w.y, 16) : w.y;
+    v.z = mis ? __builtin_amdgcn_alignbit(w.w, w.z, 16) : w.z;
+    v.w = mis ? ((w.w >> 16) | (d16 << 16)) : w.w;
     const uint32_t s0 = __builtin_amdgcn_alignbit(v.y, v.x, 16);   // scale bytes 0..3
     const uint32_t s1 = __builtin_amdgcn_alignbit(v.z, v.y, 16);   // 4..7
     const uint32_t s2 = __builtin_amdgcn_alignbit(v.w, v.z, 16);   // 8..11
@@ -200,13 +221,15 @@ __device__ __forceinline__ void decode8<T_Q3_K>(const uint8_t* blk, int t, float
     const int sc = (int)(((lo64 >> (8 * (j & 7) + 4 * (j >> 3))) & 15u) |
                          (((s2 >> (8 * (j & 3) + 2 * (j >> 2))) & 3u) << 4)) - 32;
     const float ds = __fmul_rn(d, (float)sc);
-    const uint64_t lo = ld_u64(blk + 32 + 32 * h + lq) >> (2 * s);
-    const uint64_t hm = ld_u64(blk + lq) >> (t >> 2);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int q = (int)(byte_of(lo, k) & 3) - (int)(((byte_of(hm, k) & 1) ^ 1) << 2);
-        out[k] = __fmul_rn(ds, (float)q);
-    }
+    const uint64_t lo = ld_u64(blk + 32 + 32 * h + lq);
+    const uint64_t hm = ld_u64(blk + lq);
+    const int hb = t >> 2;
+    // q + 4 in each byte: the two low bits, plus 4 when the hmask bit is set
+    // (q = low - 4 when it is clear, dequant_k.cpp:292-294); q = that - 4, exact
+    const uint32_t u0 = (((uint32_t)lo >> (2 * s)) & 0x03030303u) | ((((uint32_t)hm >> hb) & 0x01010101u) << 2);
+    const uint32_t u1 =
+        (((uint32_t)(lo >> 32) >> (2 * s)) & 0x03030303u) | ((((uint32_t)(hm >> 32) >> hb) & 0x01010101u) << 2);
+    per_byte8(u0, u1, out, [&](float u) { return __fmul_rn(ds, u - 4.0f); });
 }
 
 // Runtime-type dispatch; `type` is uniform across the wavefront, so the

@@ -91,6 +91,28 @@ __host__ __device__ inline uint32_t frag_ld16(const uint8_t* p) {
 #endif
 }
 
+// 16 bytes from a 2-byte aligned p with dword-aligned loads: the 16 bytes at
+// the dword at or below p and the dword after them, shifted by 0 or 16 bits.
+// Reads up to 2 bytes before p and 4 bytes past p + 16 (a 16-byte load that is
+// not dword aligned is slow on this GPU; every other Q6_K block starts 2 bytes
+// off a dword).
+__host__ __device__ inline void frag_ld128_a2(const uint8_t* p, uint32_t* w) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uintptr_t a = (uintptr_t)p;
+    const __attribute__((address_space(1))) uint32_t* q =
+        (const __attribute__((address_space(1))) uint32_t*)(a & ~(uintptr_t)3);
+    const uint4 v = *(const __attribute__((address_space(1))) uint4*)q;
+    const uint32_t e = q[4];
+    const uint32_t sh = (uint32_t)(a & 3) * 8;
+    w[0] = __builtin_amdgcn_alignbit(v.y, v.x, sh);
+    w[1] = __builtin_amdgcn_alignbit(v.z, v.y, sh);
+    w[2] = __builtin_amdgcn_alignbit(v.w, v.z, sh);
+    w[3] = __builtin_amdgcn_alignbit(e, v.w, sh);
+#else
+    memcpy(w, p, 16);
+#endif
+}
+
 template <int T>
 __host__ __device__ inline void frag_load(const uint8_t* blk, int q, uint32_t* r) {
     const int qq = (q + 3) & 3;
@@ -104,10 +126,11 @@ __host__ __device__ inline void frag_load(const uint8_t* blk, int q, uint32_t* r
         frag_ld128(blk + 48 + 16 * qq, r + 8);          // qs bytes 16qq .. +16
         frag_ld128(blk + 112 + 16 * qq, r + 12);        // qs bytes 64 + 16qq .. +16
     } else if constexpr (T == T_Q6_K) {
-        frag_ld128(blk + 16 * qq, r);                   // ql bytes 16qq .. +16
-        frag_ld128(blk + 64 + 16 * qq, r + 4);          // ql bytes 64 + 16qq .. +16
-        frag_ld128(blk + 128 + 16 * (qq & 1), r + 8);   // qh bytes 16(qq&1) .. +16
-        frag_ld128(blk + 160 + 16 * (qq & 1), r + 12);  // qh bytes 32 + 16(qq&1) .. +16
+        frag_ld128_a2(blk + 16 * qq, r);                   // ql bytes 16qq .. +16
+        frag_ld128_a2(blk + 64 + 16 * qq, r + 4);          // ql bytes 64 + 16qq .. +16
+        frag_ld128_a2(blk + 128 + 16 * (qq & 1), r + 8);   // qh bytes 16(qq&1) .. +16
+        frag_ld128_a2(blk + 160 + 16 * (qq & 1), r + 12);  // qh bytes 32 + 16(qq&1) .. +16
+        // (the four reads above end by byte 196, inside the block)
         frag_ld128(blk + 192, r + 16);                  // int8 scales[16]
         r[20] = frag_ld16(blk + 208);                   // d
     } else {  // Q3_K

@@ -73,6 +73,8 @@ class MoeRunner:
         sh = layer.shared if use_shared else None
         if y is None:
             y = torch.empty((T, layer.hidden), dtype=torch.float32, device=x.device)
+        if T == 0:
+            return y
         ws = self._workspace(T, top_k, layer.intermediate if top_k else 0, sh.intermediate if sh else 0, stream)
         t = layer.tensors
         rc = self.lib.mqh_moe_decode(
@@ -145,6 +147,8 @@ class MoeRunner:
             scores = torch.empty((T, layer.n_experts), dtype=torch.float32, device=dev)
         if y is None:
             y = torch.empty((T, layer.hidden), dtype=torch.float32, device=dev)
+        if T == 0:
+            return y, ids, weights
         sh = layer.shared if use_shared else None
         ws = self._workspace(T, top_k, layer.intermediate, sh.intermediate if sh else 0, stream)
         t = layer.tensors

@@ -366,3 +366,50 @@ def test_iq4_nl_layer(hip, oracle_mod, types):
     assert runner.status() == 0
     y2 = runner.decode(layer, torch.from_numpy(X).cuda(), rid, rw)
     np.testing.assert_array_equal(y.cpu().numpy(), y2.cpu().numpy())
+
+
+def test_edge_inputs(hip, oracle_mod):
+    """Empty token batches, more slots than the digit kernels take (top-20 runs
+    the FP32 kernels), a hidden/intermediate pair outside the digit kernels'
+    sizes, and a non-finite token reported as -4 (moe_quant_dot.cpp:209-210)."""
+    import torch
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    runner = MoeRunner()
+    types = {"gate": 12, "up": 12, "down": 14}
+    layer, host, shared = make_layer(51, 24, 512, 256, types, shared_types=types)
+    empty = torch.empty((0, 512), dtype=torch.float32, device="cuda")
+    y = runner.decode(layer, empty, torch.empty((0, 4), dtype=torch.int32, device="cuda"),
+                      torch.empty((0, 4), dtype=torch.float32, device="cuda"))
+    assert tuple(y.shape) == (0, 512)
+    layer.router_weights = np.zeros((512, 24), np.float32)
+    y, i, w = runner.decode_routed(layer, empty, 4)
+    assert tuple(y.shape) == (0, 512) and tuple(i.shape) == (0, 4)
+
+    rng = np.random.default_rng(52)
+    X = rng.standard_normal((2, 512)).astype(np.float32)
+    ids = np.stack([rng.permutation(24)[:20] for _ in range(2)])
+    ws = rng.dirichlet(np.ones(20), size=2)
+    print("top-20 decode", flush=True)
+    got, st = run(layer, X, ids, ws)
+    assert st == 0
+    for t in range(2):
+        want = oracle_layer(oracle_mod, layer, host, shared, X[t], ids[t].tolist(), ws[t].tolist())
+        assert oracle_mod.max_relative_error(got[t], want) <= TOL
+
+    layer2, host2, shared2 = make_layer(53, 5, 768, 768, types, shared_types=types)
+    X2 = rng.standard_normal((2, 768)).astype(np.float32)
+    ids2 = np.array([[0, 4], [2, 2]])
+    ws2 = np.array([[0.7, 0.3], [0.5, 0.5]])
+    print("H=768 I=768 decode", flush=True)
+    got2, st = run(layer2, X2, ids2, ws2)
+    assert st == 0
+    for t in range(2):
+        want = oracle_layer(oracle_mod, layer2, host2, shared2, X2[t], ids2[t].tolist(), ws2[t].tolist())
+        assert oracle_mod.max_relative_error(got2[t], want) <= TOL
+
+    X3 = X.copy()
+    X3[1, 7] = np.inf
+    print("non-finite token", flush=True)
+    _, st = run(layer, X3, ids[:, :8], ws[:, :8] / ws[:, :8].sum(1, keepdims=True))
+    assert st == -4

@@ -176,9 +176,9 @@ def roofline(kern: dict, layer, floor=None) -> dict:
         a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
         b_bytes = (K + 1) * layer.expert_bytes("down")
         if kern["a_us"] >= kern["b_us"]:
-            name, nbytes, us = "mqh::k_fast_gate_up<12, 32>", a_bytes, kern["a_us"]
+            name, nbytes, us = "mqh::k_fast_gate_up<12, 12, 32>", a_bytes, kern["a_us"]
         else:
-            name, nbytes, us = "mqh::k_fast_down<14, 8, 1>", b_bytes, kern["b_us"]
+            name, nbytes, us = "mqh::k_fast_down<14, 14, 8, 1>", b_bytes, kern["b_us"]
     return _hbm_roofline(name, nbytes, us, floor(nbytes) if floor else None)
 
 
@@ -513,7 +513,7 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
         dom = "A" if kb["A"] >= kb["B"] else "B"
         frac = frac_a if dom == "A" else 1 - frac_a
     kname = {"prefill": {"A": "mqh::k_prefill_gate_up<11, 8, false, 1>", "B": "mqh::k_prefill_down<11, 2, 1>"},
-             "decode": {"A": "mqh::k_fast_gate_up<11, 32>", "B": "mqh::k_fast_down<11, 8, 4>",
+             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32>", "B": "mqh::k_fast_down<11, 11, 8, 4>",
                         "AB": "mqh::k_fast_layer<11, 11, 32, 8>"}}[best][dom]
     out = {
         "workload": f"batched decode: {T} tokens, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "

@@ -224,14 +224,29 @@ def cpu_baseline(layers, xs, ids, ws, seconds: float, workers: int = 4):
             steps += 1
         dt = time.perf_counter() - t0
     per_step = dt / steps
+    # the same calls on every host thread of the GPU's share, several token-layers in flight
+    with ThreadPoolExecutor(CPU_THREADS) as pool:
+        calls, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds / 2:
+            futs = [pool.submit(oracle.expert_forward, t, TYPES, jobs[j % n_src][1], H, I, 0)
+                    for j in range(4) for t in jobs[j % n_src][0]]
+            for f in futs:
+                f.result()
+            calls += len(futs)
+        dt_all = time.perf_counter() - t0
+    per_step_all = dt_all / calls * (K + 1)
     return {
         "value": round(step_bytes(layers[0]) / per_step / 1e9, 3),
         "unit": "GB/s",
         "cores": workers,
         "kind": "port",
         "sample": f"{steps} token-layers (9 expert calls each, FP32 graph) over {n_src} layers, "
-                  f"{dt:.1f} s on {workers} threads; host has {os.cpu_count()} logical CPUs",
+                  f"{dt:.1f} s on {workers} threads (the reference's expert-worker count); host has "
+                  f"{os.cpu_count()} logical CPUs",
         "us_per_layer": round(per_step * 1e6, 1),
+        "all_cores": {"value": round(step_bytes(layers[0]) / per_step_all / 1e9, 3), "cores": CPU_THREADS,
+                      "us_per_layer": round(per_step_all * 1e6, 1),
+                      "sample": f"{calls} expert calls, four token-layers in flight, {dt_all:.1f} s"},
     }
 
 
@@ -706,6 +721,62 @@ def _delta_kernel_us(states, ins, outs, reps: int) -> float:
     return float(np.mean(us))
 
 
+def bench_single_expert(dev, reps: int, cpu_seconds: float) -> dict:
+    """One Q4_K expert (gate/up [512x2048], down [2048x512]), one token, x ~ N(0,1),
+    seed 0 (the reference's single-expert decode): 40 such experts resident and
+    rotated, each call through the fused decode with top-1 weight 1.0 and no
+    shared expert.  The 70 MB of weights fit in the Infinity Cache, and the call
+    is launch-bound: this line is the CPU comparison of the smallest unit."""
+    import torch
+
+    import oracle
+    from flash_moe_hip.layer_store import ExpertLayer
+    from flash_moe_hip.moe_gpu import MoeRunner
+    from flash_moe_hip.synthetic import config1_expert
+
+    n = 40
+    tensors, kinds, x = config1_expert(0)
+    layers = [ExpertLayer.from_host(tensors, kinds, 1, H, I, device=dev)]
+    layers += [ExpertLayer.synthetic(kinds, 1, H, I, seed=500 + l, device=dev) for l in range(n - 1)]
+    X = torch.from_numpy(x[None]).to(dev)
+    IDS = torch.zeros((1, 1), dtype=torch.int32, device=dev)
+    WS = torch.ones((1, 1), dtype=torch.float32, device=dev)
+    Y = torch.empty((n, H), dtype=torch.float32, device=dev)
+    runner = MoeRunner(dev)
+
+    def sweep():
+        for l in range(n):
+            runner.decode(layers[l], X, IDS, WS, y=Y[l:l + 1], use_shared=False)
+
+    sweep()
+    torch.cuda.synchronize()
+    assert runner.status() == 0
+    want = oracle.expert_forward(tensors, kinds, x, H, I, 0)
+    err = oracle.max_relative_error(Y[0].cpu().numpy(), want)
+    ms = _time(_graph(sweep, dev), reps) / n
+    nbytes = layers[0].bytes_per_expert()
+    log(f"single expert: {ms * 1e3:.2f} us per call, parity {err:.2e}")
+    out = {
+        "workload": "one Q4_K expert, 1 token (gate/up [512x2048], down [2048x512], x ~ N(0,1), seed 0); 40 resident "
+                    "experts rotated (70 MB: Infinity-Cache resident), fused decode top-1, no shared expert",
+        "metric": "us per expert call", "value": round(ms * 1e3, 3), "unit": "us", "higher_is_better": False,
+        "weight_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "parity_max_rel_err": float(f"{err:.3e}"),
+    }
+    if cpu_seconds > 0:
+        oracle.lib()
+        calls, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds / 2:
+            oracle.expert_forward(tensors, kinds, x, H, I, 0)
+            calls += 1
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(dt / calls * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
+                               "sample": f"{calls} calls of the moe_quant_expert port (FP32 graph), one thread, "
+                                         f"{dt:.1f} s"}
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_deltanet(dev, reps: int, cpu_seconds: float) -> dict:
     """The DeltaNet decode recurrence (moe_delta_heads) of the reference model's
     recurrent layers: 30 layers, each a [32 heads x 128 x 128] FP32 state
@@ -786,7 +857,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch every step from Python instead of a graph")
     ap.add_argument("--only-decode", action="store_true", help="skip the batched-decode, prefill and dequant lines")
-    ap.add_argument("--workloads", default="batched_decode,prefill,dequant,deltanet",
+    ap.add_argument("--workloads", default="single_expert,batched_decode,prefill,dequant,deltanet",
                     help="comma-separated workloads run after the headline decode")
     ap.add_argument("--extra-cpu-seconds", type=float, default=4.0)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
@@ -946,6 +1017,7 @@ def main() -> int:
         cpu_s = 0.0 if args.no_cpu_baseline else args.extra_cpu_seconds
         wanted = set(args.workloads.split(","))
         runs = {
+            "single_expert": lambda: bench_single_expert(dev, 50, cpu_s),
             "batched_decode": lambda: bench_batched_decode(dev, args.layers, args.steps // 4, cpu_s),
             "prefill": lambda: bench_prefill(dev, 8, 20, cpu_s),
             "dequant": lambda: bench_dequant(dev, 10, cpu_s),

@@ -329,7 +329,7 @@ def _f64_expert(oracle_mod, tensors, types, x, H, I):
     u = oracle_mod.dequant(types["up"], tensors["up"]).astype(np.float64).reshape(I, H)
     d = oracle_mod.dequant(types["down"], tensors["down"]).astype(np.float64).reshape(H, I)
     gx, ux = g @ x.astype(np.float64), u @ x.astype(np.float64)
-    return d @ (gx / (1.0 + np.exp(-gx)) * ux)
+    return d @ (gx * oracle_mod._sigmoid(gx) * ux)   # the oracle's overflow-free sigmoid
 
 
 @pytest.mark.parametrize("types", [(20, 20), (12, 20), (20, 14)])

@@ -125,20 +125,47 @@ __host__ __device__ constexpr float IQ4NL_TABLE[16] = {
     -1.0f, -0.6961914f, -0.515625f, -0.375f, -0.25390625f, -0.1484375f, -0.0546875f, 0.02734375f,
     0.1015625f, 0.1796875f, 0.265625f, 0.359375f, 0.46875f, 0.59765625f, 0.7578125f, 1.0f};
 
-// table[i] for a 4-bit i, selected in registers (no memory access)
-__device__ __forceinline__ float iq4nl_value(uint32_t i) {
-    float r = IQ4NL_TABLE[0];
+// Table lookups in registers.  Every entry's low 16 bits are zero except
+// entry 1's (0x3999), so an entry is its two high bytes, each found for four
+// indices at once with v_perm_b32 over the 8 bytes of entries 0..7 and of
+// entries 8..15 (index bit 3 picks between the two), plus that one fix-up.
+// IQ4NL_BYTES(first, shift): byte `shift` of entries first .. first+3.
+__host__ __device__ constexpr uint32_t iq4nl_bytes(int first, int shift) {
+    uint32_t w = 0;
+    for (int i = 0; i < 4; ++i)
+        w |= ((__builtin_bit_cast(uint32_t, IQ4NL_TABLE[first + i]) >> (8 * shift)) & 0xFFu) << (8 * i);
+    return w;
+}
+
+// (byte `shift` of table[n_i]) for the four nibbles n_i held one per byte of u
+template <int SHIFT>
+__device__ __forceinline__ uint32_t iq4nl_byte4(uint32_t u, uint32_t sel, uint32_t hi_mask) {
+    const uint32_t lo = __builtin_amdgcn_perm(iq4nl_bytes(4, SHIFT), iq4nl_bytes(0, SHIFT), sel);
+    const uint32_t hi = __builtin_amdgcn_perm(iq4nl_bytes(12, SHIFT), iq4nl_bytes(8, SHIFT), sel);
+    return (hi & hi_mask) | (lo & ~hi_mask);
+}
+
+// table[n] for the four nibbles of u (one per byte), scaled by d
+__device__ __forceinline__ void iq4nl_decode4(uint32_t u, float d, float out[4]) {
+    const uint32_t sel = u & 0x07070707u;
+    const uint32_t hi_mask = ((u >> 3) & 0x01010101u) * 0xFFu;
+    const uint32_t b3 = iq4nl_byte4<3>(u, sel, hi_mask), b2 = iq4nl_byte4<2>(u, sel, hi_mask);
 #pragma unroll
-    for (uint32_t k = 1; k < 16; ++k) r = i == k ? IQ4NL_TABLE[k] : r;
-    return r;
+    for (int k = 0; k < 4; ++k) {
+        // bytes 3, 2 of the entry from b3, b2 (byte k of each), bytes 1, 0 zero
+        const uint32_t bits = __builtin_amdgcn_perm(b3, b2, 0x0C0Cu | ((uint32_t)k << 16) | ((uint32_t)(4 + k) << 24));
+        const uint32_t lo16 = ((u >> (8 * k)) & 0xFFu) == 1u ? (__builtin_bit_cast(uint32_t, IQ4NL_TABLE[1]) & 0xFFFFu) : 0u;
+        out[k] = __fmul_rn(d, __uint_as_float(bits | lo16));
+    }
 }
 
 template <>
 __device__ __forceinline__ void decode8<T_IQ4_NL>(const uint8_t* blk, int t, float out[8]) {
     const float d = h2f(ld_u16(blk));
-    const uint64_t w = ld_u64(blk + 2 + 8 * (t & 1)) >> (4 * (t >> 1));
-#pragma unroll
-    for (int k = 0; k < 8; ++k) out[k] = __fmul_rn(d, iq4nl_value(byte_of(w, k) & 15u));
+    const uint64_t w = ld_u64(blk + 2 + 8 * (t & 1));
+    const int sh = 4 * (t >> 1);
+    iq4nl_decode4(((uint32_t)w >> sh) & 0x0F0F0F0Fu, d, out);
+    iq4nl_decode4(((uint32_t)(w >> 32) >> sh) & 0x0F0F0F0Fu, d, out + 4);
 }
 
 // Scale and min j (0..7) of Q4_K/Q5_K from header dwords h1..h3 (scale bytes

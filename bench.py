@@ -305,7 +305,7 @@ def kernel_times(runner, layers, X, IDS, WS, Y, reps: int) -> dict:
 
 # ---------------------------------------------------------------- other workloads
 
-CPU_THREADS = 16   # the GPU box's host-CPU share per GPU
+CPU_THREADS = 16   # host threads per GPU (the host-CPU share of one MI355X)
 DEQ_TYPES = (11, 12, 14, 8)
 
 
@@ -868,8 +868,8 @@ def main() -> int:
                     help="run one device-to-device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the experts would shard); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only: there is no multi-GPU path (the experts would shard by "
+              "expert, one reduce per layer); run with --gpus 1", file=sys.stderr)
         return 1
 
     import torch

@@ -1,8 +1,8 @@
 """CPU oracle for the quantized-expert hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
-``bench.py`` may import this package, and only as the checker (or, for the
-baseline, as the thing timed on the host).  The HIP product path never imports
+``bench.py`` may import this package, and only to check results against (or,
+for the baseline, as the thing timed on the host).  The HIP product path never imports
 it and never falls back to it.
 
 Contents

@@ -1,7 +1,7 @@
 """Shared pytest setup.
 
 Markers: ``gpu`` -- needs a HIP GPU (MI355X); everything else runs on the CPU.
-The CPU oracle (``oracle/``) is the checker for every parity test.
+Every parity test checks the HIP results against the CPU oracle (``oracle/``).
 """
 from __future__ import annotations
 

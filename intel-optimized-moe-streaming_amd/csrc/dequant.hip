@@ -15,15 +15,19 @@
 
 namespace mqh {
 
+// threads per workgroup, a compile-time constant: blockDim.x would cost every
+// workgroup a memory round trip before its first address is known
+constexpr int DQ_THREADS = 256;
+
 template <int T, bool F16>
-__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src, void* __restrict__ dst,
+__global__ __launch_bounds__(DQ_THREADS) void k_dequant(const uint8_t* __restrict__ src, void* __restrict__ dst,
                                                  int64_t n_groups) {
     constexpr int G = block_size(T) / 8;
     constexpr int PB = block_bytes(T);
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t stride = (int64_t)gridDim.x * DQ_THREADS;
     // two groups per pass, stride apart, both decoded before either is stored,
     // so each thread has two groups' loads in flight
-    for (int64_t g0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g0 < n_groups; g0 += 2 * stride) {
+    for (int64_t g0 = (int64_t)blockIdx.x * DQ_THREADS + threadIdx.x; g0 < n_groups; g0 += 2 * stride) {
         float v[2][8];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -60,7 +64,7 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src
 template <int T>
 static hipError_t launch_t(const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream) {
     const int64_t n_groups = n / 8;
-    const int threads = 256;
+    const int threads = DQ_THREADS;
     int64_t blocks = (n_groups + threads - 1) / threads;
     if (blocks > 65536) blocks = 65536;
     if (want_f16)

@@ -83,13 +83,15 @@ inline WorkspaceLayout decode_workspace_layout(int n_tokens, int top_k, int inte
     return w;
 }
 
-// Layout of one (token, slot) activation in the fast path's workspace region:
-// digit planes int8 [3][inter] at 0, xs16 float [inter/16] at xs_off, sum8
-// float [inter/8] at sum_off; consecutive (token, slot) pairs act_stride apart
-// (at most 4 * inter bytes, the generic path's FP32 row).
+// Layout of one (token, slot) activation in the single-launch kernel's
+// workspace region: digit planes int8 [2][inter] at 0, run scales float
+// [inter/16] at xs_off, run sums float [inter/16] at sum_off; consecutive
+// (token, slot) pairs act_stride apart (at most 4 * inter bytes, the FP32 row
+// that the two-kernel path and the generic path hand over instead).
 struct FastLayout {
     int inter;
     int64_t xs_off, sum_off, act_stride;
+    int a_waves;   // waves per kernel-A workgroup of the two-kernel path (blockDim.x / 64)
 };
 
 // Grouped prefill (moe_prefill.hip).  Token/slot pairs are bucketed by expert

@@ -7,14 +7,19 @@
 //   act[t,s] = silu(W_gate x_t) * (W_up x_t)
 //   y[t]     = sum_s w[t,s] * W_down act[t,s]   (+ sigmoid(x_t . g_inp) * shared)
 //
-// Kernel A  grid (I / 16, S, T).  A workgroup computes 16 consecutive
-//           intermediate rows of one (token, slot): the token's activation digits
-//           go to LDS, each lane keeps the digits of its 64 columns in registers,
-//           and the gate and up rows' quantized bytes are all requested before any
-//           arithmetic.  The 16 results are published as digits to the workspace.
-// Kernel B  grid (H / RB, T), 64*S threads: wave s computes the down rows of
-//           slot s for RB output rows, then the workgroup combines the slots in
-//           top-k order (+ shared) from LDS.
+// Kernel A  grid (ceil(items / W), T), W waves per workgroup.  An item is the
+//           64/(H/64) rows of the gate and up matrices that one wave covers, of
+//           one slot; a token's S * I / (64/(H/64)) items are dealt to the
+//           workgroups in order, W chosen per launch so the workgroups spread
+//           evenly over the CUs (top-8 + shared at H 2048, I 512: 2,304 items,
+//           256 workgroups of 9 waves).  The token's activation digits go to
+//           LDS, each lane keeps the digits of its 64 columns in registers, and
+//           the gate and up rows' quantized bytes are all requested before any
+//           arithmetic.  Each item writes its SwiGLU activations in FP32.
+// Kernel B  grid (H / RB, T), 64*S threads: wave s splits slot s's activations
+//           into digits in LDS (while its weights are in flight), computes the
+//           down rows of slot s for RB output rows, then the workgroup combines
+//           the slots in top-k order (+ shared) from LDS.
 //
 // Lanes follow kquant_lane.h: lane k of a super-block owns 64 of its weights,
 // so a row of C columns is C/64 consecutive lanes and an instruction covers
@@ -22,9 +27,15 @@
 //
 // Supported (checked by fast_supported): FP32 graph; types Q3_K/Q4_K/Q5_K/Q6_K/Q8_0
 // with gate type == up type; hidden and intermediate in {256, 512, 1024, 2048};
-// at most 16 slots; a shared expert with the routed intermediate size and the
-// routed types or Q6_K.  The single-launch kernel takes the K-quant types only.
+// at most 16 slots (12 at intermediate 2048: kernel B's digit LDS); a shared
+// expert with the routed intermediate size and the routed types or Q6_K.  The
+// single-launch kernel takes the K-quant types only; its producers keep
+// 16-row workgroups and hand over digits (publish_run_dev).
 #include <hip/hip_ext.h>
+
+#include <algorithm>
+#include <atomic>
+#include <climits>
 
 #include "kquant_lane.h"
 #include "moe_decode.h"
@@ -90,42 +101,107 @@ __device__ __forceinline__ DigitsRef act_digits(const FastLayout& L, const uint8
     return v;
 }
 
-// Digits of the 16 values of one run held in LDS (vals, 16-byte aligned):
-// lanes 0..15 each read the whole run (broadcast reads, no cross-lane chain),
-// take its max and sum, and write their value's two digits; lane 0 writes the
-// run scale and sum.
-__device__ __forceinline__ void publish_run(const float* vals, int lane, int8_t* planes, int plane_stride,
-                                            float* xs16, float* sum16) {
-    if (lane < RUN) {
-        float amax = 0.0f, s = 0.0f;
+// Max |v| and sum of a 16-value run, in the order every digit producer uses
+// (four-value groups, left to right).
+__device__ __forceinline__ void run_stats(const float4* q, float& amax, float& sum) {
+    amax = 0.0f;
+    sum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < RUN; i += 4) {
-            const float4 q = *(const float4*)(vals + i);
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w))));
-            s += (q.x + q.y) + (q.z + q.w);
+    for (int i = 0; i < RUN / 4; ++i) {
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(q[i].x), fabsf(q[i].y)), fmaxf(fabsf(q[i].z), fabsf(q[i].w))));
+        sum += (q[i].x + q[i].y) + (q[i].z + q[i].w);
+    }
+}
+
+// Two digit planes of four values, one byte each per word.
+__device__ __forceinline__ uint2 split4(float4 v, float inv) {
+    const uint32_t a = split2(v.x, inv), b = split2(v.y, inv), c = split2(v.z, inv), d = split2(v.w, inv);
+    return make_uint2((a & 0xFFu) | ((b & 0xFFu) << 8) | ((c & 0xFFu) << 16) | ((d & 0xFFu) << 24),
+                      (a >> 8) | ((b >> 8) << 8) | ((c >> 8) << 16) | ((d >> 8) << 24));
+}
+
+// Kernel B's digits of one slot's I FP32 activations, in two steps so the
+// loads go out before the weight loads and the arithmetic runs while those are
+// in flight.  Lane l owns columns [l*V, (l+1)*V), V = I/64, and reads the
+// whole 16-column run(s) it lies in: every lane of a run takes the same max and
+// sum (run_stats), and for V < 16 picks its own four-value groups out of the
+// run by lane-constant selects.
+template <int I>
+struct ActRegs {
+    static constexpr int V = I / 64;
+    static constexpr int NQ = V >= RUN ? V / 4 : RUN / 4;   // float4 per lane
+    float4 q[NQ];
+};
+
+template <int I>
+__device__ __forceinline__ void act_load(const float* a, int lane, ActRegs<I>& r) {
+    constexpr int V = ActRegs<I>::V;
+    const float* src = a + (V >= RUN ? lane * V : (lane * V) & ~(RUN - 1));
+#pragma unroll
+    for (int i = 0; i < ActRegs<I>::NQ; ++i) r.q[i] = *(const float4*)(src + 4 * i);
+}
+
+template <int I>
+__device__ __forceinline__ void act_digits_lds(const ActRegs<I>& r, int lane, int8_t* planes, float* xs16,
+                                               float* sum16) {
+    constexpr int V = ActRegs<I>::V;
+    if constexpr (V >= RUN) {
+#pragma unroll
+        for (int run = 0; run < V / RUN; ++run) {
+            const int c0 = lane * V + run * RUN;
+            float amax, sum;
+            run_stats(r.q + 4 * run, amax, sum);
+            const float inv = digit_inv(amax);
+            uint4 lo, hi;
+            uint2 w = split4(r.q[4 * run + 0], inv); lo.x = w.x; hi.x = w.y;
+            w = split4(r.q[4 * run + 1], inv); lo.y = w.x; hi.y = w.y;
+            w = split4(r.q[4 * run + 2], inv); lo.z = w.x; hi.z = w.y;
+            w = split4(r.q[4 * run + 3], inv); lo.w = w.x; hi.w = w.y;
+            *(uint4*)(planes + c0) = lo;
+            *(uint4*)(planes + I + c0) = hi;
+            xs16[c0 / RUN] = digit_scale(amax);
+            sum16[c0 / RUN] = sum;
         }
-        const uint32_t dg = split2(vals[lane], digit_inv(amax));
-        planes[lane] = (int8_t)(dg & 0xFFu);
-        planes[plane_stride + lane] = (int8_t)(dg >> 8);
-        if (lane == 0) {
-            *xs16 = digit_scale(amax);
-            *sum16 = s;
+    } else {
+        const int c0 = lane * V, g0 = (c0 & (RUN - 1)) / 4;   // first own four-value group of the run
+        float amax, sum;
+        run_stats(r.q, amax, sum);
+        const float inv = digit_inv(amax);
+        uint32_t lo[V / 4], hi[V / 4];
+#pragma unroll
+        for (int j = 0; j < V / 4; ++j) {
+            float4 v = r.q[0];
+#pragma unroll
+            for (int m = 1; m < RUN / 4; ++m)
+                if (g0 + j == m) v = r.q[m];
+            const uint2 w = split4(v, inv);
+            lo[j] = w.x;
+            hi[j] = w.y;
+        }
+        if constexpr (V == 8) {
+            *(uint2*)(planes + c0) = make_uint2(lo[0], lo[1]);
+            *(uint2*)(planes + I + c0) = make_uint2(hi[0], hi[1]);
+        } else {
+            static_assert(V == 4, "intermediate 256 or 512 below a run per lane");
+            *(uint32_t*)(planes + c0) = lo[0];
+            *(uint32_t*)(planes + I + c0) = hi[0];
+        }
+        if (g0 == 0) {
+            xs16[c0 / RUN] = digit_scale(amax);
+            sum16[c0 / RUN] = sum;
         }
     }
 }
 
-// Digits of the H values of token x into LDS, in two steps so the loads can be
-// issued early: x_load reads this thread's 4 consecutive values (a whole
-// workgroup of NT = H/4 threads, as every supported shape has), x_digits splits
-// them and writes the two planes, run scales and run sums.
-template <int H, int NT>
-__device__ __forceinline__ float4 x_load(const float* x) {
-    static_assert(H / NT == 4, "four values per thread");
-    return *(const float4*)(x + threadIdx.x * 4);
-}
+// LDS bytes of one slot's digits in kernel B: planes [2][I], run scales and sums.
+__host__ __device__ constexpr int act_lds_bytes(int inter) { return 2 * inter + 2 * (inter / RUN) * 4; }
 
+// Digits of the H values of token x into LDS: thread i (i < NT = H/4) holds
+// values 4i .. 4i+3, loaded early by the caller; x_digits splits them and
+// writes the two planes, run scales and run sums.
 template <int H, int NT>
 __device__ __forceinline__ void x_digits(float4 v, int8_t* planes, float* xs16, float* sum16) {
+    static_assert(H / NT == 4, "four values per thread");
     const int i0 = threadIdx.x * 4;
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     float s = (v.x + v.y) + (v.z + v.w);
@@ -243,6 +319,172 @@ __device__ __forceinline__ void lane_x_dev(const DigitsRef& v, int blk, int k, L
 
 // ---------------------------------------------------------------- kernel A
 
+// Kernel A of the two-kernel path.  An item is RPI = 64 / LPR rows (LPR =
+// hidden / 64 lanes per row) of the gate and of the up matrix of one slot, one
+// wave's work.  Token t's S * inter / RPI items go to workgroups of
+// blockDim.x / 64 waves in order (grid (ceil(items / waves), T)); the waves of
+// a workgroup share the token's digits in LDS.  The token's last workgroup
+// also computes the shared expert's sigmoid gate.
+
+template <int H>
+struct SharedX {
+    __attribute__((aligned(16))) int8_t planes[2 * H];
+    float xs16[H / RUN];
+    float sum16[H / RUN];
+    float s_gate[16];
+};
+
+// every weight load of one item's lane (type T)
+template <int T, int H>
+__device__ __forceinline__ void item_loads(const uint8_t* Gm, const uint8_t* Um, int row, int blk, int k,
+                                           uint32_t* rg, uint32_t* ru) {
+    constexpr int64_t ROW_BYTES = (int64_t)(H / 256) * unit_bytes(T);
+    const int64_t off = (int64_t)row * ROW_BYTES + blk * unit_bytes(T);
+    lane_load<T>(Gm + off, k, rg);
+    lane_load<T>(Um + off, k, ru);
+}
+
+// gate and up dot products of one item's lane (type T), summed over the row's lanes
+template <int T, int LPR>
+__device__ __forceinline__ float2 item_dots(const uint32_t* rg, const uint32_t* ru, const DigitsRef& xd, int blk,
+                                            int k) {
+    LaneX X;
+    lane_x<T>(xd, blk, k, X);
+    const float g = lane_dot<T>(rg, k, X);
+    const float u = lane_dot<T>(ru, k, X);
+    return make_float2(lane_group_sum<LPR>(g), lane_group_sum<LPR>(u));
+}
+
+// SGT: the shared expert's gate/up type (its waves take that code path).
+// ROUTED: the router's select step first (p.route_scores set, at most
+// ROUTE_PROLOGUE_MAX_EXPERTS experts).
+template <int GT, int SGT, int LPR, bool ROUTED>
+__device__ __forceinline__ void gate_up_items(const DecodeParams& p, const FastLayout& L, SharedX<64 * LPR>& sh) {
+    constexpr int H = 64 * LPR, RPI = 64 / LPR, NX = H / 4;   // NX threads hold the token, four values each
+    constexpr int NA = LaneGeo<GT>::NRAW > LaneGeo<SGT>::NRAW ? LaneGeo<GT>::NRAW : LaneGeo<SGT>::NRAW;
+    const int t = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // this wave's item, slot and expert-id address, before the first loads so
+    // that their kernel arguments come in with the token's (L.a_waves =
+    // blockDim.x / 64 as an argument: blockDim.x is a 16-bit field that takes
+    // a vector load and a full wait); items per slot are a power of two
+    const int per_slot = L.inter / RPI;
+    const int item = uniform((int)blockIdx.x * L.a_waves + wave);
+    const bool live = item < p.S * per_slot;
+    const int s = live ? item >> __builtin_ctz(per_slot) : 0;
+    const int row0 = live ? (item & (per_slot - 1)) * RPI : 0;
+    // (bitwise: a short-circuit would branch on its first kernel argument)
+    const bool shared = live & (p.has_shared != 0) & (s == p.top_k);
+    const bool scale_wg = (p.has_shared != 0) & (blockIdx.x == gridDim.x - 1);
+    const bool gate_wg = scale_wg & (p.sh_gate_inp != nullptr);
+
+    // 1. the token's values and the expert id, together and before any branch
+    // (each branch would wait for its own kernel-argument loads): threads past
+    // NX re-read the last four values, outside the gate workgroup the gate
+    // vector's load re-reads the token, and a wave with no id to read (shared
+    // slot, past the end, routed in the prologue) reads the token's first word;
+    // none of these is used.
+    const float* xt = p.x + (int64_t)t * H;
+    const int xi = min((int)threadIdx.x, NX - 1) * 4;
+    const bool id_item = !ROUTED & live & !shared;
+    const int id_raw = *(id_item ? p.ids + (t * p.top_k + s) : (const int32_t*)xt);
+    const float4 xv = *(const float4*)(xt + xi);
+    const float4 gi = *(const float4*)((gate_wg ? p.sh_gate_inp : xt) + xi);   // the shared expert's gate vector
+    __builtin_amdgcn_sched_barrier(0);
+
+    const uint8_t *Gm = p.sh_gate, *Um = p.sh_up;
+    bool bad = false;
+    if (live && !shared) {
+        int e = 0;
+        if constexpr (ROUTED) {
+            // routing in the prologue (router.py:140-170): every wave takes the
+            // top s+1 of token t's router scores (the x load above is in flight
+            // meanwhile); the token's first item takes all top_k and writes the
+            // ids and softmax weights for the down kernel and the caller
+            const bool publish = item == 0;
+            uint64_t key[ROUTE_PROLOGUE_MAX_EXPERTS / 64];
+            route_keys(p.route_scores + (int64_t)t * p.n_experts, p.n_experts, lane, key);
+            const int rounds = publish ? p.top_k : s + 1;
+            float mine = 0.0f;
+            for (int r = 0; r < rounds; ++r) {
+                const uint64_t win = route_next(key);
+                if (r == s) e = key_expert(win);
+                if (lane == r) mine = key_score(win);
+                if (publish && lane == 0) p.route_ids[t * p.top_k + r] = key_expert(win);
+            }
+            if (publish) {
+                const float w = route_weight(mine, p.top_k, lane);
+                if (lane < p.top_k) p.route_weights[t * p.top_k + lane] = w;
+            }
+        } else {
+            e = id_raw;
+            if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }
+        }
+        Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
+    }
+
+    const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
+    const int row = row0 + rr;
+    const bool sw = SGT != GT && shared;   // wave-uniform
+
+    // then every weight load of this lane (waiting for x does not wait for them)
+    uint32_t rg[NA], ru[NA];
+    if (live) {
+        if (sw) item_loads<SGT, H>(Gm, Um, row, blk, k, rg, ru);
+        else item_loads<GT, H>(Gm, Um, row, blk, k, rg, ru);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. token digits (the weight loads are in flight meanwhile)
+    if (threadIdx.x < NX) x_digits<H, NX>(xv, sh.planes, sh.xs16, sh.sum16);
+    __syncthreads();
+
+    // 3. gate and up dot products, SwiGLU: one FP32 activation per row
+    if (live) {
+        DigitsRef xd;
+        xd.planes = sh.planes; xd.xs16 = sh.xs16; xd.sum16 = sh.sum16; xd.n = H;
+        const float2 gu = sw ? item_dots<SGT, LPR>(rg, ru, xd, blk, k) : item_dots<GT, LPR>(rg, ru, xd, blk, k);
+        if (li == 0) p.act[((int64_t)t * p.S + s) * L.inter + row] = bad ? 0.0f : silu_mul(gu.x, gu.y);
+        if (bad && lane == 0 && row0 == 0) atomicOr(&p.flags[FLAG_BAD_ID], 1);
+    }
+
+    // the shared expert's scale: sigmoid(x . g_inp) (shared_expert.py:221-251)
+    // or 1, once per token; the first NX threads hold 4 products each
+    if (scale_wg) {
+        if (gate_wg && wave < NX / 64) {
+            float acc = fmaf(xv.x, gi.x, xv.y * gi.y) + fmaf(xv.z, gi.z, xv.w * gi.w);
+            acc = lane_group_sum<64>(acc);
+            if (lane == 0) sh.s_gate[wave] = acc;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float scale = 1.0f;
+            if (gate_wg) {
+                float dsum = 0.0f;
+#pragma unroll
+                for (int w = 0; w < NX / 64; ++w) dsum += sh.s_gate[w];
+                scale = sigmoid_stable(dsum);
+            }
+            p.sh_scale[t] = scale;
+        }
+    }
+}
+
+template <int GT, int SGT, int LPR>
+__global__ __launch_bounds__(1024) void k_fast_gate_up(DecodeParams p, FastLayout L) {
+    __shared__ SharedX<64 * LPR> sh;
+    gate_up_items<GT, SGT, LPR, false>(p, L, sh);
+}
+
+// Kernel A with the router's select step in its prologue: the same work as
+// k_fast_gate_up once each wave knows its expert.
+template <int GT, int SGT, int LPR>
+__global__ __launch_bounds__(1024) void k_fast_gate_up_routed(DecodeParams p, FastLayout L) {
+    __shared__ SharedX<64 * LPR> sh;
+    gate_up_items<GT, SGT, LPR, true>(p, L, sh);
+}
+
+// ------------------------------------- producers of the single-launch kernel
+
 // Geometry.  LPR = hidden / 64 lanes per row; an instruction covers RPI =
 // 64 / LPR rows of the gate and of the up matrix; a workgroup is WPG = 16 / RPI
 // waves, 16 rows (one activation digit run).
@@ -254,7 +496,6 @@ struct GeoA {
     static constexpr int NT = 64 * WPG;
 };
 
-// LDS of kernel A (and of the producer role of the single-launch kernel)
 template <int H, int WPG>
 struct SharedA {
     __attribute__((aligned(16))) int8_t x_planes[2 * H];
@@ -264,11 +505,11 @@ struct SharedA {
     float s_gate[WPG];
 };
 
-// Workgroup (bx, s, t) of kernel A: 16 intermediate rows of slot s of token t.
-// Threads at or past NT (the single-launch kernel's wider workgroups) only join
-// the barriers.  FUSED: publish with device-scope stores, then write `stamp`
-// into ready word `ready` (else plain stores; the kernel boundary orders them).
-template <int GT, int LPR, bool FUSED, bool ROUTED = false>
+// Producer workgroup (bx, s, t): 16 intermediate rows of slot s of token t,
+// published as digits with device-scope stores, then `stamp` written into
+// ready word `ready`.  Threads at or past NT (the kernel's wider workgroups)
+// only join the barriers.
+template <int GT, int LPR>
 __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLayout& L, int bx, int s, int t,
                                              SharedA<64 * LPR, GeoA<LPR>::WPG>& sh, uint64_t* ready,
                                              uint64_t stamp) {
@@ -283,15 +524,12 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
     const bool active = threadIdx.x < NT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
-    // 1. the token's values first: their address needs no expert id, so the
-    // load goes out while the id is still being read
     const float* xt = p.x + (int64_t)t * H;
     const bool gate_wg = shared && bx == 0 && p.sh_gate_inp != nullptr;
     float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f), gi = xv;
     if (active) {
-        xv = x_load<H, NT>(xt);
-        // the shared expert's sigmoid gate vector, same columns (one workgroup per token)
-        if (gate_wg) gi = x_load<H, NT>(p.sh_gate_inp);
+        xv = *(const float4*)(xt + threadIdx.x * 4);
+        if (gate_wg) gi = *(const float4*)(p.sh_gate_inp + threadIdx.x * 4);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -299,28 +537,6 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
     bool bad = false;
     if (shared) {
         Gm = p.sh_gate; Um = p.sh_up;
-    } else if constexpr (ROUTED) {
-        // routing in the prologue (router.py:140-170): every wave takes the
-        // top s+1 of token t's router scores (the x load above is in flight
-        // meanwhile); one workgroup per token takes all top_k and writes the
-        // ids and softmax weights for the down kernel and the caller
-        const bool publish = bx == 0 && s == 0;
-        uint64_t key[ROUTE_PROLOGUE_MAX_EXPERTS / 64];
-        route_keys(p.route_scores + (int64_t)t * p.n_experts, p.n_experts, lane, key);
-        const int rounds = publish ? p.top_k : s + 1;
-        float mine = 0.0f;
-        int e = 0;
-        for (int r = 0; r < rounds; ++r) {
-            const uint64_t win = route_next(key);
-            if (r == s) e = key_expert(win);
-            if (lane == r) mine = key_score(win);
-            if (publish && threadIdx.x == 0) p.route_ids[t * p.top_k + r] = key_expert(win);
-        }
-        if (publish && wave == 0) {
-            const float w = route_weight(mine, p.top_k, lane);
-            if (lane < p.top_k) p.route_weights[t * p.top_k + lane] = w;
-        }
-        Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
     } else {
         int e = p.ids[t * p.top_k + s];
         if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }
@@ -330,14 +546,12 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
     const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
     const int row = bx * RA + wave * RPI + rr;
 
-    // then every weight load of this lane (waiting for x does not wait for them)
     uint32_t rg[N], ru[N];
     if (active) {
         const int64_t off = (int64_t)row * ROW_BYTES + blk * BB;
         lane_load<GT>(Gm + off, k, rg);
         lane_load<GT>(Um + off, k, ru);
         __builtin_amdgcn_sched_barrier(0);
-        // 2. token digits (the weight loads are in flight meanwhile)
         x_digits<H, NT>(xv, sh.x_planes, sh.x_xs16, sh.x_sum16);
     }
     __syncthreads();
@@ -346,16 +560,11 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
         xd.planes = sh.x_planes; xd.xs16 = sh.x_xs16; xd.sum16 = sh.x_sum16; xd.n = H;
         LaneX X;
         lane_x<GT>(xd, blk, k, X);
-
-        // 3. gate and up dot products, SwiGLU
         float g = lane_dot<GT>(rg, k, X);
         float u = lane_dot<GT>(ru, k, X);
         g = lane_group_sum<LPR>(g);
         u = lane_group_sum<LPR>(u);
         if (li == 0) sh.s_act[wave * RPI + rr] = bad ? 0.0f : silu_mul(g, u);
-
-        // shared slot: sigmoid(x . g_inp), the shared expert's gate, once per token
-        // (shared_expert.py:221-251); every thread holds 4 products
         if (gate_wg) {
             float acc = fmaf(xv.x, gi.x, xv.y * gi.y) + fmaf(xv.z, gi.z, xv.w * gi.w);
             acc = lane_group_sum<64>(acc);
@@ -368,55 +577,19 @@ __device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLa
         float dsum = 0.0f;
 #pragma unroll
         for (int w = 0; w < WPG; ++w) dsum += sh.s_gate[w];
-        const float scale = gate_wg ? sigmoid_stable(dsum) : 1.0f;
-        if constexpr (FUSED) st_dev(p.sh_scale + t, __float_as_uint(scale));
-        else p.sh_scale[t] = scale;
+        st_dev(p.sh_scale + t, __float_as_uint(gate_wg ? sigmoid_stable(dsum) : 1.0f));
     }
 
-    // 4. publish the RA activations as digits
+    // publish the RA activations as digits
     if (wave == 0) {
         uint8_t* base = (uint8_t*)p.act + ((int64_t)t * p.S + s) * L.act_stride;
         const int r0 = bx * RA;
-        if constexpr (FUSED)
-            publish_run_dev(sh.s_act, lane, (int8_t*)base + r0, L.inter, (float*)(base + L.xs_off) + r0 / RUN,
-                            (float*)(base + L.sum_off) + r0 / RUN);
-        else
-            publish_run(sh.s_act, lane, (int8_t*)base + r0, L.inter, (float*)(base + L.xs_off) + r0 / RUN,
+        publish_run_dev(sh.s_act, lane, (int8_t*)base + r0, L.inter, (float*)(base + L.xs_off) + r0 / RUN,
                         (float*)(base + L.sum_off) + r0 / RUN);
     }
-    if constexpr (FUSED) {
-        wait_stores();
-        __syncthreads();
-        if (threadIdx.x == 0) st_dev64(ready, stamp);
-    }
-}
-
-// SGT: the shared expert's gate/up type (its workgroups take that code path).
-template <int GT, int SGT, int LPR>
-__global__ __launch_bounds__(GeoA<LPR>::NT) void k_fast_gate_up(DecodeParams p, FastLayout L) {
-    __shared__ SharedA<64 * LPR, GeoA<LPR>::WPG> sh;
-    if constexpr (SGT != GT) {
-        if (p.has_shared && (int)blockIdx.y == p.top_k) {
-            gate_up_body<SGT, LPR, false>(p, L, blockIdx.x, blockIdx.y, blockIdx.z, sh, nullptr, 0);
-            return;
-        }
-    }
-    gate_up_body<GT, LPR, false>(p, L, blockIdx.x, blockIdx.y, blockIdx.z, sh, nullptr, 0);
-}
-
-// Kernel A with the router's select step in its prologue (p.route_scores set,
-// at most ROUTE_PROLOGUE_MAX_EXPERTS experts): the same work as
-// k_fast_gate_up once each workgroup knows its expert.
-template <int GT, int SGT, int LPR>
-__global__ __launch_bounds__(GeoA<LPR>::NT) void k_fast_gate_up_routed(DecodeParams p, FastLayout L) {
-    __shared__ SharedA<64 * LPR, GeoA<LPR>::WPG> sh;
-    if constexpr (SGT != GT) {
-        if (p.has_shared && (int)blockIdx.y == p.top_k) {
-            gate_up_body<SGT, LPR, false>(p, L, blockIdx.x, blockIdx.y, blockIdx.z, sh, nullptr, 0);
-            return;
-        }
-    }
-    gate_up_body<GT, LPR, false, true>(p, L, blockIdx.x, blockIdx.y, blockIdx.z, sh, nullptr, 0);
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) st_dev64(ready, stamp);
 }
 
 // ---------------------------------------------------------------- kernel B
@@ -460,10 +633,11 @@ __device__ __forceinline__ void down_slot(const DecodeParams& p, const FastLayou
     const bool shared = p.has_shared && s == p.top_k;
 
     LaneX X;
-    // the activation digits first: their address needs no expert id, so the
+    // the slot's activations first: their address needs no expert id, so the
     // loads go out while the id is still being read
+    ActRegs<I> A;
     if constexpr (!FUSED) {
-        if (active) lane_x<DT>(act_digits(L, (const uint8_t*)p.act, t, s, p.S), blk, k, X);
+        if (active) act_load<I>(p.act + ((int64_t)t * p.S + s) * I, lane, A);
         __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -512,6 +686,19 @@ __device__ __forceinline__ void down_slot(const DecodeParams& p, const FastLayou
                 lane_load<DT>(D + (int64_t)(r0 + q * RPI + rr) * ROW_BYTES + blk * BB, k, raw[q]);
         }
         __builtin_amdgcn_sched_barrier(0);
+        // the slot's digits into this wave's LDS region while the weights are
+        // in flight; the wave reads them back once its LDS stores are done
+        if (active) {
+            extern __shared__ __attribute__((aligned(16))) uint8_t b_digits[];
+            int8_t* planes = (int8_t*)(b_digits + s * act_lds_bytes(I));
+            float* xs16 = (float*)(planes + 2 * I);
+            float* sum16 = xs16 + I / RUN;
+            act_digits_lds<I>(A, lane, planes, xs16, sum16);
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            DigitsRef xd;
+            xd.planes = planes; xd.xs16 = xs16; xd.sum16 = sum16; xd.n = I;
+            lane_x<DT>(xd, blk, k, X);
+        }
     }
 
     if (active) {
@@ -592,7 +779,9 @@ bool fast_supported(const DecodeParams& p) {
             return false;
     }
     const int inter = p.top_k > 0 ? p.inter : p.sh_inter;
-    return fast_dim(inter);
+    // kernel B holds every slot's digits in LDS (64 KiB per workgroup, its
+    // static part below 4 KiB)
+    return fast_dim(inter) && (int64_t)p.S * act_lds_bytes(inter) <= 65536 - 4096;
 }
 
 FastLayout fast_layout(int inter) {
@@ -601,25 +790,62 @@ FastLayout fast_layout(int inter) {
     L.xs_off = 2 * inter;
     L.sum_off = L.xs_off + (inter / RUN) * 4;
     L.act_stride = align256(L.sum_off + (inter / RUN) * 4);
+    L.a_waves = 0;
     return L;
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// Waves per kernel-A workgroup for `items` items per token: at least
+// hidden / 256 (the threads that hold the token, four values each), at most
+// 16; the fewest waves on the busiest CU when the launch's workgroups are
+// dealt evenly over the CUs (ties: the smaller workgroup).
+static int gate_up_waves(int items, int tokens, int hidden, int cus) {
+    const int lo = std::max(1, hidden / 256);
+    int best = lo;
+    int64_t best_cost = INT64_MAX;
+    for (int w = lo; w <= 16; ++w) {
+        const int64_t wgs = (int64_t)((items + w - 1) / w) * tokens;
+        const int64_t cost = ((wgs + cus - 1) / cus) * w;
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = w;
+        }
+    }
+    return best;
 }
 
 template <int GT, int SGT, int LPR>
 static void launch_a(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
-    dim3 grid(p.inter / GeoA<LPR>::RA, p.S, p.n_tokens);
+    const int items = p.S * (p.inter / (64 / LPR));
+    const int w = gate_up_waves(items, p.n_tokens, 64 * LPR, device_cus());
+    const dim3 grid((items + w - 1) / w, p.n_tokens), block(64 * w);
+    FastLayout LA = L;
+    LA.a_waves = w;
     if (p.route_scores != nullptr) {
         if (ev.armed_a())
-            hipExtLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream,
-                                  ev.a_start, ev.a_stop, 0, p, L);
+            hipExtLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, block, 0, stream, ev.a_start,
+                                  ev.a_stop, 0, p, LA);
         else
-            hipLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, p, L);
+            hipLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, block, 0, stream, p, LA);
         return;
     }
     if (ev.armed_a())
-        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, ev.a_start,
-                              ev.a_stop, 0, p, L);
+        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p,
+                              LA);
     else
-        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, dim3(GeoA<LPR>::NT), 0, stream, p, L);
+        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, block, 0, stream, p, LA);
 }
 
 template <int GT, int SGT>
@@ -646,11 +872,12 @@ static void launch_a_t(const DecodeParams& p, const FastLayout& L, hipStream_t s
 template <int DT, int SDT, int LPR, int NPB>
 static void launch_b_n(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
     dim3 grid(p.hidden / GeoB<LPR, NPB>::RB, p.n_tokens);
+    const size_t lds = (size_t)p.S * act_lds_bytes(64 * LPR);   // the slots' digits
     if (ev.armed_b())
-        hipExtLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), 0, stream, ev.b_start,
+        hipExtLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), lds, stream, ev.b_start,
                               ev.b_stop, 0, p, L);
     else
-        hipLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), 0, stream, p, L);
+        hipLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), lds, stream, p, L);
 }
 
 // Row groups per wave: one while the grid is small (a single token: every
@@ -703,7 +930,7 @@ __global__ __launch_bounds__(1024) void k_fast_layer(DecodeParams p, FastLayout 
     const int b = blockIdx.x;
     if (b < n_prod) {
         const int bx = b % NXA, s = (b / NXA) % p.S, t = b / (NXA * p.S);
-        gate_up_body<GT, LPRA, true>(p, L, bx, s, t, sha, p.sync + b, stamp);
+        gate_up_body<GT, LPRA>(p, L, bx, s, t, sha, p.sync + b, stamp);
     } else {
         constexpr int NXB = (64 * LPRA) / GeoB<LPRB, FUSED_NPB>::RB;   // kernel B workgroups per token
         const int c = b - n_prod;

@@ -287,14 +287,16 @@ __device__ __forceinline__ int4 pf_tile(const PrefillParams& p, int tile) { retu
 
 // ------------------------------------------------------------ P0
 
-__global__ __launch_bounds__(1024) void k_prefill_route(PrefillParams p) {
+constexpr int PF_ROUTE_THREADS = 1024;   // one workgroup (a constant: blockDim.x costs a memory round trip)
+
+__global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParams p) {
     __shared__ int cnt[PREFILL_MAX_EXPERTS], off[PREFILL_MAX_EXPERTS], fill[PREFILL_MAX_EXPERTS];
     __shared__ int wsum[16][2];
     const int T = p.n_tokens, K = p.top_k, E = p.n_experts, TK = T * K;
     const int e = threadIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (e < E) { cnt[e] = 0; fill[e] = 0; }
     __syncthreads();
-    for (int i = threadIdx.x; i < TK; i += blockDim.x) {
+    for (int i = threadIdx.x; i < TK; i += PF_ROUTE_THREADS) {
         const int id = p.ids[i];
         if (id < 0 || id >= E) atomicOr(&p.flags[FLAG_BAD_ID], 1);
         else atomicAdd(&cnt[id], 1);
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(1024) void k_prefill_route(PrefillParams p) {
     __syncthreads();
     // pair order inside an expert follows the atomics; a pair's result does not
     // depend on its column in the tile, so outputs do not depend on it
-    for (int i = threadIdx.x; i < TK; i += blockDim.x) {
+    for (int i = threadIdx.x; i < TK; i += PF_ROUTE_THREADS) {
         const int id = p.ids[i];
         int pp = -1;
         if (id >= 0 && id < E) {
@@ -341,7 +343,7 @@ __global__ __launch_bounds__(1024) void k_prefill_route(PrefillParams p) {
         p.pos[(i / K) * p.S + (i % K)] = pp;
     }
     if (p.has_shared)
-        for (int t = threadIdx.x; t < T; t += blockDim.x) {
+        for (int t = threadIdx.x; t < T; t += PF_ROUTE_THREADS) {
             p.pair_tok[TK + t] = t;
             p.pos[t * p.S + K] = TK + t;
         }
@@ -549,7 +551,7 @@ static void launch_p2_i(const PrefillParams& p, hipStream_t s, const KernelEvent
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
     if (p.n_tokens <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_prefill_route, dim3(1), dim3(1024), 0, s, p);
+    hipLaunchKernelGGL(k_prefill_route, dim3(1), dim3(PF_ROUTE_THREADS), 0, s, p);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     switch (p.gate_type) {

@@ -262,19 +262,20 @@ __device__ __forceinline__ uint64_t launch_stamp() {
 // statement with a memory clobber, so no store moves across it
 __device__ __forceinline__ void wait_stores() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// publish_run with device-scope stores: lanes 0..15 compute the digits, lanes
-// 0..3 store four values per plane as one word each (all lanes shuffle).
+// Digits of the 16 values of one run held in LDS (vals, 16-byte aligned),
+// published with device-scope stores: lanes 0..15 each read the whole run
+// (broadcast reads), take its max and sum (run_stats) and their value's two
+// digits; lanes 0..3 store four values per plane as one word each (all lanes
+// shuffle); lane 0 stores the run scale and sum.
 __device__ __forceinline__ void publish_run_dev(const float* vals, int lane, int8_t* planes, int plane_stride,
                                                 float* xs16, float* sum16) {
     float amax = 0.0f, sum = 0.0f;
     uint32_t dg = 0;
     if (lane < RUN) {
+        float4 q[RUN / 4];
 #pragma unroll
-        for (int i = 0; i < RUN; i += 4) {
-            const float4 q = *(const float4*)(vals + i);
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w))));
-            sum += (q.x + q.y) + (q.z + q.w);
-        }
+        for (int i = 0; i < RUN / 4; ++i) q[i] = *(const float4*)(vals + 4 * i);
+        run_stats(q, amax, sum);
         dg = split2(vals[lane], digit_inv(amax));
     }
     const int j = lane & 3;

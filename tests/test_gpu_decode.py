@@ -324,6 +324,34 @@ def test_shared_expert_q6k_with_other_routed_types(hip, oracle_mod, routed):
             assert oracle_mod.max_relative_error(got[tok], gen[tok]) <= TOL, (routed, T, tok)
 
 
+@pytest.mark.parametrize("H,I,k,T", [(512, 512, 9, 1), (512, 512, 8, 2), (512, 256, 4, 4)])
+def test_partial_last_workgroup(hip, oracle_mod, H, I, k, T):
+    """Shapes whose gate/up work items do not fill the last workgroup of a
+    token (3, 5 and 3 waves per workgroup; that workgroup also computes the
+    shared expert's sigmoid gate): against the oracle and the generic kernels."""
+    t = {"gate": 12, "up": 12, "down": 14}
+    layer, host, shared = make_layer(300 + H + k + T, 16, H, I, t, shared_types=t)
+    rng = np.random.default_rng(H + I + k + T)
+    X = rng.standard_normal((T, H)).astype(np.float32)
+    ids = np.stack([rng.permutation(16)[:k] for _ in range(T)])
+    ws = rng.dirichlet(np.ones(k), size=T).astype(np.float32)
+    print(f"partial last workgroup H={H} I={I} k={k} T={T}", flush=True)
+    old = hip.mqh_set_decode_path(0)
+    try:
+        got, st = run(layer, X, ids, ws)
+        assert st == 0
+        assert hip.mqh_last_decode_kernels() == 2
+        hip.mqh_set_decode_path(1)
+        gen, st = run(layer, X, ids, ws)
+        assert st == 0
+    finally:
+        hip.mqh_set_decode_path(old)
+    for tok in range(T):
+        want = oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist())
+        assert oracle_mod.max_relative_error(got[tok], want) <= TOL, (H, I, k, T, tok)
+        assert oracle_mod.max_relative_error(got[tok], gen[tok]) <= TOL, (H, I, k, T, tok)
+
+
 def _f64_expert(oracle_mod, tensors, types, x, H, I):
     g = oracle_mod.dequant(types["gate"], tensors["gate"]).astype(np.float64).reshape(I, H)
     u = oracle_mod.dequant(types["up"], tensors["up"]).astype(np.float64).reshape(I, H)

@@ -167,18 +167,14 @@ def measured_traffic(instance: str):
 def roofline(kern: dict, layer, floor=None) -> dict:
     """The dominant kernel (the larger average duration) against HBM peak.
     Algorithmic bytes per launch: the quantized weight bytes it must read --
-    the single-launch kernel all three matrices of the 9 experts, else kernel
-    A the gate and up slices, kernel B the down slices -- plus activations in
-    and out (a few KB)."""
-    if kern["kernels"] == 1:
-        name, nbytes, us = "mqh::k_fast_layer<12, 14, 32, 8>", step_bytes(layer), kern["a_us"]
+    kernel A the gate and up slices, kernel B the down slices -- plus
+    activations in and out (a few KB)."""
+    a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
+    b_bytes = (K + 1) * layer.expert_bytes("down")
+    if kern["a_us"] >= kern["b_us"]:
+        name, nbytes, us = "mqh::k_fast_gate_up<12, 12, 32>", a_bytes, kern["a_us"]
     else:
-        a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
-        b_bytes = (K + 1) * layer.expert_bytes("down")
-        if kern["a_us"] >= kern["b_us"]:
-            name, nbytes, us = "mqh::k_fast_gate_up<12, 12, 32>", a_bytes, kern["a_us"]
-        else:
-            name, nbytes, us = "mqh::k_fast_down<14, 14, 8, 1>", b_bytes, kern["b_us"]
+        name, nbytes, us = "mqh::k_fast_down<14, 14, 8, 1>", b_bytes, kern["b_us"]
     return _hbm_roofline(name, nbytes, us, floor(nbytes) if floor else None)
 
 

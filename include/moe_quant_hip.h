@@ -22,6 +22,9 @@
  * Quantized matrices are GGUF row-major: rows = output features, each row a
  * run of (cols / block_size) blocks.  A stacked expert tensor holds
  * n_experts such matrices back to back, exactly as a GGUF *_exps tensor.
+ * Device-resident quantized pointers must be even addresses (every block is
+ * an even number of bytes and GGUF aligns tensor data to 32 bytes); an odd
+ * one is rejected with -1.
  *
  * Status codes (shared by all entry points):
  *    0  ok
@@ -92,7 +95,7 @@ void dequantize_iq4_nl_avx2(const uint8_t* src_bytes, float* dst, int rows, int 
 /* Device form of dequant_k for weights already in HBM (the conversion that
  * dequant_to_f16, src/run_q4k_f16_openvino.py:62-85, performs on the host),
  * for the five types and IQ4_NL (FP16 output: RN_f16 of the FP32 value).
- * `dst` must be 16-byte aligned.  Returns 0, -1 or -5. */
+ * `dst` must be 16-byte aligned and `src` even.  Returns 0, -1 or -5. */
 int mqh_dequant(int type, const void* src, void* dst, int64_t n, int want_f16, void* stream);
 
 /* Bytes of workspace mqh_moe_decode needs for n_tokens tokens of top_k
@@ -129,8 +132,8 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
  * written (the router's outputs, as mqh_route returns them), then the layer
  * runs as mqh_moe_decode on those ids and weights.  With at most 256 experts
  * and the two fast kernels (path 0), the top-k and softmax run inside the
- * gate/up kernel; otherwise (or on paths 1 and 2) a select kernel of their own
- * runs first.  n_experts <=
+ * gate/up kernel; otherwise (or on path 1) a select kernel of its own runs
+ * first.  n_experts <=
  * 1024, 1 <= top_k <= min(64, n_experts).  Returns as mqh_moe_decode. */
 int mqh_moe_decode_routed(int gate_type, const void* gate, int up_type, const void* up,
                           int down_type, const void* down, int n_experts, int hidden, int intermediate,
@@ -193,16 +196,13 @@ int mqh_moe_prefill(int gate_type, const void* gate, int up_type, const void* up
 
 /* Select the kernels behind mqh_moe_decode and moe_quant_expert: 0 (default)
  * = the two integer-digit fast kernels (gate/up + SwiGLU, then down +
- * combine) whenever the shapes and types allow it (FP32 graph, K-quant types,
- * hidden and intermediate in 256..2048), else the generic kernels; 1 = always
- * the generic kernels; 2 = one kernel launch per call (gate/up and down
- * workgroups of the same launch hand the activations over through the
- * workspace) when the shapes allow it (as for 0, plus hidden 1024 or 2048,
- * intermediate 256 to 1024, at most 16384 gate/up workgroups), else as 0.
- * Process-wide; returns the previous setting, or -1 for another value. */
+ * combine) whenever the shapes and types allow it (FP32 graph, K-quant or
+ * Q8_0 types, hidden and intermediate in 256..2048), else the generic
+ * kernels; 1 = always the generic kernels.  Process-wide; returns the
+ * previous setting, or -1 for another value. */
 int mqh_set_decode_path(int path);
 
-/* Number of kernels (1 or 2) the calling thread's last mqh_moe_decode or
+/* Number of kernels (2) the calling thread's last mqh_moe_decode or
  * moe_quant_expert launched; 0 before the first.  No counterpart in the
  * reference (a profiling aid). */
 int mqh_last_decode_kernels(void);
@@ -242,13 +242,11 @@ int mqh_read_floor(const void* src, int64_t bytes, void* sink, void* start_event
  * (its timers are host wall clocks, bench_phases.py:45-56). */
 int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_stop);
 
-/* Zero a workspace's flags and handoff words on `stream` (once, before first use). */
+/* Zero a workspace's flag words on `stream` (once, before first use). */
 int mqh_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Synchronize `stream`, then read and clear the fault flags latched in
- * `workspace`: 0, -4 (non-finite output), -7 (a single-launch decode's
- * activation handoff did not complete; results invalid), -9 (bad expert id)
- * or -5. */
+ * `workspace`: 0, -4 (non-finite output), -9 (bad expert id) or -5. */
 int mqh_status(void* workspace, void* stream);
 
 #ifdef __cplusplus

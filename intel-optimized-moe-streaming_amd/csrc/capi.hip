@@ -15,7 +15,7 @@ using namespace mqh;
 namespace {
 
 constexpr int ST_OK = 0, ST_ARG = -1, ST_TYPE = -2, ST_BYTES = -3, ST_NONFINITE = -4, ST_HIP = -5,
-              ST_WORKSPACE = -6, ST_TIMEOUT = -7, ST_BAD_ID = -9;
+              ST_WORKSPACE = -6, ST_BAD_ID = -9;
 
 // dequant_k and moe_quant_expert accept the reference's five types; the
 // device entry points also IQ4_NL
@@ -23,8 +23,7 @@ bool supported(int t) { return reference_type(t); }
 bool device_supported(int t) { return reference_type(t) || t == T_IQ4_NL; }
 
 // 0: the two integer-digit kernels when the shapes allow them, else the
-// generic kernels; 1: always the generic kernels; 2: the single-launch kernel
-// when the shapes allow it, else as 0
+// generic kernels; 1: always the generic kernels
 int g_decode_path = 0;
 
 // events armed by mqh_profile_next_decode for this thread's next decode, and
@@ -38,16 +37,12 @@ thread_local int t_last_route_kernels = 0;
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s) {
     const KernelEvents ev = t_events;
     t_events = KernelEvents();
-    if (g_decode_path == 2 && fused_supported(p)) {
-        t_last_kernels = 1;
-        return launch_decode_fused(p, s, ev);
-    }
     t_last_kernels = 2;
     if (g_decode_path != 1 && fast_supported(p)) return launch_decode_fast(p, s, ev);
     return launch_decode_generic(p, s, ev);
 }
 
-// words to zero in a fresh workspace: the flags and the handoff words
+// words to zero in a fresh workspace: the flags
 constexpr int64_t WS_INIT_WORDS = WS_HEAD_BYTES / 4;
 
 // Expected bytes of a [rows x cols] matrix, or a negative status.
@@ -125,15 +120,14 @@ void release_ctx(Ctx* c) {
 }
 
 int read_and_clear_flags(int* flags_dev, hipStream_t s) {
-    int h[3] = {0, 0, 0};   // FLAG_NONFINITE, FLAG_BAD_ID, FLAG_TIMEOUT
+    int h[2] = {0, 0};   // FLAG_NONFINITE, FLAG_BAD_ID
     if (hipStreamSynchronize(s) != hipSuccess) return ST_HIP;
     if (hipMemcpyAsync(h, flags_dev, sizeof(h), hipMemcpyDeviceToHost, s) != hipSuccess) return ST_HIP;
     if (hipStreamSynchronize(s) != hipSuccess) return ST_HIP;
-    if (h[0] | h[1] | h[2]) {
-        if (zero_words(flags_dev, 3, s) != hipSuccess) return ST_HIP;
+    if (h[0] | h[1]) {
+        if (zero_words(flags_dev, 2, s) != hipSuccess) return ST_HIP;
         if (hipStreamSynchronize(s) != hipSuccess) return ST_HIP;
     }
-    if (h[FLAG_TIMEOUT]) return ST_TIMEOUT;
     if (h[FLAG_BAD_ID]) return ST_BAD_ID;
     if (h[FLAG_NONFINITE]) return ST_NONFINITE;
     return ST_OK;
@@ -147,6 +141,11 @@ int check_expert_types(int gt, int ut, int dt, int hidden, int inter, bool devic
     if (hidden % block_size(gt) || hidden % block_size(ut) || inter % block_size(dt)) return ST_TYPE;
     return ST_OK;
 }
+
+// Quantized weights must start at an even address: every block is an even
+// number of bytes, so each block then starts 0 or 2 bytes past a dword, the
+// two cases the Q3_K header load of the decoders handles.
+bool odd(const void* p) { return ((uintptr_t)p & 1) != 0; }
 
 }  // namespace
 
@@ -224,7 +223,7 @@ int moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes, int
     p.x = (const float*)IO; p.n_tokens = 1;
     p.ids = (const int32_t*)(IO + off_id); p.weights = (const float*)(IO + off_id + 4); p.top_k = 1;
     p.y = (float*)(IO + off_y); p.fp16 = fp16_graph;
-    p.flags = (int*)(WS + wl.flags_off); p.sync = (uint64_t*)(WS + wl.sync_off);
+    p.flags = (int*)(WS + wl.flags_off);
     p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
     p.S = 1; p.Imax = intermediate;
 
@@ -332,7 +331,7 @@ void dequantize_iq4_nl_avx2(const uint8_t* src_bytes, float* dst, int rows, int 
 int mqh_dequant(int type, const void* src, void* dst, int64_t n, int want_f16, void* stream) {
     const int bs = device_supported(type) ? block_size(type) : 0;
     if (bs == 0 || src == nullptr || dst == nullptr) return ST_ARG;
-    if (n <= 0 || n % bs != 0 || ((uintptr_t)dst & 15)) return ST_ARG;
+    if (n <= 0 || n % bs != 0 || ((uintptr_t)dst & 15) || odd(src)) return ST_ARG;
     return launch_dequant(type, (const uint8_t*)src, dst, n, want_f16, (hipStream_t)stream) == hipSuccess ? ST_OK
                                                                                                       : ST_HIP;
 }
@@ -372,6 +371,7 @@ int decode_params(int gate_type, const void* gate, int up_type, const void* up, 
     int st = ST_OK;
     if (top_k > 0) {
         if (!gate || !up || !down || !ids || !weights) return ST_ARG;
+        if (odd(gate) || odd(up) || odd(down)) return ST_ARG;
         if (n_experts <= 0 || intermediate <= 0 || intermediate > 65536) return ST_ARG;
         st = check_expert_types(gate_type, up_type, down_type, hidden, intermediate, true);
         if (st) return st;
@@ -380,6 +380,7 @@ int decode_params(int gate_type, const void* gate, int up_type, const void* up, 
     }
     if (has_shared) {
         if (!sh_up || !sh_down || sh_intermediate <= 0 || sh_intermediate > 65536) return ST_ARG;
+        if (odd(sh_gate) || odd(sh_up) || odd(sh_down)) return ST_ARG;
         st = check_expert_types(sh_gate_type, sh_up_type, sh_down_type, hidden, sh_intermediate, true);
         if (st) return st;
     }
@@ -404,7 +405,7 @@ int decode_params(int gate_type, const void* gate, int up_type, const void* up, 
     }
     p.x = x; p.n_tokens = n_tokens; p.ids = ids; p.weights = weights; p.top_k = top_k;
     p.y = y; p.fp16 = fp16_graph;
-    p.flags = (int*)(WS + wl.flags_off); p.sync = (uint64_t*)(WS + wl.sync_off);
+    p.flags = (int*)(WS + wl.flags_off);
     p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
     p.S = top_k + (has_shared ? 1 : 0);
     p.Imax = std::max(intermediate, has_shared ? sh_intermediate : 0);
@@ -482,6 +483,7 @@ int mqh_moe_prefill(int gate_type, const void* gate, int up_type, const void* up
     if (n_experts <= 0 || hidden <= 0 || intermediate <= 0) return ST_ARG;
     if (top_k > 0 && (!gate || !up || !down || !ids || !weights)) return ST_ARG;
     if (has_shared && (!sh_up || !sh_down)) return ST_ARG;
+    if (odd(gate) || odd(up) || odd(down) || odd(sh_gate) || odd(sh_up) || odd(sh_down)) return ST_ARG;
     const int st = check_expert_types(gate_type, up_type, down_type, hidden, intermediate);
     if (st) return st;
     // 16-byte vector loads of x rows, of the gate vector and of the packed tile records
@@ -545,7 +547,7 @@ int mqh_read_floor(const void* src, int64_t bytes, void* sink, void* start_event
 }
 
 int mqh_set_decode_path(int path) {
-    if (path < 0 || path > 2) return ST_ARG;
+    if (path < 0 || path > 1) return ST_ARG;
     const int old = g_decode_path;
     g_decode_path = path;
     return old;

@@ -8,16 +8,10 @@
 
 namespace mqh {
 
-// workspace flag words (int32), sticky until read by mqh_status
-enum : int { FLAG_NONFINITE = 0, FLAG_BAD_ID = 1, FLAG_TIMEOUT = 2, N_FLAGS = 64 };
-
-// Handoff words of the single-launch decode kernel, at a fixed place right after
-// the flags in every workspace (decode and prefill layouts both leave it alone):
-// one 64-bit ready word per producer workgroup.  A producer writes its launch's
-// stamp (unique per queue and dispatch), so words left by earlier launches never
-// match and nothing has to be cleared between launches.
-constexpr int SYNC_MAX_PRODUCERS = 16384;
-constexpr int64_t WS_HEAD_BYTES = (int64_t)N_FLAGS * 4 + (int64_t)SYNC_MAX_PRODUCERS * 8;   // flags + handoff words
+// workspace flag words (int32) at the start of every workspace, sticky until
+// read by mqh_status
+enum : int { FLAG_NONFINITE = 0, FLAG_BAD_ID = 1, N_FLAGS = 64 };
+constexpr int64_t WS_HEAD_BYTES = (int64_t)N_FLAGS * 4;
 
 constexpr int ROUTE_PROLOGUE_MAX_EXPERTS = 256;   // 4 router scores per lane
 
@@ -59,14 +53,13 @@ struct DecodeParams {
     int fp16;
     // workspace views
     int* flags;             // [N_FLAGS]
-    uint64_t* sync;         // [SYNC_MAX_PRODUCERS] handoff words of the single-launch kernel
     float* sh_scale;        // [n_tokens]
     float* act;             // [n_tokens x S x Imax]
     int S, Imax;
 };
 
 struct WorkspaceLayout {
-    int64_t flags_off, sync_off, scale_off, act_off, total;
+    int64_t flags_off, scale_off, act_off, total;
 };
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
@@ -76,22 +69,17 @@ inline WorkspaceLayout decode_workspace_layout(int n_tokens, int top_k, int inte
     const int S = top_k + 1;  // room for the shared slot
     const int Imax = std::max(inter, sh_inter);
     w.flags_off = 0;
-    w.sync_off = (int64_t)N_FLAGS * 4;
     w.scale_off = align256(WS_HEAD_BYTES);
     w.act_off = align256(w.scale_off + (int64_t)n_tokens * 4);
     w.total = align256(w.act_off + (int64_t)n_tokens * S * Imax * 4);
     return w;
 }
 
-// Layout of one (token, slot) activation in the single-launch kernel's
-// workspace region: digit planes int8 [2][inter] at 0, run scales float
-// [inter/16] at xs_off, run sums float [inter/16] at sum_off; consecutive
-// (token, slot) pairs act_stride apart (at most 4 * inter bytes, the FP32 row
-// that the two-kernel path and the generic path hand over instead).
+// Geometry of the fast decode kernels: the activations of (token, slot) are
+// FP32 rows of `inter` values in the workspace.
 struct FastLayout {
     int inter;
-    int64_t xs_off, sum_off, act_stride;
-    int a_waves;   // waves per kernel-A workgroup of the two-kernel path (blockDim.x / 64)
+    int a_waves;   // waves per kernel-A workgroup (blockDim.x / 64)
 };
 
 // Grouped prefill (moe_prefill.hip).  Token/slot pairs are bucketed by expert
@@ -156,8 +144,6 @@ hipError_t launch_delta_heads(float* state, const float* q, const float* k, cons
 bool fast_supported(const DecodeParams& p);
 FastLayout fast_layout(int inter);
 hipError_t launch_decode_fast(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev);
-bool fused_supported(const DecodeParams& p);
-hipError_t launch_decode_fused(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev);
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream, const KernelEvents& ev);
 hipError_t launch_dequant(int type, const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream);
 hipError_t launch_route(const float* x, int n_tokens, int hidden, const float* w, int n_experts, int top_k,

@@ -28,9 +28,7 @@
 // Supported (checked by fast_supported): FP32 graph; types Q3_K/Q4_K/Q5_K/Q6_K/Q8_0
 // with gate type == up type; hidden and intermediate in {256, 512, 1024, 2048};
 // at most 16 slots (12 at intermediate 2048: kernel B's digit LDS); a shared
-// expert with the routed intermediate size and the routed types or Q6_K.  The
-// single-launch kernel takes the K-quant types only; its producers keep
-// 16-row workgroups and hand over digits (publish_run_dev).
+// expert with the routed intermediate size and the routed types or Q6_K.
 #include <hip/hip_ext.h>
 
 #include <algorithm>
@@ -44,10 +42,6 @@
 namespace mqh {
 
 constexpr int FAST_MAX_SLOTS = 16;
-constexpr int FUSED_SPIN_LIMIT = 1 << 20;   // ready-word polls before a consumer gives up (~1 s)
-#ifndef FUSED_NPB
-#define FUSED_NPB 1   // row groups per consumer workgroup of the single-launch kernel
-#endif
 constexpr int RUN = 16;          // activation digit run (columns sharing one scale)
 
 // silu(g) * u with the hardware exp2 and reciprocal (a few ulp; the FP32 graph
@@ -89,17 +83,6 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 
 // Wave-uniform value held in a VGPR, as a scalar.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
-
-// Workspace view of the digits of act[t, s] (I values).
-__device__ __forceinline__ DigitsRef act_digits(const FastLayout& L, const uint8_t* base, int t, int s, int S) {
-    const uint8_t* p = base + ((int64_t)t * S + s) * L.act_stride;
-    DigitsRef v;
-    v.planes = (const int8_t*)p;
-    v.xs16 = (const float*)(p + L.xs_off);
-    v.sum16 = (const float*)(p + L.sum_off);
-    v.n = L.inter;
-    return v;
-}
 
 // Max |v| and sum of a 16-value run, in the order every digit producer uses
 // (four-value groups, left to right).
@@ -218,103 +201,6 @@ __device__ __forceinline__ void x_digits(float4 v, int8_t* planes, float* xs16, 
     if ((i0 & (RUN - 1)) == 0) {
         xs16[i0 / RUN] = digit_scale(amax);
         sum16[i0 / RUN] = s;
-    }
-}
-
-// ------------------------------------------------ handoff inside one launch
-//
-// The single-launch kernel hands activations from producer workgroups to
-// consumer workgroups on other XCDs, whose L2s are not coherent with each
-// other.  Producers store with device-scope (write-through) stores, wait until
-// the stores are acknowledged, then write the launch's stamp into their ready
-// word; consumers poll the ready words for that stamp and read with
-// device-scope loads.  No fences, no atomics and no reset: an agent-scope fence
-// writes back the whole L2 and costs ~30 ns per workgroup, serialised; a
-// same-address counter serialises its atomics (~16 ns each, ~4 us for 256
-// consumers); and a stamp that differs for every launch makes every word left
-// by an earlier launch stale by construction.
-
-__device__ __forceinline__ void st_dev(void* p, uint32_t v) {
-    __hip_atomic_store((uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev64(void* p, uint64_t v) {
-    __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_dev(const void* p) {
-    return __hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_dev64(const void* p) {
-    return __hip_atomic_load((uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The dispatch id: the packet's index in its hardware queue (64-bit, never
-// reused on that queue), delivered in SGPRs by the command processor.
-__device__ uint64_t amdgcn_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
-
-// Stamp of this launch: the dispatch id mixed with the queue's address (ids of
-// different queues overlap), never zero (the value of a fresh workspace).
-__device__ __forceinline__ uint64_t launch_stamp() {
-    const uint64_t q = (uint64_t)(uintptr_t)__builtin_amdgcn_queue_ptr();
-    return (amdgcn_dispatch_id() ^ (q * 0x9E3779B97F4A7C15ull)) | 1ull;
-}
-
-// this thread's stores are acknowledged (vector memory counter drained); an asm
-// statement with a memory clobber, so no store moves across it
-__device__ __forceinline__ void wait_stores() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// Digits of the 16 values of one run held in LDS (vals, 16-byte aligned),
-// published with device-scope stores: lanes 0..15 each read the whole run
-// (broadcast reads), take its max and sum (run_stats) and their value's two
-// digits; lanes 0..3 store four values per plane as one word each (all lanes
-// shuffle); lane 0 stores the run scale and sum.
-__device__ __forceinline__ void publish_run_dev(const float* vals, int lane, int8_t* planes, int plane_stride,
-                                                float* xs16, float* sum16) {
-    float amax = 0.0f, sum = 0.0f;
-    uint32_t dg = 0;
-    if (lane < RUN) {
-        float4 q[RUN / 4];
-#pragma unroll
-        for (int i = 0; i < RUN / 4; ++i) q[i] = *(const float4*)(vals + 4 * i);
-        run_stats(q, amax, sum);
-        dg = split2(vals[lane], digit_inv(amax));
-    }
-    const int j = lane & 3;
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t d = (uint32_t)__shfl((int)dg, 4 * j + i, 64);
-        w0 |= (d & 0xFFu) << (8 * i);
-        w1 |= ((d >> 8) & 0xFFu) << (8 * i);
-    }
-    if (lane < 4) {
-        st_dev(planes + 4 * lane, w0);
-        st_dev(planes + plane_stride + 4 * lane, w1);
-    }
-    if (lane == 0) {
-        st_dev(xs16, __float_as_uint(digit_scale(amax)));
-        st_dev(sum16, __float_as_uint(sum));
-    }
-}
-
-// lane_x (kquant_lane.h) with device-scope loads
-template <int T>
-__device__ __forceinline__ void lane_x_dev(const DigitsRef& v, int blk, int k, LaneX& x) {
-    constexpr int NR = LaneGeo<T>::NR, RL = LaneGeo<T>::RL;
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-        const int c = 256 * blk + lane_col<T>(k, r);
-#pragma unroll
-        for (int p = 0; p < RL / 16; ++p) {
-            const int piece = r * (RL / 16) + p, cc = c + 16 * p;
-            const uint64_t a0 = ld_dev64(v.planes + cc), a1 = ld_dev64(v.planes + cc + 8);
-            const uint64_t b0 = ld_dev64(v.planes + v.n + cc), b1 = ld_dev64(v.planes + v.n + cc + 8);
-            x.d0[4 * piece + 0] = (uint32_t)a0; x.d0[4 * piece + 1] = (uint32_t)(a0 >> 32);
-            x.d0[4 * piece + 2] = (uint32_t)a1; x.d0[4 * piece + 3] = (uint32_t)(a1 >> 32);
-            x.d1[4 * piece + 0] = (uint32_t)b0; x.d1[4 * piece + 1] = (uint32_t)(b0 >> 32);
-            x.d1[4 * piece + 2] = (uint32_t)b1; x.d1[4 * piece + 3] = (uint32_t)(b1 >> 32);
-            x.xs[piece] = __uint_as_float(ld_dev(v.xs16 + (cc >> 4)));
-            x.sum[piece] = __uint_as_float(ld_dev(v.sum16 + (cc >> 4)));
-        }
     }
 }
 
@@ -484,115 +370,6 @@ __global__ __launch_bounds__(1024) void k_fast_gate_up_routed(DecodeParams p, Fa
     gate_up_items<GT, SGT, LPR, true>(p, L, sh);
 }
 
-// ------------------------------------- producers of the single-launch kernel
-
-// Geometry.  LPR = hidden / 64 lanes per row; an instruction covers RPI =
-// 64 / LPR rows of the gate and of the up matrix; a workgroup is WPG = 16 / RPI
-// waves, 16 rows (one activation digit run).
-template <int LPR>
-struct GeoA {
-    static constexpr int RPI = 64 / LPR;
-    static constexpr int RA = 16;
-    static constexpr int WPG = RA / RPI;
-    static constexpr int NT = 64 * WPG;
-};
-
-template <int H, int WPG>
-struct SharedA {
-    __attribute__((aligned(16))) int8_t x_planes[2 * H];
-    float x_xs16[H / RUN];
-    float x_sum16[H / RUN];
-    __attribute__((aligned(16))) float s_act[16];
-    float s_gate[WPG];
-};
-
-// Producer workgroup (bx, s, t): 16 intermediate rows of slot s of token t,
-// published as digits with device-scope stores, then `stamp` written into
-// ready word `ready`.  Threads at or past NT (the kernel's wider workgroups)
-// only join the barriers.
-template <int GT, int LPR>
-__device__ __forceinline__ void gate_up_body(const DecodeParams& p, const FastLayout& L, int bx, int s, int t,
-                                             SharedA<64 * LPR, GeoA<LPR>::WPG>& sh, uint64_t* ready,
-                                             uint64_t stamp) {
-    using G_ = GeoA<LPR>;
-    constexpr int N = LaneGeo<GT>::NRAW;
-    constexpr int BB = unit_bytes(GT);
-    constexpr int H = 64 * LPR;
-    constexpr int RPI = G_::RPI, RA = G_::RA, NT = G_::NT, WPG = G_::WPG;
-    constexpr int64_t ROW_BYTES = (int64_t)(H / 256) * BB;
-
-    const bool shared = p.has_shared && s == p.top_k;
-    const bool active = threadIdx.x < NT;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-
-    const float* xt = p.x + (int64_t)t * H;
-    const bool gate_wg = shared && bx == 0 && p.sh_gate_inp != nullptr;
-    float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f), gi = xv;
-    if (active) {
-        xv = *(const float4*)(xt + threadIdx.x * 4);
-        if (gate_wg) gi = *(const float4*)(p.sh_gate_inp + threadIdx.x * 4);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    const uint8_t *Gm, *Um;
-    bool bad = false;
-    if (shared) {
-        Gm = p.sh_gate; Um = p.sh_up;
-    } else {
-        int e = p.ids[t * p.top_k + s];
-        if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }
-        Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
-    }
-
-    const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
-    const int row = bx * RA + wave * RPI + rr;
-
-    uint32_t rg[N], ru[N];
-    if (active) {
-        const int64_t off = (int64_t)row * ROW_BYTES + blk * BB;
-        lane_load<GT>(Gm + off, k, rg);
-        lane_load<GT>(Um + off, k, ru);
-        __builtin_amdgcn_sched_barrier(0);
-        x_digits<H, NT>(xv, sh.x_planes, sh.x_xs16, sh.x_sum16);
-    }
-    __syncthreads();
-    if (active) {
-        DigitsRef xd;
-        xd.planes = sh.x_planes; xd.xs16 = sh.x_xs16; xd.sum16 = sh.x_sum16; xd.n = H;
-        LaneX X;
-        lane_x<GT>(xd, blk, k, X);
-        float g = lane_dot<GT>(rg, k, X);
-        float u = lane_dot<GT>(ru, k, X);
-        g = lane_group_sum<LPR>(g);
-        u = lane_group_sum<LPR>(u);
-        if (li == 0) sh.s_act[wave * RPI + rr] = bad ? 0.0f : silu_mul(g, u);
-        if (gate_wg) {
-            float acc = fmaf(xv.x, gi.x, xv.y * gi.y) + fmaf(xv.z, gi.z, xv.w * gi.w);
-            acc = lane_group_sum<64>(acc);
-            if (lane == 0) sh.s_gate[wave] = acc;
-        }
-    }
-    if (bad && threadIdx.x == 0 && bx == 0) atomicOr(&p.flags[FLAG_BAD_ID], 1);
-    __syncthreads();
-    if (shared && bx == 0 && threadIdx.x == 0) {
-        float dsum = 0.0f;
-#pragma unroll
-        for (int w = 0; w < WPG; ++w) dsum += sh.s_gate[w];
-        st_dev(p.sh_scale + t, __float_as_uint(gate_wg ? sigmoid_stable(dsum) : 1.0f));
-    }
-
-    // publish the RA activations as digits
-    if (wave == 0) {
-        uint8_t* base = (uint8_t*)p.act + ((int64_t)t * p.S + s) * L.act_stride;
-        const int r0 = bx * RA;
-        publish_run_dev(sh.s_act, lane, (int8_t*)base + r0, L.inter, (float*)(base + L.xs_off) + r0 / RUN,
-                        (float*)(base + L.sum_off) + r0 / RUN);
-    }
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) st_dev64(ready, stamp);
-}
-
 // ---------------------------------------------------------------- kernel B
 
 // LPR = intermediate / 64 lanes per down row; RPI = 64 / LPR rows per
@@ -614,13 +391,9 @@ struct SharedB {
 // Workgroup (bx, t) of kernel B: RB down rows of token t for every slot (wave
 // s = slot s; waves at or past S only join the barriers), combined in top-k
 // order.  down_slot is the calling wave's part (its slot's rows into LDS, with
-// the slot's weight type DT), down_combine the workgroup's.  FUSED: the weights
-// are requested first, then the workgroup waits until the n_ready ready words
-// of token t's producers (sync[t * n_ready ...]) hold `stamp`, and reads the
-// activations with device-scope loads (every wave takes part in that wait).
-template <int DT, int LPR, bool FUSED, int NPB_ = 1>
-__device__ __forceinline__ void down_slot(const DecodeParams& p, const FastLayout& L, int bx, int t,
-                                          SharedB<GeoB<LPR, NPB_>::RB>& sh, int n_ready, uint64_t stamp) {
+// the slot's weight type DT), down_combine the workgroup's.
+template <int DT, int LPR, int NPB_ = 1>
+__device__ __forceinline__ void down_slot(const DecodeParams& p, int bx, int t, SharedB<GeoB<LPR, NPB_>::RB>& sh) {
     constexpr int N = LaneGeo<DT>::NRAW;
     constexpr int BB = unit_bytes(DT);
     constexpr int I = 64 * LPR;
@@ -637,10 +410,8 @@ __device__ __forceinline__ void down_slot(const DecodeParams& p, const FastLayou
     // the slot's activations first: their address needs no expert id, so the
     // loads go out while the id is still being read
     ActRegs<I> A;
-    if constexpr (!FUSED) {
-        if (active) act_load<I>(p.act + ((int64_t)t * p.S + s) * I, lane, A);
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    if (active) act_load<I>(p.act + ((int64_t)t * p.S + s) * I, lane, A);
+    __builtin_amdgcn_sched_barrier(0);
 
     const uint8_t* D = p.sh_down;
     bool bad = false;
@@ -652,54 +423,26 @@ __device__ __forceinline__ void down_slot(const DecodeParams& p, const FastLayou
         w = bad ? 0.0f : p.weights[t * p.top_k + s];
     }
 
+    // then every weight load
     uint32_t raw[NPB][N];
-    if constexpr (FUSED) {
-        // every weight load first (it does not depend on the producers) ...
-        if (active) {
+    if (active) {
 #pragma unroll
-            for (int q = 0; q < NPB; ++q)
-                lane_load<DT>(D + (int64_t)(r0 + q * RPI + rr) * ROW_BYTES + blk * BB, k, raw[q]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // ... then wait for token t's producers (bounded: a launch that cannot
-        // complete raises FLAG_TIMEOUT instead of hanging)
-        if (threadIdx.x < 64) {
-            const uint64_t* rd = p.sync + t * n_ready;
-            int spins = 0;
-            for (;;) {
-                bool ok = true;
-                for (int i = lane; i < n_ready; i += 64) ok &= ld_dev64(rd + i) == stamp;
-                if (__all(ok)) break;
-                if (++spins > FUSED_SPIN_LIMIT) {
-                    if (lane == 0) atomicOr(&p.flags[FLAG_TIMEOUT], 1);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-        __syncthreads();
-        if (active) lane_x_dev<DT>(act_digits(L, (const uint8_t*)p.act, t, s, p.S), blk, k, X);
-    } else {
-        // then every weight load
-        if (active) {
-#pragma unroll
-            for (int q = 0; q < NPB; ++q)
-                lane_load<DT>(D + (int64_t)(r0 + q * RPI + rr) * ROW_BYTES + blk * BB, k, raw[q]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // the slot's digits into this wave's LDS region while the weights are
-        // in flight; the wave reads them back once its LDS stores are done
-        if (active) {
-            extern __shared__ __attribute__((aligned(16))) uint8_t b_digits[];
-            int8_t* planes = (int8_t*)(b_digits + s * act_lds_bytes(I));
-            float* xs16 = (float*)(planes + 2 * I);
-            float* sum16 = xs16 + I / RUN;
-            act_digits_lds<I>(A, lane, planes, xs16, sum16);
-            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            DigitsRef xd;
-            xd.planes = planes; xd.xs16 = xs16; xd.sum16 = sum16; xd.n = I;
-            lane_x<DT>(xd, blk, k, X);
-        }
+        for (int q = 0; q < NPB; ++q)
+            lane_load<DT>(D + (int64_t)(r0 + q * RPI + rr) * ROW_BYTES + blk * BB, k, raw[q]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the slot's digits into this wave's LDS region while the weights are in
+    // flight; the wave reads them back once its LDS stores are done
+    if (active) {
+        extern __shared__ __attribute__((aligned(16))) uint8_t b_digits[];
+        int8_t* planes = (int8_t*)(b_digits + s * act_lds_bytes(I));
+        float* xs16 = (float*)(planes + 2 * I);
+        float* sum16 = xs16 + I / RUN;
+        act_digits_lds<I>(A, lane, planes, xs16, sum16);
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        DigitsRef xd;
+        xd.planes = planes; xd.xs16 = xs16; xd.sum16 = sum16; xd.n = I;
+        lane_x<DT>(xd, blk, k, X);
     }
 
     if (active) {
@@ -709,14 +452,7 @@ __device__ __forceinline__ void down_slot(const DecodeParams& p, const FastLayou
             v = lane_group_sum<LPR>(v);
             if (li == 0) sh.s_y[s][q * RPI + rr] = bad ? 0.0f : v;
         }
-        if (lane == 0) {
-            float sc = w;
-            if (shared) {
-                if constexpr (FUSED) sc = __uint_as_float(ld_dev(p.sh_scale + t));
-                else sc = p.sh_scale[t];
-            }
-            sh.s_w[s] = sc;
-        }
+        if (lane == 0) sh.s_w[s] = shared ? p.sh_scale[t] : w;
     }
 }
 
@@ -735,23 +471,16 @@ __device__ __forceinline__ void down_combine(const DecodeParams& p, int bx, int 
     }
 }
 
-template <int DT, int LPR, bool FUSED, int NPB_ = 1>
-__device__ __forceinline__ void down_body(const DecodeParams& p, const FastLayout& L, int bx, int t,
-                                          SharedB<GeoB<LPR, NPB_>::RB>& sh, int n_ready, uint64_t stamp) {
-    down_slot<DT, LPR, FUSED, NPB_>(p, L, bx, t, sh, n_ready, stamp);
-    down_combine<LPR, NPB_>(p, bx, t, sh);
-}
-
 // SDT: the shared expert's down type (its wave takes that code path).
 template <int DT, int SDT, int LPR, int NPB>
 __global__ __launch_bounds__(1024) void k_fast_down(DecodeParams p, FastLayout L) {
     __shared__ SharedB<GeoB<LPR, NPB>::RB> sh;
     if constexpr (SDT != DT) {
         const int s = uniform(threadIdx.x >> 6);
-        if (p.has_shared && s == p.top_k) down_slot<SDT, LPR, false, NPB>(p, L, blockIdx.x, blockIdx.y, sh, 0, 0);
-        else down_slot<DT, LPR, false, NPB>(p, L, blockIdx.x, blockIdx.y, sh, 0, 0);
+        if (p.has_shared && s == p.top_k) down_slot<SDT, LPR, NPB>(p, blockIdx.x, blockIdx.y, sh);
+        else down_slot<DT, LPR, NPB>(p, blockIdx.x, blockIdx.y, sh);
     } else {
-        down_slot<DT, LPR, false, NPB>(p, L, blockIdx.x, blockIdx.y, sh, 0, 0);
+        down_slot<DT, LPR, NPB>(p, blockIdx.x, blockIdx.y, sh);
     }
     down_combine<LPR, NPB>(p, blockIdx.x, blockIdx.y, sh);
 }
@@ -788,9 +517,6 @@ bool fast_supported(const DecodeParams& p) {
 FastLayout fast_layout(int inter) {
     FastLayout L;
     L.inter = inter;
-    L.xs_off = 2 * inter;
-    L.sum_off = L.xs_off + (inter / RUN) * 4;
-    L.act_stride = align256(L.sum_off + (inter / RUN) * 4);
     L.a_waves = 0;
     return L;
 }
@@ -914,104 +640,6 @@ static void launch_b_t(const DecodeParams& p, const FastLayout& L, hipStream_t s
         case 1024: launch_b<DT, 16>(p, L, stream, ev); break;
         default: launch_b<DT, 32>(p, L, stream, ev); break;
     }
-}
-
-// ------------------------------------------------------- single launch
-
-// One launch per layer call: workgroups [0, n_prod) are kernel A's (bx, s, t)
-// and never wait; workgroups [n_prod, n_prod + n_cons) are kernel B's (bx, t).
-// Producers come first in the grid and workgroups are dispatched in grid order
-// (on each XCD), so every producer gets a slot before any consumer can hold
-// one, and consumers' waits always end (a bounded spin reports FLAG_TIMEOUT
-// otherwise).  Consumers request their weights before waiting, so the down
-// projection's weight stream overlaps the gate/up work.
-template <int GT, int DT, int LPRA, int LPRB>
-__global__ __launch_bounds__(1024) void k_fast_layer(DecodeParams p, FastLayout L, int n_prod) {
-    __shared__ SharedA<64 * LPRA, GeoA<LPRA>::WPG> sha;
-    __shared__ SharedB<GeoB<LPRB, FUSED_NPB>::RB> shb;
-    constexpr int NXA = (64 * LPRB) / GeoA<LPRA>::RA;   // kernel A workgroups per (token, slot)
-    const uint64_t stamp = launch_stamp();
-    const int b = blockIdx.x;
-    if (b < n_prod) {
-        const int bx = b % NXA, s = (b / NXA) % p.S, t = b / (NXA * p.S);
-        gate_up_body<GT, LPRA>(p, L, bx, s, t, sha, p.sync + b, stamp);
-    } else {
-        constexpr int NXB = (64 * LPRA) / GeoB<LPRB, FUSED_NPB>::RB;   // kernel B workgroups per token
-        const int c = b - n_prod;
-        down_body<DT, LPRB, true, FUSED_NPB>(p, L, c % NXB, c / NXB, shb, NXA * p.S, stamp);
-    }
-}
-
-static bool fused_dims(int h, int i) { return (h == 2048 || h == 1024) && (i == 256 || i == 512 || i == 1024); }
-
-bool fused_supported(const DecodeParams& p) {
-    if (!fast_supported(p) || p.sync == nullptr) return false;
-    // the single-launch kernel is built for the K-quant types
-    if (p.top_k > 0 && (p.gate_type == T_Q8_0 || p.down_type == T_Q8_0)) return false;
-    if (p.has_shared && (p.sh_gate_type == T_Q8_0 || p.sh_down_type == T_Q8_0)) return false;
-    if (p.has_shared && p.top_k > 0 && (p.sh_gate_type != p.gate_type || p.sh_down_type != p.down_type)) return false;
-    const int inter = p.top_k > 0 ? p.inter : p.sh_inter;
-    if (!fused_dims(p.hidden, inter)) return false;
-    const int64_t n_prod = (int64_t)(inter / 16) * p.S * p.n_tokens;
-    return n_prod <= SYNC_MAX_PRODUCERS;
-}
-
-template <int GT, int DT, int LPRA, int LPRB>
-static void launch_fused(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
-    const int n_prod = (p.inter / GeoA<LPRA>::RA) * p.S * p.n_tokens;
-    const int n_cons = (p.hidden / GeoB<LPRB, FUSED_NPB>::RB) * p.n_tokens;
-    const int nt = std::max(GeoA<LPRA>::NT, 64 * p.S);
-    const dim3 grid(n_prod + n_cons);
-    if (ev.armed_a())
-        hipExtLaunchKernelGGL((k_fast_layer<GT, DT, LPRA, LPRB>), grid, dim3(nt), 0, stream, ev.a_start, ev.a_stop, 0,
-                              p, L, n_prod);
-    else
-        hipLaunchKernelGGL((k_fast_layer<GT, DT, LPRA, LPRB>), grid, dim3(nt), 0, stream, p, L, n_prod);
-}
-
-template <int GT, int DT, int LPRA>
-static void launch_fused_i(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
-    switch (p.inter) {
-        case 256: launch_fused<GT, DT, LPRA, 4>(p, L, stream, ev); break;
-        case 512: launch_fused<GT, DT, LPRA, 8>(p, L, stream, ev); break;
-        default: launch_fused<GT, DT, LPRA, 16>(p, L, stream, ev); break;
-    }
-}
-
-template <int GT, int DT>
-static void launch_fused_h(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
-    if (p.hidden == 1024) launch_fused_i<GT, DT, 16>(p, L, stream, ev);
-    else launch_fused_i<GT, DT, 32>(p, L, stream, ev);
-}
-
-template <int GT>
-static void launch_fused_d(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
-    switch (p.down_type) {
-        case T_Q4_K: launch_fused_h<GT, T_Q4_K>(p, L, stream, ev); break;
-        case T_Q5_K: launch_fused_h<GT, T_Q5_K>(p, L, stream, ev); break;
-        case T_Q6_K: launch_fused_h<GT, T_Q6_K>(p, L, stream, ev); break;
-        default: launch_fused_h<GT, T_Q3_K>(p, L, stream, ev); break;
-    }
-}
-
-hipError_t launch_decode_fused(const DecodeParams& p0, hipStream_t stream, const KernelEvents& ev) {
-    DecodeParams p = p0;
-    if (p.top_k == 0) {   // shared expert only: present it as the routed types
-        p.gate_type = p.sh_gate_type; p.up_type = p.sh_up_type; p.down_type = p.sh_down_type;
-        p.inter = p.sh_inter;
-    }
-    const FastLayout L = fast_layout(p.inter);
-    switch (p.gate_type) {
-        case T_Q4_K: launch_fused_d<T_Q4_K>(p, L, stream, ev); break;
-        case T_Q5_K: launch_fused_d<T_Q5_K>(p, L, stream, ev); break;
-        case T_Q6_K: launch_fused_d<T_Q6_K>(p, L, stream, ev); break;
-        default: launch_fused_d<T_Q3_K>(p, L, stream, ev); break;
-    }
-    hipError_t err = hipGetLastError();
-    // the second profiling interval is empty: one kernel did both
-    if (err == hipSuccess && ev.b_start) err = hipEventRecord(ev.b_start, stream);
-    if (err == hipSuccess && ev.b_stop) err = hipEventRecord(ev.b_stop, stream);
-    return err;
 }
 
 hipError_t launch_decode_fast(const DecodeParams& p0, hipStream_t stream, const KernelEvents& ev) {

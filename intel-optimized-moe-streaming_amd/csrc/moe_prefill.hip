@@ -482,7 +482,7 @@ PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden,
     L.max_tiles = (int)(std::min<int64_t>(n_experts, TK) + (TK + PREFILL_TILE - 1) / PREFILL_TILE +
                         (has_shared ? (n_tokens + PREFILL_TILE - 1) / PREFILL_TILE : 0));
     L.flags_off = 0;
-    L.scale_off = align256(WS_HEAD_BYTES);   // the decode handoff words stay untouched
+    L.scale_off = align256(WS_HEAD_BYTES);
     L.tiles_off = align256(L.scale_off + (int64_t)n_tokens * 4);
     L.ntiles_off = align256(L.tiles_off + (int64_t)std::max(L.max_tiles, 1) * 16);
     L.pair_off = align256(L.ntiles_off + 4);

@@ -48,7 +48,6 @@ STATUS_TEXT = {
     -4: "non-finite output",
     -5: "HIP runtime failure",
     -6: "workspace too small",
-    -7: "decode activation handoff timed out",
     -9: "expert id out of range",
 }
 

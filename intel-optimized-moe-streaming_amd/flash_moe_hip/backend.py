@@ -14,9 +14,15 @@ plus two fused entry points that ``flash_moe_hip.moe_layer`` prefers:
   moe_tokens(layer, activations, ids, weights)    the same for a batch of tokens
 
 All arithmetic runs in the HIP kernels; results come back as NumPy FP32 like
-the reference backend's.
+the reference backend's.  Each call stages its inputs through one pinned host
+buffer (one host-to-device copy) and returns after one synchronisation, which
+also reads the kernels' fault flags.  The calls are thread-safe: the reference
+runs ``forward`` for a token's experts on the backend's ``_moe_executor``
+(``moe_layer.py:74-94``), and every worker thread has a workspace of its own.
 """
 from __future__ import annotations
+
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -26,7 +32,7 @@ from .moe_gpu import MoeRunner
 
 
 class HipExpertBackend:
-    def __init__(self, layers: dict[int, ExpertLayer], fp16_graph: int = 0, device=None):
+    def __init__(self, layers: dict[int, ExpertLayer], fp16_graph: int = 0, device=None, expert_workers: int = 4):
         import torch
 
         if not torch.cuda.is_available():
@@ -35,10 +41,11 @@ class HipExpertBackend:
         self.fp16_graph = int(fp16_graph)
         self.runner = MoeRunner(device)
         self.device = self.runner.device
-        # Weights are resident: there is no store to read or prefetch from,
-        # and no worker pool (one launch covers all experts of a token).
+        # Weights are resident: there is no store to read or prefetch from.
+        # The bounded worker pool the reference's run_moe_layer fans forward()
+        # out on (backend_ov.py:160); the fused entry points do not use it.
         self.store = None
-        self._moe_executor = None
+        self._moe_executor = ThreadPoolExecutor(max_workers=max(1, int(expert_workers)))
         self._native_enabled = False
 
     # ------------------------------------------------------------ protocol
@@ -64,35 +71,43 @@ class HipExpertBackend:
         self._native_enabled = False
 
     def close(self):
-        pass
+        self._moe_executor.shutdown(wait=True)
 
-    def _x(self, activations, hidden):
+    def _stage(self, activations, hidden: int, ids=None, weights=None):
+        """x [T, hidden] FP32 and the optional ids [T, k] int32 / weights [T, k]
+        FP32 on the device, through one pinned host buffer and one copy."""
         import torch
 
-        x = np.ascontiguousarray(activations, dtype=np.float32).reshape(-1, hidden)
-        return torch.from_numpy(x).to(self.device)
+        x = np.asarray(activations, dtype=np.float32).reshape(-1, hidden)
+        T = x.shape[0]
+        k = 0 if ids is None else int(np.asarray(ids).reshape(T, -1).shape[1])
+        host = torch.empty(T * hidden + 2 * T * k, dtype=torch.float32, pin_memory=True)
+        h = host.numpy()
+        h[:T * hidden] = x.reshape(-1)
+        if k:
+            h[T * hidden:T * (hidden + k)].view(np.int32)[:] = np.asarray(ids, dtype=np.int64).reshape(-1)
+            h[T * (hidden + k):] = np.asarray(weights, dtype=np.float32).reshape(-1)
+        dev = host.to(self.device, non_blocking=True)
+        xd = dev[:T * hidden].view(T, hidden)
+        if not k:
+            return xd, None, None
+        idd = dev[T * hidden:T * (hidden + k)].view(torch.int32).view(T, k)
+        wd = dev[T * (hidden + k):].view(T, k)
+        return xd, idd, wd
 
     def _finish(self, y, what: str) -> np.ndarray:
-        out = y.cpu().numpy()          # synchronizes the stream
-        rc = self.runner.status()
+        out, rc = self.runner.fetch(y)
         if rc:
             raise RuntimeError(f"{what} failed with status {rc} ({_lib.STATUS_TEXT.get(rc, 'unknown')})")
         return out
 
-    def _run(self, layer: ExpertLayer, x, ids: np.ndarray | None, weights: np.ndarray | None,
-             include_shared: bool, fp16_graph: int):
-        import torch
-
-        tid = tw = None
-        if ids is not None:
-            tid = torch.from_numpy(np.ascontiguousarray(ids, dtype=np.int32)).to(self.device)
-            tw = torch.from_numpy(np.ascontiguousarray(weights, dtype=np.float32)).to(self.device)
+    def _decode(self, layer: ExpertLayer, activations, ids, weights, include_shared: bool, fp16_graph: int):
+        x, tid, tw = self._stage(activations, layer.hidden, ids, weights)
         return self.runner.decode(layer, x, tid, tw, fp16_graph=fp16_graph, use_shared=include_shared)
 
     def forward(self, key, activation, hidden_size: int, intermediate_size: int) -> np.ndarray:
         L = self._get(key.layer, hidden_size, intermediate_size)
-        y = self._run(L, self._x(activation, hidden_size), np.array([[key.expert]]), np.ones((1, 1)),
-                      False, self.fp16_graph)
+        y = self._decode(L, activation, [[key.expert]], [[1.0]], False, self.fp16_graph)
         return self._finish(y, "native expert").reshape(hidden_size)
 
     def forward_batch(self, key, activations, hidden_size: int, intermediate_size: int) -> np.ndarray:
@@ -103,36 +118,31 @@ class HipExpertBackend:
             return np.empty((0, hidden_size), dtype=np.float32)
         L = self._get(key.layer, hidden_size, intermediate_size)
         T = x.shape[0]
-        y = self._run(L, self._x(x, hidden_size), np.full((T, 1), key.expert), np.ones((T, 1)),
-                      False, self.fp16_graph)
+        y = self._decode(L, x, np.full((T, 1), key.expert), np.ones((T, 1)), False, self.fp16_graph)
         return self._finish(y, "native expert batch")
 
     # --------------------------------------------------------------- fused
     def moe_layer(self, layer: int, activation, expert_ids, weights, include_shared: bool = True) -> np.ndarray:
         L = self.layers[layer]
-        y = self._run(L, self._x(activation, L.hidden), np.asarray(expert_ids).reshape(1, -1),
-                      np.asarray(weights, dtype=np.float32).reshape(1, -1), include_shared, self.fp16_graph)
+        y = self._decode(L, activation, np.asarray(expert_ids).reshape(1, -1),
+                         np.asarray(weights, dtype=np.float32).reshape(1, -1), include_shared, self.fp16_graph)
         return self._finish(y, "fused MoE layer").reshape(L.hidden)
 
     def moe_tokens(self, layer: int, activations, ids, weights, include_shared: bool = True) -> np.ndarray:
         """A prompt's tokens through the layer (run_moe_sequence): the grouped
         prefill kernels when they cover the layer (FP32 graph, more than one
         token), else the fused decode kernels."""
-        import torch
-
         L = self.layers[layer]
-        x = self._x(activations, L.hidden)
+        x, tid, tw = self._stage(activations, L.hidden, ids, weights)
         if self.fp16_graph == 0 and x.shape[0] > 1 and self.runner.prefill_supported(L):
-            tid = torch.from_numpy(np.ascontiguousarray(ids, dtype=np.int32)).to(self.device)
-            tw = torch.from_numpy(np.ascontiguousarray(weights, dtype=np.float32)).to(self.device)
             y = self.runner.prefill(L, x, tid, tw, use_shared=include_shared)
         else:
-            y = self._run(L, x, ids, weights, include_shared, self.fp16_graph)
+            y = self.runner.decode(L, x, tid, tw, fp16_graph=self.fp16_graph, use_shared=include_shared)
         return self._finish(y, "fused MoE tokens")
 
     def shared_forward(self, layer: int, activations) -> np.ndarray | None:
         L = self.layers.get(layer)
         if L is None or L.shared is None:
             return None
-        y = self._run(L, self._x(activations, L.hidden), None, None, True, 0)
+        y = self._decode(L, activations, None, None, True, 0)
         return self._finish(y, "shared expert")

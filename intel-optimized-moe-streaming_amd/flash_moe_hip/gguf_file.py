@@ -70,6 +70,22 @@ class GGUFTensor:
         return n
 
 
+@dataclass(frozen=True)
+class ReaderTensor:
+    """A tensor as the ``gguf`` package's reader presents it, the form the
+    reference's callers take (``router.py:93-140`` reads ``shape`` and
+    ``data``; ``shared_expert.py:65-94`` also ``data_offset``, ``n_bytes`` and
+    ``tensor_type``): ``shape`` in ggml order (row length first), ``data`` a
+    zero-copy NumPy view in row-major order -- typed for F32/F16, the raw
+    bytes ``[rows, row_bytes]`` for quantized types."""
+    name: str
+    shape: tuple
+    tensor_type: int
+    data_offset: int
+    n_bytes: int
+    data: np.ndarray
+
+
 def tensor_nbytes(ggml_type: int, dims) -> int | None:
     name = GGML_TYPE_NAMES.get(int(ggml_type))
     if name is None:
@@ -179,6 +195,21 @@ class GGUFFile:
         else:
             raise GGUFError(f"{name}: ggml type {t.ggml_type} is not a float type")
         return np.asarray(a).reshape(t.shape)
+
+    def reader_tensor(self, name: str) -> ReaderTensor:
+        t = self.tensors[name]
+        raw = self.raw(name)
+        if t.ggml_type in (0, 1):
+            data = raw.view(np.float32 if t.ggml_type == 0 else np.float16).reshape(t.shape)
+        else:
+            rows = t.n_elements // int(t.dims[0])
+            data = raw.reshape(rows, -1)
+        return ReaderTensor(name, tuple(int(d) for d in t.dims), t.ggml_type, t.offset, int(t.n_bytes), data)
+
+    def tensor_map(self) -> dict:
+        """{name: ReaderTensor} for every tensor of a known type: the ``tmap``
+        the reference's routers_from_gguf and SharedExpert read."""
+        return {n: self.reader_tensor(n) for n, t in self.tensors.items() if t.n_bytes is not None}
 
     def expert_layers(self) -> dict[int, dict[str, int]]:
         """{layer: {role: ggml type}} of every layer with stacked expert

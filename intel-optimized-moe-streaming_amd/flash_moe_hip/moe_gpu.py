@@ -6,8 +6,16 @@ for every routed expert of every token plus the layer's shared expert;
 bucketed per expert on the device).  Nothing is synchronized.
 ``MoeRunner.status()`` synchronizes and returns the fault status latched by
 the kernels (0, -4 non-finite, -9 bad expert id).
+
+Threads.  The reference fans one token's experts out over a thread pool
+(``moe_layer.py:74-94``), so one runner is called from several threads at
+once.  Every calling thread gets a workspace of its own (activations and
+fault flags), so concurrent calls never share scratch memory, and ``status()``
+reports the faults of the calling thread's calls only.
 """
 from __future__ import annotations
+
+import threading
 
 from . import _lib
 from .layer_store import ExpertLayer
@@ -21,15 +29,18 @@ PREFILL_MAX_EXPERTS = 1024
 
 
 class MoeRunner:
-    """Owns the workspace of the fused kernels on one device."""
+    """Owns the workspaces of the fused kernels on one device (one per calling thread)."""
 
     def __init__(self, device=None):
         import torch
 
         self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         self.lib = _lib.load()
-        self._ws = None
-        self._ws_bytes = 0
+        self._local = threading.local()
+
+    @property
+    def _ws(self):
+        return getattr(self._local, "ws", None)
 
     def _workspace(self, n_tokens: int, top_k: int, inter: int, sh_inter: int, stream):
         need = int(self.lib.mqh_moe_workspace_bytes(n_tokens, top_k, inter, sh_inter))
@@ -38,17 +49,22 @@ class MoeRunner:
         return self._reserve(need, stream)
 
     def _reserve(self, need: int, stream):
+        """The calling thread's workspace, grown to at least `need` bytes.  A
+        new buffer is zeroed (its flag words) before it replaces the old one;
+        the old one's latched faults are raised first."""
         import torch
 
-        if self._ws is None or need > self._ws_bytes:
-            if self._ws is not None:
-                # keep the latched flags of the old workspace visible
-                _lib.check(self.lib.mqh_status(self._ws.data_ptr(), stream.cuda_stream), "pending kernel")
-            self._ws_bytes = max(need, 2 * self._ws_bytes)
-            self._ws = torch.empty(self._ws_bytes, dtype=torch.uint8, device=self.device)
-            _lib.check(self.lib.mqh_workspace_init(self._ws.data_ptr(), self._ws_bytes, stream.cuda_stream),
+        ws = self._ws
+        if ws is None or need > ws.numel():
+            size = max(need, 2 * ws.numel()) if ws is not None else need
+            if ws is not None:
+                _lib.check(self.lib.mqh_status(ws.data_ptr(), stream.cuda_stream), "pending kernel")
+            new = torch.empty(size, dtype=torch.uint8, device=self.device)
+            _lib.check(self.lib.mqh_workspace_init(new.data_ptr(), new.numel(), stream.cuda_stream),
                        "mqh_workspace_init")
-        return self._ws
+            self._local.ws = new
+            ws = new
+        return ws
 
     def decode(self, layer: ExpertLayer, x, ids=None, weights=None, *, y=None, fp16_graph: int = 0,
                use_shared: bool = True, stream=None):
@@ -86,7 +102,33 @@ class MoeRunner:
             sh.intermediate if sh else 0,
             sh.gate_inp.data_ptr() if (sh is not None and sh.gate_inp is not None) else _NULL,
             x.data_ptr(), T, ids.data_ptr() if top_k else _NULL, weights.data_ptr() if top_k else _NULL, top_k,
-            y.data_ptr(), int(fp16_graph), ws.data_ptr(), self._ws_bytes, stream.cuda_stream)
+            y.data_ptr(), int(fp16_graph), ws.data_ptr(), ws.numel(), stream.cuda_stream)
+        _lib.check(rc, "mqh_moe_decode")
+        return y
+
+    def decode_shared(self, shared, hidden: int, x, *, y=None, stream=None):
+        """y[t] = sigmoid(x[t] . gate_inp) * E_sh(x[t]) for a shared expert on
+        its own (``SharedWeights``: no routed experts), x [T, hidden] FP32."""
+        import torch
+
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        x = x.reshape(-1, hidden)
+        T = x.shape[0]
+        if x.dtype != torch.float32 or not x.is_contiguous():
+            raise ValueError("x must be contiguous FP32")
+        if y is None:
+            y = torch.empty((T, hidden), dtype=torch.float32, device=x.device)
+        if T == 0:
+            return y
+        ws = self._workspace(T, 0, 0, shared.intermediate, stream)
+        sh = shared
+        rc = self.lib.mqh_moe_decode(
+            0, _NULL, 0, _NULL, 0, _NULL, 0, hidden, 0,
+            sh.types["gate"], sh.gate.data_ptr(), sh.types["up"], sh.up.data_ptr(),
+            sh.types["down"], sh.down.data_ptr(), sh.intermediate,
+            sh.gate_inp.data_ptr() if sh.gate_inp is not None else _NULL,
+            x.data_ptr(), T, _NULL, _NULL, 0, y.data_ptr(), 0, ws.data_ptr(), ws.numel(), stream.cuda_stream)
         _lib.check(rc, "mqh_moe_decode")
         return y
 
@@ -161,7 +203,7 @@ class MoeRunner:
             sh.intermediate if sh else 0,
             sh.gate_inp.data_ptr() if (sh is not None and sh.gate_inp is not None) else _NULL,
             x.data_ptr(), T, w.data_ptr(), int(top_k), scores.data_ptr(), ids.data_ptr(), weights.data_ptr(),
-            y.data_ptr(), 0, ws.data_ptr(), self._ws_bytes, stream.cuda_stream)
+            y.data_ptr(), 0, ws.data_ptr(), ws.numel(), stream.cuda_stream)
         _lib.check(rc, "mqh_moe_decode_routed")
         return y, ids, weights
 
@@ -220,17 +262,42 @@ class MoeRunner:
             sh.down.data_ptr() if inside else _NULL,
             sh.gate_inp.data_ptr() if (inside and sh.gate_inp is not None) else _NULL,
             x.data_ptr(), int(x.dtype == torch.bfloat16), T, ids.data_ptr(), weights.data_ptr(), top_k,
-            y.data_ptr(), ws.data_ptr(), self._ws_bytes, stream.cuda_stream)
+            y.data_ptr(), ws.data_ptr(), ws.numel(), stream.cuda_stream)
         _lib.check(rc, "mqh_moe_prefill")
         if sh is not None and not inside:
             y += self.decode(layer, x.float(), None, None, use_shared=True, stream=stream)
         return y
 
     def status(self, stream=None) -> int:
+        """Synchronize `stream` and return (and clear) the faults latched by
+        the calling thread's calls."""
         import torch
 
-        if self._ws is None:
+        ws = self._ws
+        if ws is None:
             return 0
         if stream is None:
             stream = torch.cuda.current_stream(self.device)
-        return int(self.lib.mqh_status(self._ws.data_ptr(), stream.cuda_stream))
+        return int(self.lib.mqh_status(ws.data_ptr(), stream.cuda_stream))
+
+    def fetch(self, y, stream=None):
+        """(y as a NumPy array, status) with one synchronisation: y and the
+        calling thread's fault flags are copied to the host together; the flags
+        are cleared (a second synchronisation) only when a fault was latched."""
+        import torch
+
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        ws = self._ws
+        with torch.cuda.stream(stream):
+            out = torch.empty(y.shape, dtype=y.dtype, pin_memory=True)
+            out.copy_(y, non_blocking=True)
+            flags = None
+            if ws is not None:
+                flags = torch.empty(2, dtype=torch.int32, pin_memory=True)
+                flags.copy_(ws[:8].view(torch.int32), non_blocking=True)
+        stream.synchronize()
+        rc = 0
+        if flags is not None and bool(flags.any()):
+            rc = int(self.lib.mqh_status(ws.data_ptr(), stream.cuda_stream))
+        return out.numpy(), rc

@@ -8,7 +8,10 @@ renormalised over the selection.  Gate weights are stored rounded to
 ``gate_dtype`` (FP16 by default) and promoted to FP32 once (router.py:39-59).
 
 ``route_batch`` returns the device-ready int32/FP32 arrays for a batch of
-tokens, in the layout the fused kernels read.
+tokens, in the layout the fused kernels read.  ``from_gguf_tensor`` and
+``routers_from_gguf`` build the per-layer routers from
+``blk.N.ffn_gate_inp.weight`` (router.py:93-140, 180-210): the tensor map of
+``GGUFFile.tensor_map()`` or of the ``gguf`` package's reader.
 """
 from __future__ import annotations
 
@@ -38,6 +41,22 @@ class ExpertRouter:
         if not np.isfinite(w.astype(np.float32)).all():
             raise ValueError("gate weights contain NaN or Inf")
         self.gate_weights = np.ascontiguousarray(w, dtype=np.float32)
+
+    @classmethod
+    def from_gguf_tensor(cls, tensor, hidden_size: int, num_experts: int, top_k: int,
+                         gate_dtype=np.float16) -> "ExpertRouter":
+        """The layer's router from ``ffn_gate_inp.weight``: ``tensor.shape`` in
+        ggml order (hidden first), so the stored matrix is (experts, hidden)
+        and is transposed by the constructor."""
+        shape = tuple(int(s) for s in reversed(tensor.shape))
+        if shape not in ((num_experts, hidden_size), (hidden_size, num_experts)):
+            raise ValueError(f"ffn_gate_inp shape {shape} does not match {num_experts} experts x "
+                             f"{hidden_size} hidden")
+        gate = np.asarray(tensor.data)
+        if gate.size != num_experts * hidden_size:
+            raise ValueError(f"ffn_gate_inp has {gate.size} elements, expected {num_experts * hidden_size}")
+        return cls(hidden_size=hidden_size, num_experts=num_experts, top_k=top_k,
+                   gate_weights=gate.reshape(shape).astype(gate_dtype, copy=False), gate_dtype=gate_dtype)
 
     def scores(self, activation) -> np.ndarray:
         x = np.asarray(activation, dtype=np.float32).reshape(-1)
@@ -73,6 +92,23 @@ def softmax_all_experts(scores: np.ndarray) -> np.ndarray:
     s = np.asarray(scores, dtype=np.float64)
     e = np.exp(s - s.max())
     return e / e.sum()
+
+
+def routers_from_gguf(tmap: dict, num_layers: int, hidden_size: int, num_experts: int, top_k: int,
+                      arch: str = "qwen35moe", gate_dtype=np.float16) -> dict[int, ExpertRouter]:
+    """{layer: ExpertRouter} from every ``blk.N.ffn_gate_inp.weight`` of the
+    tensor map; a layer without one raises KeyError (router.py:180-210)."""
+    routers: dict[int, ExpertRouter] = {}
+    missing: list[int] = []
+    for layer in range(num_layers):
+        t = tmap.get(f"blk.{layer}.ffn_gate_inp.weight")
+        if t is None:
+            missing.append(layer)
+            continue
+        routers[layer] = ExpertRouter.from_gguf_tensor(t, hidden_size, num_experts, top_k, gate_dtype=gate_dtype)
+    if missing:
+        raise KeyError(f"ffn_gate_inp.weight is missing for layers {missing}: the experts to run cannot be chosen")
+    return routers
 
 
 def synthetic_router(hidden_size: int, num_experts: int, top_k: int, seed: int = 0,

@@ -71,19 +71,24 @@ def run(layer, X, ids, ws, fp16=0, use_shared=True):
     return out, runner.status()
 
 
-@pytest.fixture(params=[0, 2, 1], ids=["two-kernel", "single-launch", "generic"])
+@pytest.fixture(params=[0, 1], ids=["two-kernel", "generic"])
 def path(request, hip):
-    """Run the test through the two integer-digit kernels, the single-launch
-    kernel (where the shapes allow it) and the generic kernels."""
+    """Run the test through the two integer-digit kernels and the generic kernels."""
     old = hip.mqh_set_decode_path(request.param)
     yield request.param
     hip.mqh_set_decode_path(old)
 
 
-def expect_kernels(hip, path, fused_shape):
-    """The number of kernels the last decode on this thread must have launched."""
-    want = 1 if path == 2 and fused_shape else 2
-    assert hip.mqh_last_decode_kernels() == want
+def expect_kernels(hip):
+    """Every decode launches two kernels (gate/up + SwiGLU, then down + combine)."""
+    assert hip.mqh_last_decode_kernels() == 2
+
+
+def test_removed_decode_path_rejected(hip):
+    """Only paths 0 (fast kernels) and 1 (generic kernels) exist."""
+    old = hip.mqh_set_decode_path(0)
+    assert hip.mqh_set_decode_path(2) == -1
+    assert hip.mqh_set_decode_path(old) == 0
 
 
 @pytest.fixture(scope="module")
@@ -102,7 +107,7 @@ def test_one_token_top8_plus_shared(decode_layer, oracle_mod, hip, path):
     print(f"decode 1 token path={path} ids={ids}", flush=True)
     got, st = run(layer, x[None], np.array([ids]), np.array([ws]))
     assert st == 0
-    expect_kernels(hip, path, True)
+    expect_kernels(hip)
     want = oracle_layer(oracle_mod, layer, host, shared, x, ids, ws)
     err = oracle_mod.max_relative_error(got[0], want)
     print(f"  max rel err (kernel semantics) {err:.3e}", flush=True)
@@ -153,7 +158,7 @@ def test_batched_tokens_q3k(hip, oracle_mod, path):
     ws /= ws.sum(1, keepdims=True)
     got, st = run(layer, X, ids, ws)
     assert st == 0
-    expect_kernels(hip, path, True)
+    expect_kernels(hip)
     worst = 0.0
     for t in range(16):
         want = oracle_layer(oracle_mod, layer, host, shared, X[t], ids[t].tolist(), ws[t].tolist())
@@ -181,8 +186,8 @@ def test_fp16_graph_routed_experts(hip, oracle_mod):
 
 @pytest.mark.parametrize("types", [(12, 14), (11, 11), (13, 12), (14, 14), (12, 13), (11, 14)])
 def test_fast_type_pairs(hip, oracle_mod, types):
-    """Every (gate/up, down) type pair of the single-launch and two-kernel
-    paths, 3 tokens, at shapes each path takes, against the oracle."""
+    """Every (gate/up, down) type pair of the two-kernel path, 3 tokens, at
+    several shapes, against the oracle."""
     gu, dn = types
     t = {"gate": gu, "up": gu, "down": dn}
     for H, I in ((256, 256), (2048, 512), (512, 1024), (1024, 256), (1024, 1024), (2048, 1024)):
@@ -193,18 +198,17 @@ def test_fast_type_pairs(hip, oracle_mod, types):
         ws = np.array([[0.5, 0.3, 0.2], [0.6, 0.2, 0.2], [0.4, 0.4, 0.2]])
         want = [oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist())
                 for tok in range(3)]
-        for path in (0, 2):
-            print(f"fast types={types} H={H} I={I} path={path}", flush=True)
-            old = hip.mqh_set_decode_path(path)
-            try:
-                got, st = run(layer, X, ids, ws)
-                expect_kernels(hip, path, H in (1024, 2048))
-            finally:
-                hip.mqh_set_decode_path(old)
-            assert st == 0
-            for tok in range(3):
-                err = oracle_mod.max_relative_error(got[tok], want[tok])
-                assert err <= TOL, (types, H, I, path, tok, err)
+        print(f"fast types={types} H={H} I={I}", flush=True)
+        old = hip.mqh_set_decode_path(0)
+        try:
+            got, st = run(layer, X, ids, ws)
+            expect_kernels(hip)
+        finally:
+            hip.mqh_set_decode_path(old)
+        assert st == 0
+        for tok in range(3):
+            err = oracle_mod.max_relative_error(got[tok], want[tok])
+            assert err <= TOL, (types, H, I, tok, err)
 
 
 @pytest.mark.parametrize("types,sh_types", [((12, 8), (14, 14)), ((8, 8), (8, 8)), ((8, 14), (14, 14)),
@@ -239,35 +243,9 @@ def test_fast_q8_0(hip, oracle_mod, types, sh_types):
         assert not np.array_equal(got[0], got[1])   # the digit kernels ran, not the FP32 ones
 
 
-def test_single_launch_token_limit(hip, oracle_mod):
-    """The single-launch kernel serves up to 16384 gate/up workgroups (tokens x
-    slots x intermediate/16): 56 tokens of top-8 + shared at I=512 take it, 57
-    fall back to the two kernels; both agree with the oracle."""
-    types = {"gate": 12, "up": 12, "down": 14}
-    layer, host, shared = make_layer(17, 16, 1024, 512, types, shared_types=types)
-    rng = np.random.default_rng(19)
-    for T, kernels in ((56, 1), (57, 2)):
-        X = rng.standard_normal((T, 1024)).astype(np.float32)
-        ids = np.stack([rng.permutation(16)[:8] for _ in range(T)])
-        ws = rng.dirichlet(np.ones(8), size=T).astype(np.float32)
-        old = hip.mqh_set_decode_path(2)
-        try:
-            print(f"single-launch limit T={T}", flush=True)
-            got, st = run(layer, X, ids, ws)
-            assert hip.mqh_last_decode_kernels() == kernels
-        finally:
-            hip.mqh_set_decode_path(old)
-        assert st == 0
-        for tok in (0, T // 2, T - 1):
-            want = oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist())
-            assert oracle_mod.max_relative_error(got[tok], want) <= TOL, (T, tok)
-
-
-@pytest.mark.parametrize("dpath", [0, 2], ids=["two-kernel", "single-launch"])
-def test_fast_repeated_launches_share_workspace(decode_layer, oracle_mod, hip, dpath):
-    """Back-to-back launches on one workspace, read once at the end: each result
-    is its own (the single-launch kernel's handoff words are reset by every
-    launch for the next)."""
+def test_fast_repeated_launches_share_workspace(decode_layer, oracle_mod, hip):
+    """Back-to-back launches on one workspace with no host synchronisation in
+    between, read once at the end: each result is its own."""
     import torch
 
     from flash_moe_hip.moe_gpu import MoeRunner
@@ -278,16 +256,13 @@ def test_fast_repeated_launches_share_workspace(decode_layer, oracle_mod, hip, d
     xs = [rng.standard_normal((1, 2048)).astype(np.float32) for _ in range(5)]
     ids = [rng.permutation(32)[:8].reshape(1, 8) for _ in range(5)]
     ws = [rng.dirichlet(np.ones(8)).astype(np.float32).reshape(1, 8) for _ in range(5)]
+    xd = [torch.from_numpy(v).cuda() for v in xs]
+    idd = [torch.from_numpy(v.astype(np.int32)).cuda() for v in ids]
+    wd = [torch.from_numpy(v).cuda() for v in ws]
     ys = []
-    old = hip.mqh_set_decode_path(dpath)
-    try:
-        for k in range(5):
-            ys.append(runner.decode(layer, torch.from_numpy(xs[k]).cuda(),
-                                    torch.from_numpy(ids[k].astype(np.int32)).cuda(),
-                                    torch.from_numpy(ws[k]).cuda()))
-        expect_kernels(hip, dpath, True)
-    finally:
-        hip.mqh_set_decode_path(old)
+    for k in range(5):
+        ys.append(runner.decode(layer, xd[k], idd[k], wd[k]))
+    expect_kernels(hip)
     assert runner.status() == 0
     for k in range(5):
         want = oracle_layer(oracle_mod, layer, host, shared, xs[k][0], ids[k][0].tolist(), ws[k][0].tolist())

@@ -202,7 +202,7 @@ def test_backend_moe_tokens_uses_prefill(oracle_mod, hip):
             return oracle_mod.route(x, W, 4)
 
     backend = HipExpertBackend({0: layer})
-    sh = SharedExpert(backend)
+    sh = SharedExpert.from_backend(backend)
     X = rng.standard_normal((24, 512)).astype(np.float32)
     got = run_moe_sequence(0, X, Router(), backend, 512, 256, shared_expert=sh)
     worst = 0.0

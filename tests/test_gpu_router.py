@@ -196,8 +196,7 @@ def test_routed_decode_many_tokens_equals_route_then_decode():
     (300, (12, 12, 14), (14, 14, 14), 2, 0, 2),     # more experts than the prologue holds
     (32, (12, 12, 8), None, 2, 0, 1),               # Q8_0 down
     (32, (12, 12, 14), (12, 12, 14), 3, 1, 2),      # generic kernels forced
-    (32, (12, 12, 14), (12, 12, 14), 3, 2, 2),      # single-launch path requested
-], ids=["E256-T1", "E256-T16", "E64-q3k", "E16-noshared", "E300", "q8down", "generic", "single-launch"])
+], ids=["E256-T1", "E256-T16", "E64-q3k", "E16-noshared", "E300", "q8down", "generic"])
 def test_routed_decode_matches_the_oracle_layer(oracle_mod, E, types, sh_types, T, path, route_kernels):
     """Routing and the experts on the device in one call, against the oracle's
     route + run_moe_layer, and bit for bit against route() then decode()."""

@@ -124,6 +124,33 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
                    const float* x, int n_tokens, const int32_t* ids, const float* weights, int top_k,
                    float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Scratch bytes each GPU holds for mqh_moe_decode_noalloc (until the process
+ * ends). */
+#define MQH_NOALLOC_SCRATCH_BYTES (4 << 20)
+
+/* mqh_moe_decode without a workspace: it allocates nothing (no hipMalloc,
+ * hipFree or allocating library call), for callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * it.  No counterpart in the reference.  Same arguments, validation, kernels
+ * and results as mqh_moe_decode; the kernels' scratch (the shared expert's
+ * scale per token and the FP32 SwiGLU activations per (token, slot)) lives in
+ * a library-owned device array of MQH_NOALLOC_SCRATCH_BYTES per GPU, and a
+ * call that needs more (about 4 * n_tokens * (top_k + 1) * intermediate
+ * bytes) returns -6.  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other streams, other host threads) race, so order them
+ * on one stream.  `flags`: device memory of at least 256 bytes (as a
+ * workspace head: zero it once, e.g. with mqh_workspace_init(flags, 256,
+ * stream)); non-finite outputs and bad expert ids latch there as in
+ * mqh_moe_decode, read and cleared with mqh_status(flags, stream).
+ * Returns 0, -1, -2, -5 or -6. */
+int mqh_moe_decode_noalloc(int gate_type, const void* gate, int up_type, const void* up,
+                           int down_type, const void* down, int n_experts, int hidden, int intermediate,
+                           int sh_gate_type, const void* sh_gate, int sh_up_type, const void* sh_up,
+                           int sh_down_type, const void* sh_down, int sh_intermediate,
+                           const float* sh_gate_inp,
+                           const float* x, int n_tokens, const int32_t* ids, const float* weights, int top_k,
+                           float* y, int fp16_graph, int32_t* flags, void* stream);
+
 /* mqh_moe_decode with the routing on the device, for tokens whose router
  * input is already in HBM (ExpertRouter.route, src/flash_moe/router.py:140-170,
  * fused into the decode prologue): router_weights [n_experts x hidden] FP32

@@ -149,6 +149,38 @@ bool odd(const void* p) { return ((uintptr_t)p & 1) != 0; }
 
 }  // namespace
 
+// ------------------------------------------------- decode without allocation
+//
+// The scratch memory of mqh_moe_decode_noalloc: a file-scope device array, one
+// copy per GPU at that GPU's own address, held until the process ends.  Every
+// call on a GPU shares it (overlapping calls on one GPU race).  In host code
+// the name `scratch` is a host-side stand-in, not a device address: host code
+// only ever uses the address hipGetSymbolAddress returns with the device
+// current, looked up on the entry point's first call on each device.
+static __device__ __align__(256) uint8_t scratch[MQH_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int64_t NOALLOC_SCRATCH_BYTES = MQH_NOALLOC_SCRATCH_BYTES;
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[MAX_DEVICES] = {};
+
+// Device address of `scratch` on the current device, or nullptr.
+void* scratch_address() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        g_scratch_addr[dev] = ptr;
+    }
+    return g_scratch_addr[dev];
+}
+
+}  // namespace
+
 extern "C" {
 
 int dequant_k_supported(int type) { return supported(type) ? 1 : 0; }
@@ -427,6 +459,28 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
                                  sh_gate_inp, x, n_tokens, ids, weights, top_k, y, fp16_graph, workspace,
                                  workspace_bytes, p);
     if (st) return st;
+    return launch_decode(p, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
+}
+
+int mqh_moe_decode_noalloc(int gate_type, const void* gate, int up_type, const void* up, int down_type,
+                           const void* down, int n_experts, int hidden, int intermediate, int sh_gate_type,
+                           const void* sh_gate, int sh_up_type, const void* sh_up, int sh_down_type,
+                           const void* sh_down, int sh_intermediate, const float* sh_gate_inp, const float* x,
+                           int n_tokens, const int32_t* ids, const float* weights, int top_k, float* y,
+                           int fp16_graph, int32_t* flags, void* stream) {
+    if (!flags) return ST_ARG;
+    void* ws = scratch_address();
+    if (!ws) return ST_HIP;
+    // the same validation and kernels as mqh_moe_decode, on the scratch array
+    // (-6 when the call needs more than MQH_NOALLOC_SCRATCH_BYTES); the fault
+    // flags go to the caller's words instead of the scratch's own head
+    DecodeParams p;
+    const int st = decode_params(gate_type, gate, up_type, up, down_type, down, n_experts, hidden, intermediate,
+                                 sh_gate_type, sh_gate, sh_up_type, sh_up, sh_down_type, sh_down, sh_intermediate,
+                                 sh_gate_inp, x, n_tokens, ids, weights, top_k, y, fp16_graph, ws,
+                                 NOALLOC_SCRATCH_BYTES, p);
+    if (st) return st;
+    p.flags = (int*)flags;
     return launch_decode(p, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
 }
 

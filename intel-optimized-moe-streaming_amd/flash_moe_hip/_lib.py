@@ -27,6 +27,7 @@ EXPORTS = (
     "mqh_dequant",
     "mqh_moe_workspace_bytes",
     "mqh_moe_decode",
+    "mqh_moe_decode_noalloc",
     "mqh_moe_decode_routed",
     "mqh_last_route_kernels",
     "mqh_moe_prefill_workspace_bytes",
@@ -91,6 +92,13 @@ def _declare(lib: C.CDLL) -> C.CDLL:
         _P, _I, _P, _I64, _P,                    # y, fp16_graph, workspace, ws bytes, stream
     ]
     lib.mqh_moe_decode.restype = _I
+    lib.mqh_moe_decode_noalloc.argtypes = [
+        _I, _P, _I, _P, _I, _P, _I, _I, _I,      # routed types/tensors, n_experts, hidden, inter
+        _I, _P, _I, _P, _I, _P, _I, _P,          # shared types/tensors, sh_inter, sh_gate_inp
+        _P, _I, _P, _P, _I,                      # x, n_tokens, ids, weights, top_k
+        _P, _I, _P, _P,                          # y, fp16_graph, flags, stream
+    ]
+    lib.mqh_moe_decode_noalloc.restype = _I
     lib.mqh_moe_decode_routed.argtypes = [
         _I, _P, _I, _P, _I, _P, _I, _I, _I,      # routed types/tensors, n_experts, hidden, inter
         _I, _P, _I, _P, _I, _P, _I, _P,          # shared types/tensors, sh_inter, sh_gate_inp

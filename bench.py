@@ -305,6 +305,51 @@ CPU_THREADS = 16   # host threads per GPU (the host-CPU share of one MI355X)
 DEQ_TYPES = (11, 12, 14, 8)
 
 
+class StepRunner:
+    """Runs n steps of a sweep over `layers` layers (step i = layer i % layers)
+    as replays of one captured graph of the whole sweep plus, for n % layers,
+    a graph of the first n % layers steps (captured on first use)."""
+
+    def __init__(self, sweep, layers: int, dev, eager: bool = False):
+        self.sweep, self.layers, self.dev, self.eager = sweep, layers, dev, eager
+        self.parts = {}
+
+    def _replay(self, n: int):
+        if n not in self.parts:
+            self.parts[n] = (lambda: self.sweep(n)) if self.eager else _graph(lambda: self.sweep(n), self.dev)
+        return self.parts[n]
+
+    def __call__(self, n: int) -> None:
+        full, rem = divmod(n, self.layers)
+        if full:
+            g = self._replay(self.layers)
+            for _ in range(full):
+                g()
+        if rem:
+            self._replay(rem)()
+
+    def timed(self, n: int) -> float:
+        """ms of GPU time for exactly n steps.  Every graph is captured (and
+        warm) first; a short spin kernel ahead of the start event keeps the GPU
+        busy while the host queues the launches, so the timed region holds the
+        n steps and their graph-node gaps only."""
+        import torch
+
+        full, rem = divmod(n, self.layers)
+        if full:
+            self._replay(self.layers)
+        if rem:
+            self._replay(rem)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(2_000_000)
+        s.record()
+        self(n)
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e)
+
+
 def _graph(fn, dev):
     """Capture fn() (already run once eagerly) as a graph; return its replay."""
     import torch
@@ -853,12 +898,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch every step from Python instead of a graph")
     ap.add_argument("--only-decode", action="store_true", help="skip the batched-decode, prefill and dequant lines")
-    # single_expert (one Q4_K expert, one token) is not in the default set: it runs the
-    # headline's kernel instances, so a profile of the default run would mix its calls
-    # into the headline kernels' averages
-    ap.add_argument("--workloads", default="batched_decode,prefill,dequant,deltanet",
-                    help="comma-separated workloads run after the headline decode "
-                         "(also: single_expert)")
+    # single_expert (one Q4_K expert, one token) runs the headline's gate/up kernel
+    # instance: a profile of the headline kernels leaves it out (--workloads)
+    ap.add_argument("--workloads", default="single_expert,batched_decode,prefill,dequant,deltanet",
+                    help="comma-separated workloads run after the headline decode")
     ap.add_argument("--extra-cpu-seconds", type=float, default=4.0)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (counter calibration)")
@@ -885,16 +928,18 @@ def main() -> int:
     Y = torch.empty((args.layers, H), dtype=torch.float32, device=dev)
     runner = MoeRunner(dev)
 
-    def sweep():
-        for l in range(args.layers):
+    def sweep(n=args.layers):
+        for l in range(n):
             runner.decode(layers[l], X[l:l + 1], IDS[l:l + 1], WS[l:l + 1], y=Y[l:l + 1])
 
-    # eager warm-up (allocates the workspace), parity spot check on layer 0
+    # eager warm-up (allocates the workspace), parity spot check on four layers
     sweep()
     torch.cuda.synchronize()
     assert runner.status() == 0, "kernel fault during warm-up"
-    err = parity_check(layers[0], xs[0], ids[0], ws[0], Y[0].cpu().numpy())
-    log(f"parity vs oracle (layer 0): max rel err {err:.3e}")
+    Yh = Y.cpu().numpy()
+    check = sorted({0, args.layers // 3, 2 * args.layers // 3, args.layers - 1})
+    err = max(parity_check(layers[l], xs[l], ids[l], ws[l], Yh[l]) for l in check)
+    log(f"parity vs oracle (layers {check}): max rel err {err:.3e}")
     if not err <= 1e-3:
         log("PARITY FAILURE")
         return 3
@@ -909,35 +954,16 @@ def main() -> int:
         log(f"calibration copy of {n} bytes done")
         del src, dst
 
-    reps_w = max(1, args.warmup // args.layers)
-    reps = max(1, args.steps // args.layers)
-    graph = None
-    if args.eager:
-        run_sweep = sweep
-    else:
-        # capture one sweep over all layers as a graph
-        graph = torch.cuda.CUDAGraph()
-        cap = torch.cuda.Stream(dev)
-        cap.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(cap):
-            sweep()
-        torch.cuda.current_stream(dev).wait_stream(cap)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=cap):
-            sweep()
-        run_sweep = graph.replay
-    for _ in range(reps_w):
-        run_sweep()
+    # exactly `warmup` untimed and then exactly `steps` timed steps: a step is
+    # one token through one layer; layer l of step i is i % layers, as the
+    # graph of one whole sweep replayed plus a graph of the first
+    # (steps % layers) layers
+    run_steps = StepRunner(sweep, args.layers, dev, eager=args.eager)
+    run_steps(args.warmup)
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        run_sweep()
-    end.record()
-    end.synchronize()
+    ms_total = run_steps.timed(args.steps)
     assert runner.status() == 0, "kernel fault during timing"
-    steps = reps * args.layers
-    ms_total = start.elapsed_time(end)
+    steps = args.steps
     ms_step = ms_total / steps
     nbytes = step_bytes(layers[0])
     gbs = nbytes / (ms_step * 1e-3) / 1e9
@@ -950,35 +976,10 @@ def main() -> int:
     # per-kernel durations: every step of an eager pass over the same layers,
     # each kernel bracketed by HIP events recorded by the runtime at its
     # start and end (mqh_profile_next_decode), on the stream it runs on
-    kern = kernel_times(runner, layers, X, IDS, WS, Y, reps=max(1, min(reps, 10)))
-    if kern["kernels"] == 1:
-        log(f"single-launch kernel {kern['a_us']:.3f} us per launch")
-        kernels_us = {"k_fast_layer": round(kern["a_us"], 3), "launches_each": kern["launches"]}
-    else:
-        log(f"kernel A (gate/up) {kern['a_us']:.3f} us, kernel B (down+combine) {kern['b_us']:.3f} us per launch")
-        kernels_us = {"k_fast_gate_up": round(kern["a_us"], 3), "k_fast_down": round(kern["b_us"], 3),
-                      "launches_each": kern["launches"]}
-
-    # the single-launch kernel on the same layers, for comparison
-    alt = None
-    if not args.eager and kern["kernels"] == 2:
-        from flash_moe_hip import _lib
-
-        lib = _lib.load()
-        old_path = lib.mqh_set_decode_path(2)
-        try:
-            sweep()
-            torch.cuda.synchronize()
-            g2 = _graph(sweep, dev)
-            ms2 = _time(g2, reps) / args.layers
-            k2 = kernel_times(runner, layers, X, IDS, WS, Y, reps=max(1, min(reps, 10)))
-            assert runner.status() == 0
-            if k2["kernels"] == 1:
-                alt = {"us_per_layer": round(ms2 * 1e3, 3), "k_fast_layer": round(k2["a_us"], 3)}
-                log(f"single-launch path: {ms2 * 1e3:.2f} us/layer (kernel {k2['a_us']:.3f} us)")
-            del g2
-        finally:
-            lib.mqh_set_decode_path(old_path)
+    kern = kernel_times(runner, layers, X, IDS, WS, Y, reps=10)
+    log(f"kernel A (gate/up) {kern['a_us']:.3f} us, kernel B (down+combine) {kern['b_us']:.3f} us per launch")
+    kernels_us = {"k_fast_gate_up": round(kern["a_us"], 3), "k_fast_down": round(kern["b_us"], 3),
+                  "launches_each": kern["launches"]}
 
     result = {
         "metric": METRIC,
@@ -986,12 +987,13 @@ def main() -> int:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": reps_w * args.layers,
+        "warmup": args.warmup,
         "ms_per_step": round(ms_step, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32 accumulate; activations as two int8 digits per 16 columns, exact int32 dot products "
+                 "with the 4/6-bit weights",
         "data": "synthetic",
         "config": {
             "workload": "decode MoE layer, 1 token: hidden 2048, 256 experts x intermediate 512, top-8 + "
@@ -1005,20 +1007,18 @@ def main() -> int:
         "kernels_us": kernels_us,
         "roofline": roofline(kern, layers[0], floor=read_floor_us),
     }
-    if alt is not None:
-        result["single_launch_path"] = alt
-    result["routed_decode"] = bench_routed_decode(runner, layers, X, ids, ws, max(1, min(reps, 20)), dev)
+    result["routed_decode"] = bench_routed_decode(runner, layers, X, ids, ws, 20, dev)
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle, 4 threads)")
         result["cpu_baseline"] = cpu_baseline(layers, xs, ids, ws, args.cpu_seconds)
     if not args.only_decode:
-        del layers, graph
+        del layers, run_steps
         torch.cuda.empty_cache()
         cpu_s = 0.0 if args.no_cpu_baseline else args.extra_cpu_seconds
         wanted = set(args.workloads.split(","))
         runs = {
             "single_expert": lambda: bench_single_expert(dev, 50, cpu_s),
-            "batched_decode": lambda: bench_batched_decode(dev, args.layers, args.steps // 4, cpu_s),
+            "batched_decode": lambda: bench_batched_decode(dev, args.layers, 25 * args.layers, cpu_s),
             "prefill": lambda: bench_prefill(dev, 8, 20, cpu_s),
             "dequant": lambda: bench_dequant(dev, 10, cpu_s),
             "deltanet": lambda: bench_deltanet(dev, 50, cpu_s),

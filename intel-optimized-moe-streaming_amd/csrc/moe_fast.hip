@@ -231,17 +231,6 @@ __device__ __forceinline__ void item_loads(const uint8_t* Gm, const uint8_t* Um,
     lane_load<T>(Um + off, k, ru);
 }
 
-// gate and up dot products of one item's lane (type T), summed over the row's lanes
-template <int T, int LPR>
-__device__ __forceinline__ float2 item_dots(const uint32_t* rg, const uint32_t* ru, const DigitsRef& xd, int blk,
-                                            int k) {
-    LaneX X;
-    lane_x<T>(xd, blk, k, X);
-    const float g = lane_dot<T>(rg, k, X);
-    const float u = lane_dot<T>(ru, k, X);
-    return make_float2(lane_group_sum<LPR>(g), lane_group_sum<LPR>(u));
-}
-
 // SGT: the shared expert's gate/up type (its waves take that code path).
 // ROUTED: the router's select step first (p.route_scores set, at most
 // ROUTE_PROLOGUE_MAX_EXPERTS experts).
@@ -279,19 +268,26 @@ __device__ __forceinline__ void gate_up_items(const DecodeParams& p, const FastL
     const float4 gi = *(const float4*)((gate_wg ? p.sh_gate_inp : xt) + xi);   // the shared expert's gate vector
     __builtin_amdgcn_sched_barrier(0);
 
-    const uint8_t *Gm = p.sh_gate, *Um = p.sh_up;
+    // The expert slices: routed expert e, the shared expert, or -- for a wave
+    // past the end -- the first slice, whose first row is read and discarded.
+    // Every wave issues the same loads with no branch around them: a
+    // conditional load makes the compiler's wait counts conservative at the
+    // join, and the token digits below would then wait for the weights.
+    const uint8_t *Gm = p.top_k > 0 ? p.gate : p.sh_gate, *Um = p.top_k > 0 ? p.up : p.sh_up;
+    if (shared) { Gm = p.sh_gate; Um = p.sh_up; }
     bool bad = false;
-    if (live && !shared) {
-        int e = 0;
-        if constexpr (ROUTED) {
-            // routing in the prologue (router.py:140-170): every wave takes the
-            // top s+1 of token t's router scores (the x load above is in flight
-            // meanwhile); the token's first item takes all top_k and writes the
-            // ids and softmax weights for the down kernel and the caller
+    if constexpr (ROUTED) {
+        // routing in the prologue (router.py:140-170): every wave takes the top
+        // s+1 of token t's router scores (the x load above is in flight
+        // meanwhile); the token's first item takes all top_k and writes the ids
+        // and softmax weights for the down kernel and the caller.  Every wave
+        // reads the scores (no conditional load).
+        uint64_t key[ROUTE_PROLOGUE_MAX_EXPERTS / 64];
+        route_keys(p.route_scores + (int64_t)t * p.n_experts, p.n_experts, lane, key);
+        if (live && !shared) {
             const bool publish = item == 0;
-            uint64_t key[ROUTE_PROLOGUE_MAX_EXPERTS / 64];
-            route_keys(p.route_scores + (int64_t)t * p.n_experts, p.n_experts, lane, key);
             const int rounds = publish ? p.top_k : s + 1;
+            int e = 0;
             float mine = 0.0f;
             for (int r = 0; r < rounds; ++r) {
                 const uint64_t win = route_next(key);
@@ -303,10 +299,11 @@ __device__ __forceinline__ void gate_up_items(const DecodeParams& p, const FastL
                 const float w = route_weight(mine, p.top_k, lane);
                 if (lane < p.top_k) p.route_weights[t * p.top_k + lane] = w;
             }
-        } else {
-            e = id_raw;
-            if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }
+            Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
         }
+    } else if (live && !shared) {
+        int e = id_raw;
+        if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }
         Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
     }
 
@@ -316,21 +313,42 @@ __device__ __forceinline__ void gate_up_items(const DecodeParams& p, const FastL
 
     // then every weight load of this lane (waiting for x does not wait for them)
     uint32_t rg[NA], ru[NA];
-    if (live) {
+    if constexpr (SGT == GT) {
+        item_loads<GT, H>(Gm, Um, row, blk, k, rg, ru);
+    } else {
         if (sw) item_loads<SGT, H>(Gm, Um, row, blk, k, rg, ru);
         else item_loads<GT, H>(Gm, Um, row, blk, k, rg, ru);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // 2. token digits (the weight loads are in flight meanwhile)
+    // 2. token digits, and this lane's digit operands out of LDS, while the
+    // weight loads are in flight
     if (threadIdx.x < NX) x_digits<H, NX>(xv, sh.planes, sh.xs16, sh.sum16);
     __syncthreads();
+    DigitsRef xd;
+    xd.planes = sh.planes; xd.xs16 = sh.xs16; xd.sum16 = sh.sum16; xd.n = H;
+    LaneX X;
+    if constexpr (SGT == GT) {
+        lane_x<GT>(xd, blk, k, X);
+    } else {
+        if (sw) lane_x<SGT>(xd, blk, k, X);
+        else lane_x<GT>(xd, blk, k, X);
+    }
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 
     // 3. gate and up dot products, SwiGLU: one FP32 activation per row
     if (live) {
-        DigitsRef xd;
-        xd.planes = sh.planes; xd.xs16 = sh.xs16; xd.sum16 = sh.sum16; xd.n = H;
-        const float2 gu = sw ? item_dots<SGT, LPR>(rg, ru, xd, blk, k) : item_dots<GT, LPR>(rg, ru, xd, blk, k);
-        if (li == 0) p.act[((int64_t)t * p.S + s) * L.inter + row] = bad ? 0.0f : silu_mul(gu.x, gu.y);
+        float g, u;
+        if (sw) {
+            g = lane_dot<SGT>(rg, k, X);
+            u = lane_dot<SGT>(ru, k, X);
+        } else {
+            g = lane_dot<GT>(rg, k, X);
+            u = lane_dot<GT>(ru, k, X);
+        }
+        g = lane_group_sum<LPR>(g);
+        u = lane_group_sum<LPR>(u);
+        if (li == 0) p.act[((int64_t)t * p.S + s) * L.inter + row] = bad ? 0.0f : silu_mul(g, u);
         if (bad && lane == 0 && row0 == 0) atomicOr(&p.flags[FLAG_BAD_ID], 1);
     }
 
@@ -400,60 +418,56 @@ __device__ __forceinline__ void down_slot(const DecodeParams& p, int bx, int t, 
     constexpr int RPI = GeoB<LPR, NPB_>::RPI, NPB = GeoB<LPR, NPB_>::NPB, RB = GeoB<LPR, NPB_>::RB;
     constexpr int64_t ROW_BYTES = (int64_t)(I / 256) * BB;
 
-    const int lane = threadIdx.x & 63, s = uniform(threadIdx.x >> 6);   // wave = slot
-    const bool active = s < p.S;
+    const int lane = threadIdx.x & 63, s = uniform(threadIdx.x >> 6);   // wave = slot (64 * S threads)
     const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
     const int r0 = bx * RB;
     const bool shared = p.has_shared && s == p.top_k;
 
-    LaneX X;
     // the slot's activations first: their address needs no expert id, so the
     // loads go out while the id is still being read
     ActRegs<I> A;
-    if (active) act_load<I>(p.act + ((int64_t)t * p.S + s) * I, lane, A);
+    act_load<I>(p.act + ((int64_t)t * p.S + s) * I, lane, A);
     __builtin_amdgcn_sched_barrier(0);
 
     const uint8_t* D = p.sh_down;
     bool bad = false;
     float w = 0.0f;
-    if (active && !shared) {
+    if (!shared) {
         int e = p.ids[t * p.top_k + s];
         if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }
         D = p.down + (int64_t)e * p.down_eb;
         w = bad ? 0.0f : p.weights[t * p.top_k + s];
     }
 
-    // then every weight load
+    // then every weight load, with no branch around them (a conditional load
+    // makes the compiler's wait counts conservative at the join, and the digit
+    // split below would then wait for the weights)
     uint32_t raw[NPB][N];
-    if (active) {
 #pragma unroll
-        for (int q = 0; q < NPB; ++q)
-            lane_load<DT>(D + (int64_t)(r0 + q * RPI + rr) * ROW_BYTES + blk * BB, k, raw[q]);
-    }
+    for (int q = 0; q < NPB; ++q) lane_load<DT>(D + (int64_t)(r0 + q * RPI + rr) * ROW_BYTES + blk * BB, k, raw[q]);
     __builtin_amdgcn_sched_barrier(0);
-    // the slot's digits into this wave's LDS region while the weights are in
-    // flight; the wave reads them back once its LDS stores are done
-    if (active) {
-        extern __shared__ __attribute__((aligned(16))) uint8_t b_digits[];
-        int8_t* planes = (int8_t*)(b_digits + s * act_lds_bytes(I));
-        float* xs16 = (float*)(planes + 2 * I);
-        float* sum16 = xs16 + I / RUN;
-        act_digits_lds<I>(A, lane, planes, xs16, sum16);
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        DigitsRef xd;
-        xd.planes = planes; xd.xs16 = xs16; xd.sum16 = sum16; xd.n = I;
-        lane_x<DT>(xd, blk, k, X);
-    }
+    // the slot's digits into this wave's LDS region, and this lane's digit
+    // operands back out of it, while the weights are in flight
+    extern __shared__ __attribute__((aligned(16))) uint8_t b_digits[];
+    int8_t* planes = (int8_t*)(b_digits + s * act_lds_bytes(I));
+    float* xs16 = (float*)(planes + 2 * I);
+    float* sum16 = xs16 + I / RUN;
+    act_digits_lds<I>(A, lane, planes, xs16, sum16);
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    DigitsRef xd;
+    xd.planes = planes; xd.xs16 = xs16; xd.sum16 = sum16; xd.n = I;
+    LaneX X;
+    lane_x<DT>(xd, blk, k, X);
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 
-    if (active) {
 #pragma unroll
-        for (int q = 0; q < NPB; ++q) {
-            float v = lane_dot<DT>(raw[q], k, X);
-            v = lane_group_sum<LPR>(v);
-            if (li == 0) sh.s_y[s][q * RPI + rr] = bad ? 0.0f : v;
-        }
-        if (lane == 0) sh.s_w[s] = shared ? p.sh_scale[t] : w;
+    for (int q = 0; q < NPB; ++q) {
+        float v = lane_dot<DT>(raw[q], k, X);
+        v = lane_group_sum<LPR>(v);
+        if (li == 0) sh.s_y[s][q * RPI + rr] = bad ? 0.0f : v;
     }
+    if (lane == 0) sh.s_w[s] = shared ? p.sh_scale[t] : w;
 }
 
 template <int LPR, int NPB_>

@@ -5,7 +5,8 @@ Usage: python intel-optimized-moe-streaming_amd/build_hip.py [--jobs N]
 Every HIP source under csrc/ is compiled to an object with hipcc (device code
 for gfx950 only) and linked into flash_moe_hip/libmoe_quant_hip.so, the
 library the Python package and the tests load.  Packed FP32 instructions are
-disabled for all device code.
+disabled for all device code; the first 16 kernel-argument dwords are
+preloaded into scalar registers.
 """
 from __future__ import annotations
 
@@ -31,6 +32,9 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # leading scalar kernel arguments arrive in SGPRs (gfx950 kernel-argument
+    # preloading): the decode kernels' first loads need no argument round trip
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

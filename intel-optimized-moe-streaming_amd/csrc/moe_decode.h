@@ -20,13 +20,27 @@ constexpr int ROWS_W = 4;    // hidden rows per wavefront, kernel B
 constexpr int ROWS_B = 4 * ROWS_W;
 
 struct DecodeParams {
+    // The first 64 bytes are what the fast kernels need before their first
+    // loads (the token, the expert ids, the activations and the geometry of
+    // the work split); the kernels take this struct as their only argument and
+    // are built to preload the first 16 argument dwords into scalar registers,
+    // so these are in registers when the first instruction runs.
+    const float* x;         // [n_tokens x hidden]
+    const int32_t* ids;     // [n_tokens x top_k]
+    float* act;             // [n_tokens x S x Imax]
+    const float* weights;   // [n_tokens x top_k]
+    const float* sh_gate_inp;  // optional sigmoid gate vector [hidden] of the shared expert
+    int top_k;
+    int S, has_shared;      // slots per token (top_k + has_shared); has_shared: 0 or 1
+    int n_experts;
+    int a_inter;            // fast kernels: the activation row length (routed, else shared intermediate)
+    int a_waves;            // fast kernels: waves per gate/up workgroup (blockDim.x / 64)
     // routed experts: stacked GGUF tensors, n_experts consecutive slices each
     const uint8_t* gate;
     const uint8_t* up;
     const uint8_t* down;
     int gate_type, up_type, down_type;
     int64_t gate_eb, up_eb, down_eb;  // bytes per expert slice
-    int n_experts;
     int hidden, inter;
     // shared expert (has_shared == 0: absent)
     const uint8_t* sh_gate;
@@ -34,14 +48,7 @@ struct DecodeParams {
     const uint8_t* sh_down;
     int sh_gate_type, sh_up_type, sh_down_type;
     int sh_inter;
-    const float* sh_gate_inp;  // optional sigmoid gate vector [hidden]
-    int has_shared;
-    // tokens
-    const float* x;         // [n_tokens x hidden]
     int n_tokens;
-    const int32_t* ids;     // [n_tokens x top_k]
-    const float* weights;   // [n_tokens x top_k]
-    int top_k;
     // routing in the gate/up prologue (route_scores != nullptr, fast path,
     // n_experts <= ROUTE_PROLOGUE_MAX_EXPERTS): router scores [n_tokens x
     // n_experts] in; the top-k ids and weights are written to route_ids /
@@ -54,8 +61,7 @@ struct DecodeParams {
     // workspace views
     int* flags;             // [N_FLAGS]
     float* sh_scale;        // [n_tokens]
-    float* act;             // [n_tokens x S x Imax]
-    int S, Imax;
+    int Imax;
 };
 
 struct WorkspaceLayout {
@@ -74,13 +80,6 @@ inline WorkspaceLayout decode_workspace_layout(int n_tokens, int top_k, int inte
     w.total = align256(w.act_off + (int64_t)n_tokens * S * Imax * 4);
     return w;
 }
-
-// Geometry of the fast decode kernels: the activations of (token, slot) are
-// FP32 rows of `inter` values in the workspace.
-struct FastLayout {
-    int inter;
-    int a_waves;   // waves per kernel-A workgroup (blockDim.x / 64)
-};
 
 // Grouped prefill (moe_prefill.hip).  Token/slot pairs are bucketed by expert
 // on the device; a tile is up to PREFILL_TILE tokens of one expert (or of the
@@ -142,7 +141,6 @@ hipError_t launch_delta_heads(float* state, const float* q, const float* k, cons
                               const float* gate, float* out, int heads, int key_dim, int value_dim, int* flags,
                               hipStream_t stream, const KernelEvents& ev);
 bool fast_supported(const DecodeParams& p);
-FastLayout fast_layout(int inter);
 hipError_t launch_decode_fast(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev);
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream, const KernelEvents& ev);
 hipError_t launch_dequant(int type, const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream);

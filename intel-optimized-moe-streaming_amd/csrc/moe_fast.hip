@@ -44,6 +44,21 @@ namespace mqh {
 constexpr int FAST_MAX_SLOTS = 16;
 constexpr int RUN = 16;          // activation digit run (columns sharing one scale)
 
+// What a fast kernel needs before its first loads: the token, the expert ids,
+// the activations and the work split.  The kernels take these as their
+// leading scalar arguments (the rest of DecodeParams follows), so that the
+// build's kernel-argument preloading puts them in scalar registers before the
+// first instruction: the expert-id load goes out at once instead of after a
+// round trip to the argument block.
+struct DecodeHot {
+    const float* x;
+    const int32_t* ids;
+    float* act;
+    const float* weights;
+    const float* sh_gate_inp;
+    int top_k, S, has_shared, n_experts, a_inter, a_waves;
+};
+
 // silu(g) * u with the hardware exp2 and reciprocal (a few ulp; the FP32 graph
 // of moe_quant_dot.cpp:200-206 with std::exp and a division)
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -235,24 +250,23 @@ __device__ __forceinline__ void item_loads(const uint8_t* Gm, const uint8_t* Um,
 // ROUTED: the router's select step first (p.route_scores set, at most
 // ROUTE_PROLOGUE_MAX_EXPERTS experts).
 template <int GT, int SGT, int LPR, bool ROUTED>
-__device__ __forceinline__ void gate_up_items(const DecodeParams& p, const FastLayout& L, SharedX<64 * LPR>& sh) {
+__device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodeParams& p, SharedX<64 * LPR>& sh) {
     constexpr int H = 64 * LPR, RPI = 64 / LPR, NX = H / 4;   // NX threads hold the token, four values each
     constexpr int NA = LaneGeo<GT>::NRAW > LaneGeo<SGT>::NRAW ? LaneGeo<GT>::NRAW : LaneGeo<SGT>::NRAW;
     const int t = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // this wave's item, slot and expert-id address, before the first loads so
-    // that their kernel arguments come in with the token's (L.a_waves =
-    // blockDim.x / 64 as an argument: blockDim.x is a 16-bit field that takes
-    // a vector load and a full wait); items per slot are a power of two
-    const int per_slot = L.inter / RPI;
-    const int item = uniform((int)blockIdx.x * L.a_waves + wave);
-    const bool live = item < p.S * per_slot;
+    // this wave's item, slot and expert-id address, from preloaded arguments
+    // (h.a_waves = blockDim.x / 64: blockDim.x is a 16-bit field that takes a
+    // vector load and a full wait); items per slot are a power of two
+    const int per_slot = h.a_inter / RPI;
+    const int item = uniform((int)blockIdx.x * h.a_waves + wave);
+    const bool live = item < h.S * per_slot;
     const int s = live ? item >> __builtin_ctz(per_slot) : 0;
     const int row0 = live ? (item & (per_slot - 1)) * RPI : 0;
     // (bitwise: a short-circuit would branch on its first kernel argument)
-    const bool shared = live & (p.has_shared != 0) & (s == p.top_k);
-    const bool scale_wg = (p.has_shared != 0) & (blockIdx.x == gridDim.x - 1);
-    const bool gate_wg = scale_wg & (p.sh_gate_inp != nullptr);
+    const bool shared = live & (h.has_shared != 0) & (s == h.top_k);
+    const bool scale_wg = (h.has_shared != 0) & (blockIdx.x == gridDim.x - 1);
+    const bool gate_wg = scale_wg & (h.sh_gate_inp != nullptr);
 
     // 1. the token's values and the expert id, together and before any branch
     // (each branch would wait for its own kernel-argument loads): threads past
@@ -260,12 +274,12 @@ __device__ __forceinline__ void gate_up_items(const DecodeParams& p, const FastL
     // vector's load re-reads the token, and a wave with no id to read (shared
     // slot, past the end, routed in the prologue) reads the token's first word;
     // none of these is used.
-    const float* xt = p.x + (int64_t)t * H;
+    const float* xt = h.x + (int64_t)t * H;
     const int xi = min((int)threadIdx.x, NX - 1) * 4;
     const bool id_item = !ROUTED & live & !shared;
-    const int id_raw = *(id_item ? p.ids + (t * p.top_k + s) : (const int32_t*)xt);
+    const int id_raw = *(id_item ? h.ids + (t * h.top_k + s) : (const int32_t*)xt);
     const float4 xv = *(const float4*)(xt + xi);
-    const float4 gi = *(const float4*)((gate_wg ? p.sh_gate_inp : xt) + xi);   // the shared expert's gate vector
+    const float4 gi = *(const float4*)((gate_wg ? h.sh_gate_inp : xt) + xi);   // the shared expert's gate vector
     __builtin_amdgcn_sched_barrier(0);
 
     // The expert slices: routed expert e, the shared expert, or -- for a wave
@@ -273,7 +287,7 @@ __device__ __forceinline__ void gate_up_items(const DecodeParams& p, const FastL
     // Every wave issues the same loads with no branch around them: a
     // conditional load makes the compiler's wait counts conservative at the
     // join, and the token digits below would then wait for the weights.
-    const uint8_t *Gm = p.top_k > 0 ? p.gate : p.sh_gate, *Um = p.top_k > 0 ? p.up : p.sh_up;
+    const uint8_t *Gm = h.top_k > 0 ? p.gate : p.sh_gate, *Um = h.top_k > 0 ? p.up : p.sh_up;
     if (shared) { Gm = p.sh_gate; Um = p.sh_up; }
     bool bad = false;
     if constexpr (ROUTED) {
@@ -283,27 +297,27 @@ __device__ __forceinline__ void gate_up_items(const DecodeParams& p, const FastL
         // and softmax weights for the down kernel and the caller.  Every wave
         // reads the scores (no conditional load).
         uint64_t key[ROUTE_PROLOGUE_MAX_EXPERTS / 64];
-        route_keys(p.route_scores + (int64_t)t * p.n_experts, p.n_experts, lane, key);
+        route_keys(p.route_scores + (int64_t)t * h.n_experts, h.n_experts, lane, key);
         if (live && !shared) {
             const bool publish = item == 0;
-            const int rounds = publish ? p.top_k : s + 1;
+            const int rounds = publish ? h.top_k : s + 1;
             int e = 0;
             float mine = 0.0f;
             for (int r = 0; r < rounds; ++r) {
                 const uint64_t win = route_next(key);
                 if (r == s) e = key_expert(win);
                 if (lane == r) mine = key_score(win);
-                if (publish && lane == 0) p.route_ids[t * p.top_k + r] = key_expert(win);
+                if (publish && lane == 0) p.route_ids[t * h.top_k + r] = key_expert(win);
             }
             if (publish) {
-                const float w = route_weight(mine, p.top_k, lane);
-                if (lane < p.top_k) p.route_weights[t * p.top_k + lane] = w;
+                const float w = route_weight(mine, h.top_k, lane);
+                if (lane < h.top_k) p.route_weights[t * h.top_k + lane] = w;
             }
             Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
         }
     } else if (live && !shared) {
         int e = id_raw;
-        if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }
+        if (e < 0 || e >= h.n_experts) { bad = true; e = 0; }
         Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
     }
 
@@ -348,7 +362,7 @@ __device__ __forceinline__ void gate_up_items(const DecodeParams& p, const FastL
         }
         g = lane_group_sum<LPR>(g);
         u = lane_group_sum<LPR>(u);
-        if (li == 0) p.act[((int64_t)t * p.S + s) * L.inter + row] = bad ? 0.0f : silu_mul(g, u);
+        if (li == 0) h.act[((int64_t)t * h.S + s) * h.a_inter + row] = bad ? 0.0f : silu_mul(g, u);
         if (bad && lane == 0 && row0 == 0) atomicOr(&p.flags[FLAG_BAD_ID], 1);
     }
 
@@ -375,17 +389,23 @@ __device__ __forceinline__ void gate_up_items(const DecodeParams& p, const FastL
 }
 
 template <int GT, int SGT, int LPR>
-__global__ __launch_bounds__(1024) void k_fast_gate_up(DecodeParams p, FastLayout L) {
+__global__ __launch_bounds__(1024) void k_fast_gate_up(const float* x, const int32_t* ids, float* act, const float* sh_gate_inp, int top_k,
+                                                  int S, int has_shared, int n_experts, int a_inter, int a_waves,
+                                                  DecodeParams p) {
     __shared__ SharedX<64 * LPR> sh;
-    gate_up_items<GT, SGT, LPR, false>(p, L, sh);
+    const DecodeHot h{x, ids, act, nullptr, sh_gate_inp, top_k, S, has_shared, n_experts, a_inter, a_waves};
+    gate_up_items<GT, SGT, LPR, false>(h, p, sh);
 }
 
 // Kernel A with the router's select step in its prologue: the same work as
 // k_fast_gate_up once each wave knows its expert.
 template <int GT, int SGT, int LPR>
-__global__ __launch_bounds__(1024) void k_fast_gate_up_routed(DecodeParams p, FastLayout L) {
+__global__ __launch_bounds__(1024) void k_fast_gate_up_routed(const float* x, const int32_t* ids, float* act, const float* sh_gate_inp, int top_k,
+                                                  int S, int has_shared, int n_experts, int a_inter, int a_waves,
+                                                  DecodeParams p) {
     __shared__ SharedX<64 * LPR> sh;
-    gate_up_items<GT, SGT, LPR, true>(p, L, sh);
+    const DecodeHot h{x, ids, act, nullptr, sh_gate_inp, top_k, S, has_shared, n_experts, a_inter, a_waves};
+    gate_up_items<GT, SGT, LPR, true>(h, p, sh);
 }
 
 // ---------------------------------------------------------------- kernel B
@@ -411,7 +431,8 @@ struct SharedB {
 // order.  down_slot is the calling wave's part (its slot's rows into LDS, with
 // the slot's weight type DT), down_combine the workgroup's.
 template <int DT, int LPR, int NPB_ = 1>
-__device__ __forceinline__ void down_slot(const DecodeParams& p, int bx, int t, SharedB<GeoB<LPR, NPB_>::RB>& sh) {
+__device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams& p, int bx, int t,
+                                          SharedB<GeoB<LPR, NPB_>::RB>& sh) {
     constexpr int N = LaneGeo<DT>::NRAW;
     constexpr int BB = unit_bytes(DT);
     constexpr int I = 64 * LPR;
@@ -421,22 +442,22 @@ __device__ __forceinline__ void down_slot(const DecodeParams& p, int bx, int t, 
     const int lane = threadIdx.x & 63, s = uniform(threadIdx.x >> 6);   // wave = slot (64 * S threads)
     const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
     const int r0 = bx * RB;
-    const bool shared = p.has_shared && s == p.top_k;
+    const bool shared = h.has_shared && s == h.top_k;
 
     // the slot's activations first: their address needs no expert id, so the
     // loads go out while the id is still being read
     ActRegs<I> A;
-    act_load<I>(p.act + ((int64_t)t * p.S + s) * I, lane, A);
+    act_load<I>(h.act + ((int64_t)t * h.S + s) * I, lane, A);
     __builtin_amdgcn_sched_barrier(0);
 
     const uint8_t* D = p.sh_down;
     bool bad = false;
     float w = 0.0f;
     if (!shared) {
-        int e = p.ids[t * p.top_k + s];
-        if (e < 0 || e >= p.n_experts) { bad = true; e = 0; }
+        int e = h.ids[t * h.top_k + s];
+        if (e < 0 || e >= h.n_experts) { bad = true; e = 0; }
         D = p.down + (int64_t)e * p.down_eb;
-        w = bad ? 0.0f : p.weights[t * p.top_k + s];
+        w = bad ? 0.0f : h.weights[t * h.top_k + s];
     }
 
     // then every weight load, with no branch around them (a conditional load
@@ -471,15 +492,16 @@ __device__ __forceinline__ void down_slot(const DecodeParams& p, int bx, int t, 
 }
 
 template <int LPR, int NPB_>
-__device__ __forceinline__ void down_combine(const DecodeParams& p, int bx, int t, SharedB<GeoB<LPR, NPB_>::RB>& sh) {
+__device__ __forceinline__ void down_combine(const DecodeHot& h, const DecodeParams& p, int bx, int t,
+                                             SharedB<GeoB<LPR, NPB_>::RB>& sh) {
     constexpr int RB = GeoB<LPR, NPB_>::RB;
     __syncthreads();
     // combine in top-k order, then the shared expert (moe_layer.py:70-106)
     if (threadIdx.x < RB) {
         const int r = threadIdx.x;
         float acc = 0.0f;
-        for (int j = 0; j < p.top_k; ++j) acc = __fadd_rn(acc, __fmul_rn(sh.s_w[j], sh.s_y[j][r]));
-        if (p.has_shared) acc = __fadd_rn(acc, __fmul_rn(sh.s_w[p.top_k], sh.s_y[p.top_k][r]));
+        for (int j = 0; j < h.top_k; ++j) acc = __fadd_rn(acc, __fmul_rn(sh.s_w[j], sh.s_y[j][r]));
+        if (h.has_shared) acc = __fadd_rn(acc, __fmul_rn(sh.s_w[h.top_k], sh.s_y[h.top_k][r]));
         p.y[(int64_t)t * p.hidden + bx * RB + r] = acc;
         if (!isfinite(acc)) atomicOr(&p.flags[FLAG_NONFINITE], 1);
     }
@@ -487,16 +509,18 @@ __device__ __forceinline__ void down_combine(const DecodeParams& p, int bx, int 
 
 // SDT: the shared expert's down type (its wave takes that code path).
 template <int DT, int SDT, int LPR, int NPB>
-__global__ __launch_bounds__(1024) void k_fast_down(DecodeParams p, FastLayout L) {
+__global__ __launch_bounds__(1024) void k_fast_down(const int32_t* ids, float* act, const float* weights, int top_k,
+                                                   int S, int has_shared, int n_experts, DecodeParams p) {
     __shared__ SharedB<GeoB<LPR, NPB>::RB> sh;
+    const DecodeHot h{nullptr, ids, act, weights, nullptr, top_k, S, has_shared, n_experts, 0, 0};
     if constexpr (SDT != DT) {
         const int s = uniform(threadIdx.x >> 6);
-        if (p.has_shared && s == p.top_k) down_slot<SDT, LPR, NPB>(p, blockIdx.x, blockIdx.y, sh);
-        else down_slot<DT, LPR, NPB>(p, blockIdx.x, blockIdx.y, sh);
+        if (has_shared && s == top_k) down_slot<SDT, LPR, NPB>(h, p, blockIdx.x, blockIdx.y, sh);
+        else down_slot<DT, LPR, NPB>(h, p, blockIdx.x, blockIdx.y, sh);
     } else {
-        down_slot<DT, LPR, NPB>(p, blockIdx.x, blockIdx.y, sh);
+        down_slot<DT, LPR, NPB>(h, p, blockIdx.x, blockIdx.y, sh);
     }
-    down_combine<LPR, NPB>(p, blockIdx.x, blockIdx.y, sh);
+    down_combine<LPR, NPB>(h, p, blockIdx.x, blockIdx.y, sh);
 }
 
 // ------------------------------------------------------------------ launch
@@ -526,13 +550,6 @@ bool fast_supported(const DecodeParams& p) {
     // kernel B holds every slot's digits in LDS (64 KiB per workgroup, its
     // static part below 4 KiB)
     return fast_dim(inter) && (int64_t)p.S * act_lds_bytes(inter) <= 65536 - 4096;
-}
-
-FastLayout fast_layout(int inter) {
-    FastLayout L;
-    L.inter = inter;
-    L.a_waves = 0;
-    return L;
 }
 
 // Compute units of the current device (cached per device).
@@ -571,42 +588,39 @@ static int gate_up_waves(int items, int tokens, int hidden, int cus) {
 }
 
 template <int GT, int SGT, int LPR>
-static void launch_a(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
+static void launch_a(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     const int items = p.S * (p.inter / (64 / LPR));
     const int w = gate_up_waves(items, p.n_tokens, 64 * LPR, device_cus());
     const dim3 grid((items + w - 1) / w, p.n_tokens), block(64 * w);
-    FastLayout LA = L;
-    LA.a_waves = w;
     if (p.route_scores != nullptr) {
         if (ev.armed_a())
             hipExtLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, block, 0, stream, ev.a_start,
-                                  ev.a_stop, 0, p, LA);
+                                  ev.a_stop, 0, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
         else
-            hipLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, block, 0, stream, p, LA);
+            hipLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
         return;
     }
     if (ev.armed_a())
-        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p,
-                              LA);
+        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
     else
-        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, block, 0, stream, p, LA);
+        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
 }
 
 template <int GT, int SGT>
-static void launch_a_h(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
+static void launch_a_h(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     switch (p.hidden) {
-        case 256: launch_a<GT, SGT, 4>(p, L, stream, ev); break;
-        case 512: launch_a<GT, SGT, 8>(p, L, stream, ev); break;
-        case 1024: launch_a<GT, SGT, 16>(p, L, stream, ev); break;
-        default: launch_a<GT, SGT, 32>(p, L, stream, ev); break;
+        case 256: launch_a<GT, SGT, 4>(p, stream, ev); break;
+        case 512: launch_a<GT, SGT, 8>(p, stream, ev); break;
+        case 1024: launch_a<GT, SGT, 16>(p, stream, ev); break;
+        default: launch_a<GT, SGT, 32>(p, stream, ev); break;
     }
 }
 
 // a shared expert of another type is Q6_K (fast_supported admits no other)
 template <int GT>
-static void launch_a_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
-    if (p.has_shared && p.top_k > 0 && p.sh_gate_type != GT) launch_a_h<GT, T_Q6_K>(p, L, stream, ev);
-    else launch_a_h<GT, GT>(p, L, stream, ev);
+static void launch_a_t(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
+    if (p.has_shared && p.top_k > 0 && p.sh_gate_type != GT) launch_a_h<GT, T_Q6_K>(p, stream, ev);
+    else launch_a_h<GT, GT>(p, stream, ev);
 }
 
 #ifndef FAST_DOWN_WG_TARGET
@@ -614,45 +628,45 @@ static void launch_a_t(const DecodeParams& p, const FastLayout& L, hipStream_t s
 #endif
 
 template <int DT, int SDT, int LPR, int NPB>
-static void launch_b_n(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
+static void launch_b_n(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     dim3 grid(p.hidden / GeoB<LPR, NPB>::RB, p.n_tokens);
     const size_t lds = (size_t)p.S * act_lds_bytes(64 * LPR);   // the slots' digits
     if (ev.armed_b())
         hipExtLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), lds, stream, ev.b_start,
-                              ev.b_stop, 0, p, L);
+                              ev.b_stop, 0, p.ids, p.act, p.weights, p.top_k, p.S, p.has_shared, p.n_experts, p);
     else
-        hipLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), lds, stream, p, L);
+        hipLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), lds, stream, p.ids, p.act, p.weights, p.top_k, p.S, p.has_shared, p.n_experts, p);
 }
 
 // Row groups per wave: one while the grid is small (a single token: every
 // workgroup on its own CU), more when many tokens would otherwise make many
 // short workgroups.
 template <int DT, int SDT, int LPR>
-static void launch_b_s(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
+static void launch_b_s(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     const int64_t wg1 = (int64_t)(p.hidden / GeoB<LPR, 1>::RB) * p.n_tokens;
     constexpr bool wide = LaneGeo<DT>::NRAW > 12 || LaneGeo<SDT>::NRAW > 12;   // four row groups would spill
     if (!wide && wg1 >= 4 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 4>::RB >= 1)
-        launch_b_n<DT, SDT, LPR, wide ? 2 : 4>(p, L, stream, ev);
+        launch_b_n<DT, SDT, LPR, wide ? 2 : 4>(p, stream, ev);
     else if (wg1 >= 2 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 2>::RB >= 1)
-        launch_b_n<DT, SDT, LPR, 2>(p, L, stream, ev);
+        launch_b_n<DT, SDT, LPR, 2>(p, stream, ev);
     else
-        launch_b_n<DT, SDT, LPR, 1>(p, L, stream, ev);
+        launch_b_n<DT, SDT, LPR, 1>(p, stream, ev);
 }
 
 // a shared expert of another type is Q6_K (fast_supported admits no other)
 template <int DT, int LPR>
-static void launch_b(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
-    if (p.has_shared && p.top_k > 0 && p.sh_down_type != DT) launch_b_s<DT, T_Q6_K, LPR>(p, L, stream, ev);
-    else launch_b_s<DT, DT, LPR>(p, L, stream, ev);
+static void launch_b(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
+    if (p.has_shared && p.top_k > 0 && p.sh_down_type != DT) launch_b_s<DT, T_Q6_K, LPR>(p, stream, ev);
+    else launch_b_s<DT, DT, LPR>(p, stream, ev);
 }
 
 template <int DT>
-static void launch_b_t(const DecodeParams& p, const FastLayout& L, hipStream_t stream, const KernelEvents& ev) {
+static void launch_b_t(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     switch (p.inter) {
-        case 256: launch_b<DT, 4>(p, L, stream, ev); break;
-        case 512: launch_b<DT, 8>(p, L, stream, ev); break;
-        case 1024: launch_b<DT, 16>(p, L, stream, ev); break;
-        default: launch_b<DT, 32>(p, L, stream, ev); break;
+        case 256: launch_b<DT, 4>(p, stream, ev); break;
+        case 512: launch_b<DT, 8>(p, stream, ev); break;
+        case 1024: launch_b<DT, 16>(p, stream, ev); break;
+        default: launch_b<DT, 32>(p, stream, ev); break;
     }
 }
 
@@ -662,22 +676,22 @@ hipError_t launch_decode_fast(const DecodeParams& p0, hipStream_t stream, const 
         p.gate_type = p.sh_gate_type; p.up_type = p.sh_up_type; p.down_type = p.sh_down_type;
         p.inter = p.sh_inter;
     }
-    const FastLayout L = fast_layout(p.inter);
+    p.a_inter = p.inter;
     switch (p.gate_type) {
-        case T_Q4_K: launch_a_t<T_Q4_K>(p, L, stream, ev); break;
-        case T_Q5_K: launch_a_t<T_Q5_K>(p, L, stream, ev); break;
-        case T_Q6_K: launch_a_t<T_Q6_K>(p, L, stream, ev); break;
-        case T_Q8_0: launch_a_t<T_Q8_0>(p, L, stream, ev); break;
-        default: launch_a_t<T_Q3_K>(p, L, stream, ev); break;
+        case T_Q4_K: launch_a_t<T_Q4_K>(p, stream, ev); break;
+        case T_Q5_K: launch_a_t<T_Q5_K>(p, stream, ev); break;
+        case T_Q6_K: launch_a_t<T_Q6_K>(p, stream, ev); break;
+        case T_Q8_0: launch_a_t<T_Q8_0>(p, stream, ev); break;
+        default: launch_a_t<T_Q3_K>(p, stream, ev); break;
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     switch (p.down_type) {
-        case T_Q4_K: launch_b_t<T_Q4_K>(p, L, stream, ev); break;
-        case T_Q5_K: launch_b_t<T_Q5_K>(p, L, stream, ev); break;
-        case T_Q6_K: launch_b_t<T_Q6_K>(p, L, stream, ev); break;
-        case T_Q8_0: launch_b_t<T_Q8_0>(p, L, stream, ev); break;
-        default: launch_b_t<T_Q3_K>(p, L, stream, ev); break;
+        case T_Q4_K: launch_b_t<T_Q4_K>(p, stream, ev); break;
+        case T_Q5_K: launch_b_t<T_Q5_K>(p, stream, ev); break;
+        case T_Q6_K: launch_b_t<T_Q6_K>(p, stream, ev); break;
+        case T_Q8_0: launch_b_t<T_Q8_0>(p, stream, ev); break;
+        default: launch_b_t<T_Q3_K>(p, stream, ev); break;
     }
     return hipGetLastError();
 }

@@ -257,7 +257,7 @@ def _hip_runtime():
     return rt
 
 
-def kernel_times(runner, layers, X, IDS, WS, Y, reps: int) -> dict:
+def kernel_times(runner, layers, X, IDS, WS, Y, reps: int, fp16_graph: int = 0) -> dict:
     """Average duration of each decode kernel: an eager pass of reps x layers
     steps, every kernel launched with start/stop HIP events."""
     import ctypes as C
@@ -280,7 +280,8 @@ def kernel_times(runner, layers, X, IDS, WS, Y, reps: int) -> dict:
         l = i % len(layers)
         _lib.check(lib.mqh_profile_next_decode(ev[4 * i], ev[4 * i + 1], ev[4 * i + 2], ev[4 * i + 3]),
                    "mqh_profile_next_decode")
-        runner.decode(layers[l], X[l:l + 1], IDS[l:l + 1], WS[l:l + 1], y=Y[l:l + 1], stream=stream)
+        runner.decode(layers[l], X[l:l + 1], IDS[l:l + 1], WS[l:l + 1], y=Y[l:l + 1], stream=stream,
+                      fp16_graph=fp16_graph)
     torch.cuda.synchronize()
 
     def ms(a, b):
@@ -762,6 +763,76 @@ def _delta_kernel_us(states, ins, outs, reps: int) -> float:
     return float(np.mean(us))
 
 
+def bench_fp16_graph_decode(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
+    """The headline decode step in the FP16 graph (fp16_graph=1), the
+    reference's production mode (native_expert.py:33-34): x, every decoded
+    weight, g, u, the sigmoid, silu, the activation and y rounded to FP16 at the
+    points of moe_quant_dot.cpp:189-211.  At the headline's scales the FP16
+    graph overflows (the reference returns -4 there too), so the layers use the
+    reference's FP16-graph check scales: super-block scales |N(0,1)| * 0.002,
+    x ~ N(0,1) * 0.05.  Same shape, types and routing as the headline."""
+    import torch
+
+    from flash_moe_hip.layer_store import ExpertLayer
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    layers = [ExpertLayer.synthetic(TYPES, E, H, I, seed=1000 * l + 1, shared_types=TYPES, shared_intermediate=I,
+                                    gate_inp=True, scale=0.002, device=dev) for l in range(n_layers)]
+    xs, ids, ws = route_layers(n_layers, layers=layers)
+    xs = (xs * 0.05).astype(np.float32)
+    X, IDS, WS = (torch.from_numpy(a).to(dev) for a in (xs, ids, ws))
+    Y = torch.empty((n_layers, H), dtype=torch.float32, device=dev)
+    runner = MoeRunner(dev)
+
+    def sweep(n=n_layers):
+        for l in range(n):
+            runner.decode(layers[l], X[l:l + 1], IDS[l:l + 1], WS[l:l + 1], y=Y[l:l + 1], fp16_graph=1)
+
+    sweep()
+    torch.cuda.synchronize()
+    assert runner.status() == 0
+    import oracle
+
+    L0 = layers[0]
+    outs = [oracle.expert_forward(L0.host_expert(int(e)), TYPES, xs[0], H, I, 1) for e in ids[0]]
+    gate = oracle._sigmoid(np.float32(xs[0] @ L0.shared.gate_inp.cpu().numpy()).reshape(()))
+    sh = (gate * oracle.expert_forward(L0.host_shared(), TYPES, xs[0], H, I, 0)).astype(np.float32)
+    err = oracle.max_relative_error(Y[0].cpu().numpy(), oracle.combine(outs, [float(v) for v in ws[0]], sh))
+    ms = _time(_graph(sweep, dev), reps) / n_layers
+    kern = kernel_times(runner, layers, X, IDS, WS, Y, reps=4, fp16_graph=1)
+    log(f"FP16-graph decode: {ms * 1e3:.2f} us/layer, parity {err:.2e}; kernels {kern['a_us']:.2f} / "
+        f"{kern['b_us']:.2f} us")
+    a_bytes = (K + 1) * (L0.expert_bytes("gate") + L0.expert_bytes("up"))
+    dom = "A" if kern["a_us"] >= kern["b_us"] else "B"
+    out = {
+        "workload": f"the headline decode step in the FP16 graph (fp16_graph=1): hidden {H}, {E} experts x "
+                    f"intermediate {I}, top-8 + shared, gate/up Q4_K, down Q6_K, super-block scales |N|*0.002, "
+                    f"x ~ N(0,1)*0.05; {n_layers} resident layers rotated",
+        "metric": "quant-weight GB/s per layer-step", "value": round(step_bytes(L0) / (ms * 1e-3) / 1e9, 1),
+        "unit": "GB/s", "us_per_layer": round(ms * 1e3, 3), "parity_max_rel_err": float(f"{err:.3e}"),
+        "kernels_us": {"A": round(kern["a_us"], 3), "B": round(kern["b_us"], 3)},
+        "roofline": _hbm_roofline("mqh::k_gate_up" if dom == "A" else "mqh::k_down_combine",
+                                  a_bytes if dom == "A" else step_bytes(L0) - a_bytes,
+                                  kern["a_us"] if dom == "A" else kern["b_us"]),
+    }
+    if cpu_seconds > 0:
+        oracle.lib()
+        jobs = [L0.host_expert(int(e)) for e in ids[0]]
+        done, t0 = 0, time.perf_counter()
+        with ThreadPoolExecutor(4) as pool:
+            while time.perf_counter() - t0 < cpu_seconds:
+                list(pool.map(lambda t: oracle.expert_forward(t, TYPES, xs[0], H, I, 1), jobs))
+                done += 1
+        dt = time.perf_counter() - t0
+        per = dt / done * (K + 1) / K
+        out["cpu_baseline"] = {"value": round(step_bytes(L0) / per / 1e9, 3), "unit": "GB/s", "cores": 4,
+                               "kind": "port", "us_per_layer": round(per * 1e6, 1),
+                               "sample": f"{done} x 8 FP16-graph expert calls on 4 threads, {dt:.1f} s"}
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_single_expert(dev, reps: int, cpu_seconds: float) -> dict:
     """One Q4_K expert (gate/up [512x2048], down [2048x512]), one token, x ~ N(0,1),
     seed 0 (the reference's single-expert decode): 40 such experts resident and
@@ -900,7 +971,7 @@ def main() -> int:
     ap.add_argument("--only-decode", action="store_true", help="skip the batched-decode, prefill and dequant lines")
     # single_expert (one Q4_K expert, one token) runs the headline's gate/up kernel
     # instance: a profile of the headline kernels leaves it out (--workloads)
-    ap.add_argument("--workloads", default="single_expert,batched_decode,prefill,dequant,deltanet",
+    ap.add_argument("--workloads", default="single_expert,fp16_graph_decode,batched_decode,prefill,dequant,deltanet",
                     help="comma-separated workloads run after the headline decode")
     ap.add_argument("--extra-cpu-seconds", type=float, default=4.0)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
@@ -1018,6 +1089,7 @@ def main() -> int:
         wanted = set(args.workloads.split(","))
         runs = {
             "single_expert": lambda: bench_single_expert(dev, 50, cpu_s),
+            "fp16_graph_decode": lambda: bench_fp16_graph_decode(dev, args.layers, 20, cpu_s),
             "batched_decode": lambda: bench_batched_decode(dev, args.layers, 25 * args.layers, cpu_s),
             "prefill": lambda: bench_prefill(dev, 8, 20, cpu_s),
             "dequant": lambda: bench_dequant(dev, 10, cpu_s),

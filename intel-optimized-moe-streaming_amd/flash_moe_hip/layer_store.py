@@ -144,8 +144,9 @@ class ExpertLayer:
     @classmethod
     def synthetic(cls, types: dict, n_experts: int, hidden: int, intermediate: int, *, seed: int,
                   shared_types: dict | None = None, shared_intermediate: int | None = None,
-                  gate_inp: bool = True, device="cuda"):
-        """Random layer generated on the GPU with the benchmark distributions."""
+                  gate_inp: bool = True, scale: float = 0.01, device="cuda"):
+        """Random layer generated on the GPU with the benchmark distributions
+        (super-block scales |N(0,1)| * scale in FP16)."""
         import torch
 
         from .synthetic import torch_random_stack
@@ -153,12 +154,12 @@ class ExpertLayer:
         g = torch.Generator(device=device)
         g.manual_seed(int(seed))
         dev = {r: torch_random_stack(types[r], n_experts, *_shape(r, hidden, intermediate),
-                                     generator=g, device=device) for r in ROLES}
+                                     generator=g, device=device, scale=scale) for r in ROLES}
         sh = None
         if shared_types is not None:
             si = int(shared_intermediate or intermediate)
-            parts = [torch_random_stack(shared_types[r], 1, *_shape(r, hidden, si), generator=g, device=device)
-                     for r in ROLES]
+            parts = [torch_random_stack(shared_types[r], 1, *_shape(r, hidden, si), generator=g, device=device,
+                                        scale=scale) for r in ROLES]
             gi = (torch.randn(hidden, generator=g, device=device) * 0.02).float() if gate_inp else None
             sh = SharedWeights(*parts, types={r: int(shared_types[r]) for r in ROLES}, intermediate=si,
                                gate_inp=gi)

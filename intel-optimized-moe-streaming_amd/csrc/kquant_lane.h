@@ -351,4 +351,181 @@ __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const Lane
     }
 }
 
+
+// ------------------------------------------------------------ FP16 graph
+//
+// The reference's FP16 graph (moe_quant_dot.cpp:154-157, 189-211) multiplies
+// FP16-rounded weights with FP16-rounded activations and accumulates in FP32.
+// A lane's 64 weights are decoded to FP32 with the reference decoders'
+// arithmetic (the formulas of decode8 in kquant_device.h: Q4_K/Q5_K
+// RN(RN(d1 q) - m1), Q6_K RN(ds (q - 32)), Q3_K RN(ds (q - 4)), Q8_0 RN(q d)),
+// rounded to FP16 (RNE) and paired in column order, as the FP16 activations of
+// the same columns are.
+
+// f rounded to FP16 (RNE), as bits.  On the device the operand is made opaque
+// first: the instruction selector would otherwise fold the FP32 arithmetic
+// that produced it into a mixed-precision instruction with one rounding.
+__host__ __device__ inline uint32_t rn16_bits(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __asm__ volatile("" : "+v"(f));
+#endif
+    const _Float16 h = (_Float16)f;
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+__host__ __device__ inline uint32_t pack_rn16(float lo, float hi) { return rn16_bits(lo) | (rn16_bits(hi) << 16); }
+
+// The FP16 activations of one lane's 64 columns, column pairs in run order
+// (pair i = the lane's columns 2i and 2i + 1).
+struct LaneH {
+    uint32_t h[32];
+};
+
+// x16: an activation vector of FP16 bit patterns (the FP16 graph's rounded x).
+template <int T>
+__host__ __device__ inline void lane_xh(const uint16_t* x16, int blk, int k, LaneH& x) {
+    constexpr int NR = LaneGeo<T>::NR, RL = LaneGeo<T>::RL;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int c = 256 * blk + lane_col<T>(k, r);
+#pragma unroll
+        for (int p = 0; p < RL / 8; ++p) {
+            const uint4 a = *(const uint4*)(x16 + c + 8 * p);
+            const int b = (r * RL + 8 * p) / 2;
+            x.h[b] = a.x; x.h[b + 1] = a.y; x.h[b + 2] = a.z; x.h[b + 3] = a.w;
+        }
+    }
+}
+
+namespace detail {
+// separately rounded FP32 products and differences, as the reference decoders
+// compute them (never contracted into one fused multiply-add)
+__host__ __device__ inline float mul_rn(float a, float b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __fmul_rn(a, b);
+#else
+#pragma clang fp contract(off)
+    return a * b;
+#endif
+}
+__host__ __device__ inline float sub_rn(float a, float b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __fsub_rn(a, b);
+#else
+#pragma clang fp contract(off)
+    return a - b;
+#endif
+}
+
+// w[j] = f(byte j of the 4 dwords at q) for 16 bytes, packed as FP16 pairs into out[0..7]
+template <class F>
+__host__ __device__ inline void pack16_bytes(const uint32_t* q, uint32_t* out, F&& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float b0 = (float)(q[i] & 0xFFu), b1 = (float)((q[i] >> 8) & 0xFFu);
+        const float b2 = (float)((q[i] >> 16) & 0xFFu), b3 = (float)(q[i] >> 24);
+        out[2 * i] = pack_rn16(f(b0), f(b1));
+        out[2 * i + 1] = pack_rn16(f(b2), f(b3));
+    }
+}
+}  // namespace detail
+
+// Piece P (0..3, 16 weights) of lane k's 64 weights as FP16 pairs, in run
+// order: out[0..7] are the pairs 8P .. 8P+7 of lane_w16 (raw bytes from
+// lane_load).
+template <int T, int P>
+__host__ __device__ inline void lane_w16_piece(const uint32_t* raw, int k, uint32_t* out) {
+    if constexpr (T == T_Q8_0) {
+        // pieces 0, 1: block 2k (d at bytes 0-1, quants at bytes 2..33); 2, 3: block 2k+1
+        if constexpr (P < 2) {
+            const float d0 = f16_bits_to_f32(raw[0] & 0xFFFFu);
+            uint32_t q[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = rotr_pair(raw[4 * P + i + 1], raw[4 * P + i], 16);
+            detail::pack16_bytes(q, out, [&](float b) { return detail::mul_rn((float)(int8_t)(int)b, d0); });
+        } else {
+            const float d1 = f16_bits_to_f32(raw[8] >> 16);
+            detail::pack16_bytes(raw + 9 + 4 * (P - 2), out,
+                                 [&](float b) { return detail::mul_rn((float)(int8_t)(int)b, d1); });
+        }
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        constexpr int QS = T == T_Q4_K ? 4 : 12, r = P / 2, p = P % 2;
+        const float d = f16_bits_to_f32(raw[0] & 0xFFFFu), dmin = f16_bits_to_f32(raw[0] >> 16);
+        uint32_t sc2, mn2;
+        k4_scale_min_pair(raw, k, sc2, mn2);
+        const float d1 = detail::mul_rn(d, (float)((sc2 >> (8 * r)) & 0xFFu));
+        const float m1 = detail::mul_rn(dmin, (float)((mn2 >> (8 * r)) & 0xFFu));
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[i] = (raw[QS + 4 * p + i] >> (4 * r)) & 0x0F0F0F0Fu;
+            if constexpr (T == T_Q5_K) q[i] |= ((raw[4 + 4 * p + i] >> (2 * k + r)) & 0x01010101u) << 4;
+        }
+        detail::pack16_bytes(q, out, [&](float b) { return detail::sub_rn(detail::mul_rn(d1, b), m1); });
+    } else if constexpr (T == T_Q6_K) {
+        constexpr int r = P / 2, p = P % 2;
+        const float d = f16_bits_to_f32(raw[18] & 0xFFFFu);
+        const int s = (k & 1) + 2 * r, rq = (2 * s - 4) & 31;
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            q[i] = ((raw[4 * p + i] >> (4 * r)) & 0x0F0F0F0Fu) | (rotr(raw[8 + 4 * p + i], rq) & 0x30303030u);
+        const int sb = 2 * s + p;
+        const int sc = (int)(int8_t)(uint8_t)((sb < 4 ? raw[16] >> (8 * sb) : raw[17] >> (8 * (sb - 4))) & 0xFFu);
+        const float ds = detail::mul_rn(d, (float)sc);
+        detail::pack16_bytes(q, out, [&](float b) { return detail::mul_rn(ds, b - 32.0f); });
+    } else {  // Q3_K: piece P is run s = P
+        const float d = f16_bits_to_f32(raw[11] & 0xFFFFu);
+        const int h = k >> 1, odd = k & 1, sh = 8 * odd + 4 * h;
+        const int r = (4 * h + P - 2) & 31;
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = ((raw[4 + i] >> (2 * P)) & 0x03030303u) | (rotr(raw[i], r) & 0x04040404u);
+        const float ds = detail::mul_rn(d, (float)k3_scale_run(raw + 8, sh, P));
+        detail::pack16_bytes(q, out, [&](float b) { return detail::mul_rn(ds, b - 4.0f); });
+    }
+}
+
+// Lane k's 64 weights as FP16 pairs in run order.
+template <int T>
+__host__ __device__ inline void lane_w16(const uint32_t* raw, int k, uint32_t (&w)[32]) {
+    lane_w16_piece<T, 0>(raw, k, w);
+    lane_w16_piece<T, 1>(raw, k, w + 8);
+    lane_w16_piece<T, 2>(raw, k, w + 16);
+    lane_w16_piece<T, 3>(raw, k, w + 24);
+}
+
+namespace detail {
+template <int T, int P>
+__host__ __device__ inline float dot16_piece(const uint32_t* raw, int k, const LaneH& x, float acc) {
+    uint32_t w[8];
+    lane_w16_piece<T, P>(raw, k, w);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#if defined(__HIP_DEVICE_COMPILE__)
+        typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w[i]), __builtin_bit_cast(half2_t, x.h[8 * P + i]),
+                                     acc, false);
+#else
+        acc += f16_bits_to_f32(w[i] & 0xFFFFu) * f16_bits_to_f32(x.h[8 * P + i] & 0xFFFFu) +
+               f16_bits_to_f32(w[i] >> 16) * f16_bits_to_f32(x.h[8 * P + i] >> 16);
+#endif
+    }
+    return acc;
+}
+}  // namespace detail
+
+// FP16-graph dot product of lane k's 64 weights with x: FP16 products summed
+// in FP32, two columns per v_dot2_f32_f16 (the host build sums the exact
+// products in FP32 in the same order), decoded one 16-weight piece at a time.
+template <int T>
+__host__ __device__ inline float lane_dot_f16(const uint32_t* raw, int k, const LaneH& x) {
+    float acc = detail::dot16_piece<T, 0>(raw, k, x, 0.0f);
+    acc = detail::dot16_piece<T, 1>(raw, k, x, acc);
+    acc = detail::dot16_piece<T, 2>(raw, k, x, acc);
+    return detail::dot16_piece<T, 3>(raw, k, x, acc);
+}
+
 }  // namespace mqh

@@ -25,7 +25,9 @@
 // so a row of C columns is C/64 consecutive lanes and an instruction covers
 // 64/(C/64) rows.  Every weight byte is read once per (token, slot).
 //
-// Supported (checked by fast_supported): FP32 graph; types Q3_K/Q4_K/Q5_K/Q6_K/Q8_0
+// Supported (checked by fast_supported): the FP32 graph, and the FP16 graph
+// (fp16_graph = 1: FP16 operands and rounding points for the routed experts);
+// types Q3_K/Q4_K/Q5_K/Q6_K/Q8_0
 // with gate type == up type; hidden and intermediate in {256, 512, 1024, 2048};
 // at most 16 slots (12 at intermediate 2048: kernel B's digit LDS); a shared
 // expert with the routed intermediate size and the routed types or Q6_K.
@@ -191,6 +193,37 @@ __device__ __forceinline__ void act_digits_lds(const ActRegs<I>& r, int lane, in
     }
 }
 
+// The FP16 graph's activations of one slot into LDS as FP16 bits: kernel A
+// rounded them to FP16 already, so the conversion is exact.  Lane l writes its
+// own V = I/64 columns (picked out of its run as in act_digits_lds).
+template <int I>
+__device__ __forceinline__ void act_halves_lds(const ActRegs<I>& r, int lane, uint16_t* dst) {
+    constexpr int V = ActRegs<I>::V;
+    const int c0 = lane * V;
+    if constexpr (V >= RUN) {
+#pragma unroll
+        for (int i = 0; i < V / 8; ++i) {
+            const float4 a = r.q[2 * i], b = r.q[2 * i + 1];
+            *(uint4*)(dst + c0 + 8 * i) = make_uint4(pack_rn16(a.x, a.y), pack_rn16(a.z, a.w), pack_rn16(b.x, b.y),
+                                                     pack_rn16(b.z, b.w));
+        }
+    } else {
+        const int g0 = (c0 & (RUN - 1)) / 4;   // first own four-value group of the run
+        uint32_t w[V / 2];
+#pragma unroll
+        for (int j = 0; j < V / 4; ++j) {
+            float4 v = r.q[0];
+#pragma unroll
+            for (int m = 1; m < RUN / 4; ++m)
+                if (g0 + j == m) v = r.q[m];
+            w[2 * j] = pack_rn16(v.x, v.y);
+            w[2 * j + 1] = pack_rn16(v.z, v.w);
+        }
+        if constexpr (V == 8) *(uint4*)(dst + c0) = make_uint4(w[0], w[1], w[2], w[3]);
+        else *(uint2*)(dst + c0) = make_uint2(w[0], w[1]);
+    }
+}
+
 // LDS bytes of one slot's digits in kernel B: planes [2][I], run scales and sums.
 __host__ __device__ constexpr int act_lds_bytes(int inter) { return 2 * inter + 2 * (inter / RUN) * 4; }
 
@@ -228,12 +261,13 @@ __device__ __forceinline__ void x_digits(float4 v, int8_t* planes, float* xs16, 
 // a workgroup share the token's digits in LDS.  The token's last workgroup
 // also computes the shared expert's sigmoid gate.
 
-template <int H>
+template <int H, bool F16G>
 struct SharedX {
     __attribute__((aligned(16))) int8_t planes[2 * H];
     float xs16[H / RUN];
     float sum16[H / RUN];
     float s_gate[16];
+    __attribute__((aligned(16))) uint16_t x16[F16G ? H : 8];   // the FP16 graph's token (FP16 bits)
 };
 
 // every weight load of one item's lane (type T)
@@ -249,8 +283,8 @@ __device__ __forceinline__ void item_loads(const uint8_t* Gm, const uint8_t* Um,
 // SGT: the shared expert's gate/up type (its waves take that code path).
 // ROUTED: the router's select step first (p.route_scores set, at most
 // ROUTE_PROLOGUE_MAX_EXPERTS experts).
-template <int GT, int SGT, int LPR, bool ROUTED>
-__device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodeParams& p, SharedX<64 * LPR>& sh) {
+template <int GT, int SGT, int LPR, bool ROUTED, bool F16G>
+__device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodeParams& p, SharedX<64 * LPR, F16G>& sh) {
     constexpr int H = 64 * LPR, RPI = 64 / LPR, NX = H / 4;   // NX threads hold the token, four values each
     constexpr int NA = LaneGeo<GT>::NRAW > LaneGeo<SGT>::NRAW ? LaneGeo<GT>::NRAW : LaneGeo<SGT>::NRAW;
     const int t = blockIdx.y;
@@ -334,25 +368,41 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
         else item_loads<GT, H>(Gm, Um, row, blk, k, rg, ru);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // 2. token digits, and this lane's digit operands out of LDS, while the
-    // weight loads are in flight
-    if (threadIdx.x < NX) x_digits<H, NX>(xv, sh.planes, sh.xs16, sh.sum16);
+    // 2. token digits (in the FP16 graph also the token rounded to FP16), and
+    // this lane's operands out of LDS, while the weight loads are in flight
+    if (threadIdx.x < NX) {
+        x_digits<H, NX>(xv, sh.planes, sh.xs16, sh.sum16);
+        if constexpr (F16G)
+            *(uint2*)(sh.x16 + 4 * threadIdx.x) = make_uint2(pack_rn16(xv.x, xv.y), pack_rn16(xv.z, xv.w));
+    }
     __syncthreads();
-    DigitsRef xd;
-    xd.planes = sh.planes; xd.xs16 = sh.xs16; xd.sum16 = sh.sum16; xd.n = H;
-    LaneX X;
-    if constexpr (SGT == GT) {
-        lane_x<GT>(xd, blk, k, X);
+    // the routed experts of the FP16 graph take FP16 operands (moe_quant_dot.cpp:
+    // 189-206); the shared expert always runs the FP32 graph, as the
+    // reference's shared expert does
+    // (each path reads its operands and runs its dot products in one branch, so
+    // only one operand set is live; the weight loads are all issued already,
+    // so the waits inside stay exact)
+    const bool f16w = F16G && !shared;   // wave-uniform
+    float g = 0.0f, u = 0.0f;
+    if (f16w) {
+        if constexpr (F16G) {
+            LaneH XH;
+            lane_xh<GT>(sh.x16, blk, k, XH);
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            // 3. gate and up dot products
+            g = lane_dot_f16<GT>(rg, k, XH);
+            u = lane_dot_f16<GT>(ru, k, XH);
+        }
     } else {
+        DigitsRef xd;
+        xd.planes = sh.planes; xd.xs16 = sh.xs16; xd.sum16 = sh.sum16; xd.n = H;
+        LaneX X;
         if (sw) lane_x<SGT>(xd, blk, k, X);
         else lane_x<GT>(xd, blk, k, X);
-    }
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-
-    // 3. gate and up dot products, SwiGLU: one FP32 activation per row
-    if (live) {
-        float g, u;
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        // 3. gate and up dot products
         if (sw) {
             g = lane_dot<SGT>(rg, k, X);
             u = lane_dot<SGT>(ru, k, X);
@@ -360,9 +410,25 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
             g = lane_dot<GT>(rg, k, X);
             u = lane_dot<GT>(ru, k, X);
         }
+    }
+
+    // SwiGLU: one FP32 activation per row
+    if (live) {
         g = lane_group_sum<LPR>(g);
         u = lane_group_sum<LPR>(u);
-        if (li == 0) h.act[((int64_t)t * h.S + s) * h.a_inter + row] = bad ? 0.0f : silu_mul(g, u);
+        if (li == 0) {
+            float a;
+            if (f16w) {
+                // the FP16 graph's rounding points (moe_quant_dot.cpp:197-206)
+                g = round16(g);
+                u = round16(u);
+                const float sig = round16(1.0f / (1.0f + expf(-g)));
+                a = round16(round16(g * sig) * u);
+            } else {
+                a = silu_mul(g, u);
+            }
+            h.act[((int64_t)t * h.S + s) * h.a_inter + row] = bad ? 0.0f : a;
+        }
         if (bad && lane == 0 && row0 == 0) atomicOr(&p.flags[FLAG_BAD_ID], 1);
     }
 
@@ -388,24 +454,24 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     }
 }
 
-template <int GT, int SGT, int LPR>
+template <int GT, int SGT, int LPR, bool F16G>
 __global__ __launch_bounds__(1024) void k_fast_gate_up(const float* x, const int32_t* ids, float* act, const float* sh_gate_inp, int top_k,
                                                   int S, int has_shared, int n_experts, int a_inter, int a_waves,
                                                   DecodeParams p) {
-    __shared__ SharedX<64 * LPR> sh;
+    __shared__ SharedX<64 * LPR, F16G> sh;
     const DecodeHot h{x, ids, act, nullptr, sh_gate_inp, top_k, S, has_shared, n_experts, a_inter, a_waves};
-    gate_up_items<GT, SGT, LPR, false>(h, p, sh);
+    gate_up_items<GT, SGT, LPR, false, F16G>(h, p, sh);
 }
 
 // Kernel A with the router's select step in its prologue: the same work as
 // k_fast_gate_up once each wave knows its expert.
-template <int GT, int SGT, int LPR>
+template <int GT, int SGT, int LPR, bool F16G>
 __global__ __launch_bounds__(1024) void k_fast_gate_up_routed(const float* x, const int32_t* ids, float* act, const float* sh_gate_inp, int top_k,
                                                   int S, int has_shared, int n_experts, int a_inter, int a_waves,
                                                   DecodeParams p) {
-    __shared__ SharedX<64 * LPR> sh;
+    __shared__ SharedX<64 * LPR, F16G> sh;
     const DecodeHot h{x, ids, act, nullptr, sh_gate_inp, top_k, S, has_shared, n_experts, a_inter, a_waves};
-    gate_up_items<GT, SGT, LPR, true>(h, p, sh);
+    gate_up_items<GT, SGT, LPR, true, F16G>(h, p, sh);
 }
 
 // ---------------------------------------------------------------- kernel B
@@ -430,7 +496,7 @@ struct SharedB {
 // s = slot s; waves at or past S only join the barriers), combined in top-k
 // order.  down_slot is the calling wave's part (its slot's rows into LDS, with
 // the slot's weight type DT), down_combine the workgroup's.
-template <int DT, int LPR, int NPB_ = 1>
+template <int DT, int LPR, int NPB_, bool F16G>
 __device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams& p, int bx, int t,
                                           SharedB<GeoB<LPR, NPB_>::RB>& sh) {
     constexpr int N = LaneGeo<DT>::NRAW;
@@ -467,27 +533,43 @@ __device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams
 #pragma unroll
     for (int q = 0; q < NPB; ++q) lane_load<DT>(D + (int64_t)(r0 + q * RPI + rr) * ROW_BYTES + blk * BB, k, raw[q]);
     __builtin_amdgcn_sched_barrier(0);
-    // the slot's digits into this wave's LDS region, and this lane's digit
-    // operands back out of it, while the weights are in flight
+    // the slot's digits (the FP16 graph's routed slots: its FP16 activations)
+    // into this wave's LDS region, and this lane's operands back out of it,
+    // while the weights are in flight
     extern __shared__ __attribute__((aligned(16))) uint8_t b_digits[];
     int8_t* planes = (int8_t*)(b_digits + s * act_lds_bytes(I));
     float* xs16 = (float*)(planes + 2 * I);
     float* sum16 = xs16 + I / RUN;
-    act_digits_lds<I>(A, lane, planes, xs16, sum16);
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    DigitsRef xd;
-    xd.planes = planes; xd.xs16 = xs16; xd.sum16 = sum16; xd.n = I;
-    LaneX X;
-    lane_x<DT>(xd, blk, k, X);
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-
+    // (each path in one branch, so only one operand set is live)
+    const bool f16w = F16G && !shared;   // wave-uniform
+    float v[NPB];
+    if (f16w) {
+        if constexpr (F16G) {
+            act_halves_lds<I>(A, lane, (uint16_t*)planes);
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            LaneH XH;
+            lane_xh<DT>((const uint16_t*)planes, blk, k, XH);
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < NPB; ++q) {
-        float v = lane_dot<DT>(raw[q], k, X);
-        v = lane_group_sum<LPR>(v);
-        if (li == 0) sh.s_y[s][q * RPI + rr] = bad ? 0.0f : v;
+            for (int q = 0; q < NPB; ++q)   // the expert's output in the FP16 graph (moe_quant_dot.cpp:208-209)
+                v[q] = round16(lane_group_sum<LPR>(lane_dot_f16<DT>(raw[q], k, XH)));
+        }
+    } else {
+        act_digits_lds<I>(A, lane, planes, xs16, sum16);
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        DigitsRef xd;
+        xd.planes = planes; xd.xs16 = xs16; xd.sum16 = sum16; xd.n = I;
+        LaneX X;
+        lane_x<DT>(xd, blk, k, X);
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < NPB; ++q) v[q] = lane_group_sum<LPR>(lane_dot<DT>(raw[q], k, X));
     }
+#pragma unroll
+    for (int q = 0; q < NPB; ++q)
+        if (li == 0) sh.s_y[s][q * RPI + rr] = bad ? 0.0f : v[q];
     if (lane == 0) sh.s_w[s] = shared ? p.sh_scale[t] : w;
 }
 
@@ -508,17 +590,17 @@ __device__ __forceinline__ void down_combine(const DecodeHot& h, const DecodePar
 }
 
 // SDT: the shared expert's down type (its wave takes that code path).
-template <int DT, int SDT, int LPR, int NPB>
+template <int DT, int SDT, int LPR, int NPB, bool F16G>
 __global__ __launch_bounds__(1024) void k_fast_down(const int32_t* ids, float* act, const float* weights, int top_k,
                                                    int S, int has_shared, int n_experts, DecodeParams p) {
     __shared__ SharedB<GeoB<LPR, NPB>::RB> sh;
     const DecodeHot h{nullptr, ids, act, weights, nullptr, top_k, S, has_shared, n_experts, 0, 0};
     if constexpr (SDT != DT) {
         const int s = uniform(threadIdx.x >> 6);
-        if (has_shared && s == top_k) down_slot<SDT, LPR, NPB>(h, p, blockIdx.x, blockIdx.y, sh);
-        else down_slot<DT, LPR, NPB>(h, p, blockIdx.x, blockIdx.y, sh);
+        if (has_shared && s == top_k) down_slot<SDT, LPR, NPB, F16G>(h, p, blockIdx.x, blockIdx.y, sh);
+        else down_slot<DT, LPR, NPB, F16G>(h, p, blockIdx.x, blockIdx.y, sh);
     } else {
-        down_slot<DT, LPR, NPB>(h, p, blockIdx.x, blockIdx.y, sh);
+        down_slot<DT, LPR, NPB, F16G>(h, p, blockIdx.x, blockIdx.y, sh);
     }
     down_combine<LPR, NPB>(h, p, blockIdx.x, blockIdx.y, sh);
 }
@@ -531,7 +613,6 @@ static bool fast_type(int t) {
 static bool fast_dim(int n) { return n == 256 || n == 512 || n == 1024 || n == 2048; }
 
 bool fast_supported(const DecodeParams& p) {
-    if (p.fp16) return false;
     if (!fast_dim(p.hidden) || p.S > FAST_MAX_SLOTS || p.S < 1) return false;
     int gt = -1, dt = -1, I = -1;
     if (p.top_k > 0) {
@@ -587,90 +668,95 @@ static int gate_up_waves(int items, int tokens, int hidden, int cus) {
     return best;
 }
 
-template <int GT, int SGT, int LPR>
+template <int GT, int SGT, int LPR, bool F16G>
 static void launch_a(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     const int items = p.S * (p.inter / (64 / LPR));
     const int w = gate_up_waves(items, p.n_tokens, 64 * LPR, device_cus());
     const dim3 grid((items + w - 1) / w, p.n_tokens), block(64 * w);
     if (p.route_scores != nullptr) {
         if (ev.armed_a())
-            hipExtLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, block, 0, stream, ev.a_start,
+            hipExtLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR, F16G>), grid, block, 0, stream, ev.a_start,
                                   ev.a_stop, 0, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
         else
-            hipLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
+            hipLaunchKernelGGL((k_fast_gate_up_routed<GT, SGT, LPR, F16G>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
         return;
     }
     if (ev.armed_a())
-        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
+        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
     else
-        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
+        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
 }
 
-template <int GT, int SGT>
+template <int GT, int SGT, bool F16G>
 static void launch_a_h(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     switch (p.hidden) {
-        case 256: launch_a<GT, SGT, 4>(p, stream, ev); break;
-        case 512: launch_a<GT, SGT, 8>(p, stream, ev); break;
-        case 1024: launch_a<GT, SGT, 16>(p, stream, ev); break;
-        default: launch_a<GT, SGT, 32>(p, stream, ev); break;
+        case 256: launch_a<GT, SGT, 4, F16G>(p, stream, ev); break;
+        case 512: launch_a<GT, SGT, 8, F16G>(p, stream, ev); break;
+        case 1024: launch_a<GT, SGT, 16, F16G>(p, stream, ev); break;
+        default: launch_a<GT, SGT, 32, F16G>(p, stream, ev); break;
     }
 }
 
 // a shared expert of another type is Q6_K (fast_supported admits no other)
-template <int GT>
+template <int GT, bool F16G>
 static void launch_a_t(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
-    if (p.has_shared && p.top_k > 0 && p.sh_gate_type != GT) launch_a_h<GT, T_Q6_K>(p, stream, ev);
-    else launch_a_h<GT, GT>(p, stream, ev);
+    if (p.has_shared && p.top_k > 0 && p.sh_gate_type != GT) launch_a_h<GT, T_Q6_K, F16G>(p, stream, ev);
+    else launch_a_h<GT, GT, F16G>(p, stream, ev);
 }
 
 #ifndef FAST_DOWN_WG_TARGET
 #define FAST_DOWN_WG_TARGET 1024   // kernel B workgroups above which rows per workgroup grow
 #endif
 
-template <int DT, int SDT, int LPR, int NPB>
+template <int DT, int SDT, int LPR, int NPB, bool F16G>
 static void launch_b_n(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     dim3 grid(p.hidden / GeoB<LPR, NPB>::RB, p.n_tokens);
     const size_t lds = (size_t)p.S * act_lds_bytes(64 * LPR);   // the slots' digits
     if (ev.armed_b())
-        hipExtLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), lds, stream, ev.b_start,
+        hipExtLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB, F16G>), grid, dim3(64 * p.S), lds, stream, ev.b_start,
                               ev.b_stop, 0, p.ids, p.act, p.weights, p.top_k, p.S, p.has_shared, p.n_experts, p);
     else
-        hipLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB>), grid, dim3(64 * p.S), lds, stream, p.ids, p.act, p.weights, p.top_k, p.S, p.has_shared, p.n_experts, p);
+        hipLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB, F16G>), grid, dim3(64 * p.S), lds, stream, p.ids, p.act, p.weights, p.top_k, p.S, p.has_shared, p.n_experts, p);
 }
 
 // Row groups per wave: one while the grid is small (a single token: every
 // workgroup on its own CU), more when many tokens would otherwise make many
 // short workgroups.
-template <int DT, int SDT, int LPR>
+template <int DT, int SDT, int LPR, bool F16G>
 static void launch_b_s(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     const int64_t wg1 = (int64_t)(p.hidden / GeoB<LPR, 1>::RB) * p.n_tokens;
     constexpr bool wide = LaneGeo<DT>::NRAW > 12 || LaneGeo<SDT>::NRAW > 12;   // four row groups would spill
-    if (!wide && wg1 >= 4 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 4>::RB >= 1)
-        launch_b_n<DT, SDT, LPR, wide ? 2 : 4>(p, stream, ev);
-    else if (wg1 >= 2 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 2>::RB >= 1)
-        launch_b_n<DT, SDT, LPR, 2>(p, stream, ev);
-    else
-        launch_b_n<DT, SDT, LPR, 1>(p, stream, ev);
-}
-
-// a shared expert of another type is Q6_K (fast_supported admits no other)
-template <int DT, int LPR>
-static void launch_b(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
-    if (p.has_shared && p.top_k > 0 && p.sh_down_type != DT) launch_b_s<DT, T_Q6_K, LPR>(p, stream, ev);
-    else launch_b_s<DT, DT, LPR>(p, stream, ev);
-}
-
-template <int DT>
-static void launch_b_t(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
-    switch (p.inter) {
-        case 256: launch_b<DT, 4>(p, stream, ev); break;
-        case 512: launch_b<DT, 8>(p, stream, ev); break;
-        case 1024: launch_b<DT, 16>(p, stream, ev); break;
-        default: launch_b<DT, 32>(p, stream, ev); break;
+    if constexpr (F16G) {   // the FP16 graph's decode holds one row group per wave (more would spill)
+        launch_b_n<DT, SDT, LPR, 1, F16G>(p, stream, ev);
+    } else {
+        if (!wide && wg1 >= 4 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 4>::RB >= 1)
+            launch_b_n<DT, SDT, LPR, wide ? 2 : 4, F16G>(p, stream, ev);
+        else if (wg1 >= 2 * FAST_DOWN_WG_TARGET && p.hidden / GeoB<LPR, 2>::RB >= 1)
+            launch_b_n<DT, SDT, LPR, 2, F16G>(p, stream, ev);
+        else
+            launch_b_n<DT, SDT, LPR, 1, F16G>(p, stream, ev);
     }
 }
 
-hipError_t launch_decode_fast(const DecodeParams& p0, hipStream_t stream, const KernelEvents& ev) {
+// a shared expert of another type is Q6_K (fast_supported admits no other)
+template <int DT, int LPR, bool F16G>
+static void launch_b(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
+    if (p.has_shared && p.top_k > 0 && p.sh_down_type != DT) launch_b_s<DT, T_Q6_K, LPR, F16G>(p, stream, ev);
+    else launch_b_s<DT, DT, LPR, F16G>(p, stream, ev);
+}
+
+template <int DT, bool F16G>
+static void launch_b_t(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
+    switch (p.inter) {
+        case 256: launch_b<DT, 4, F16G>(p, stream, ev); break;
+        case 512: launch_b<DT, 8, F16G>(p, stream, ev); break;
+        case 1024: launch_b<DT, 16, F16G>(p, stream, ev); break;
+        default: launch_b<DT, 32, F16G>(p, stream, ev); break;
+    }
+}
+
+template <bool F16G>
+static hipError_t launch_fast(const DecodeParams& p0, hipStream_t stream, const KernelEvents& ev) {
     DecodeParams p = p0;
     if (p.top_k == 0) {   // shared expert only: present it as the routed types
         p.gate_type = p.sh_gate_type; p.up_type = p.sh_up_type; p.down_type = p.sh_down_type;
@@ -678,22 +764,27 @@ hipError_t launch_decode_fast(const DecodeParams& p0, hipStream_t stream, const 
     }
     p.a_inter = p.inter;
     switch (p.gate_type) {
-        case T_Q4_K: launch_a_t<T_Q4_K>(p, stream, ev); break;
-        case T_Q5_K: launch_a_t<T_Q5_K>(p, stream, ev); break;
-        case T_Q6_K: launch_a_t<T_Q6_K>(p, stream, ev); break;
-        case T_Q8_0: launch_a_t<T_Q8_0>(p, stream, ev); break;
-        default: launch_a_t<T_Q3_K>(p, stream, ev); break;
+        case T_Q4_K: launch_a_t<T_Q4_K, F16G>(p, stream, ev); break;
+        case T_Q5_K: launch_a_t<T_Q5_K, F16G>(p, stream, ev); break;
+        case T_Q6_K: launch_a_t<T_Q6_K, F16G>(p, stream, ev); break;
+        case T_Q8_0: launch_a_t<T_Q8_0, F16G>(p, stream, ev); break;
+        default: launch_a_t<T_Q3_K, F16G>(p, stream, ev); break;
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     switch (p.down_type) {
-        case T_Q4_K: launch_b_t<T_Q4_K>(p, stream, ev); break;
-        case T_Q5_K: launch_b_t<T_Q5_K>(p, stream, ev); break;
-        case T_Q6_K: launch_b_t<T_Q6_K>(p, stream, ev); break;
-        case T_Q8_0: launch_b_t<T_Q8_0>(p, stream, ev); break;
-        default: launch_b_t<T_Q3_K>(p, stream, ev); break;
+        case T_Q4_K: launch_b_t<T_Q4_K, F16G>(p, stream, ev); break;
+        case T_Q5_K: launch_b_t<T_Q5_K, F16G>(p, stream, ev); break;
+        case T_Q6_K: launch_b_t<T_Q6_K, F16G>(p, stream, ev); break;
+        case T_Q8_0: launch_b_t<T_Q8_0, F16G>(p, stream, ev); break;
+        default: launch_b_t<T_Q3_K, F16G>(p, stream, ev); break;
     }
     return hipGetLastError();
+}
+
+
+hipError_t launch_decode_fast(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
+    return p.fp16 ? launch_fast<true>(p, stream, ev) : launch_fast<false>(p, stream, ev);
 }
 
 }  // namespace mqh

@@ -94,3 +94,31 @@ extern "C" void mqh_cpu_lane_cover(int type, int* count) {
         default: cover<T_Q4_K>(count); break;
     }
 }
+
+// The FP16-graph operands of one 256-column unit: for every lane k and every
+// weight of its 64, the FP16 bits lane_w16 produces and the column it belongs
+// to (lane_col order), 256 of each.
+template <int T>
+static void w16_unit(const uint8_t* unit, uint16_t* bits, int* cols) {
+    for (int k = 0; k < LANES_PER_BLOCK; ++k) {
+        uint32_t raw[LaneGeo<T>::NRAW];
+        uint32_t w[32];
+        lane_load<T>(unit, k, raw);
+        lane_w16<T>(raw, k, w);
+        for (int i = 0; i < 64; ++i) {
+            const int r = i / LaneGeo<T>::RL;
+            bits[64 * k + i] = (uint16_t)(w[i / 2] >> (16 * (i & 1)));
+            cols[64 * k + i] = lane_col<T>(k, r) + i % LaneGeo<T>::RL;
+        }
+    }
+}
+
+extern "C" void mqh_cpu_lane_w16(int type, const uint8_t* unit, uint16_t* bits, int* cols) {
+    switch (type) {
+        case T_Q4_K: w16_unit<T_Q4_K>(unit, bits, cols); break;
+        case T_Q5_K: w16_unit<T_Q5_K>(unit, bits, cols); break;
+        case T_Q6_K: w16_unit<T_Q6_K>(unit, bits, cols); break;
+        case T_Q8_0: w16_unit<T_Q8_0>(unit, bits, cols); break;
+        default: w16_unit<T_Q3_K>(unit, bits, cols); break;
+    }
+}

@@ -36,6 +36,7 @@ def chk():
     L.mqh_cpu_row_dot.restype = C.c_float
     L.mqh_cpu_digit_roundtrip.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
     L.mqh_cpu_lane_cover.argtypes = [C.c_int, C.c_void_p]
+    L.mqh_cpu_lane_w16.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
     return L
 
 
@@ -89,3 +90,27 @@ def test_lanes_cover_each_column_once(chk, t):
     count = np.zeros(256, np.int32)
     chk.mqh_cpu_lane_cover(t, count.ctypes.data)
     assert np.all(count == 1)
+
+
+@pytest.mark.parametrize("t", [8, 11, 12, 13, 14])
+def test_fp16_graph_lane_weights_bit_exact(chk, oracle_mod, t):
+    """The FP16 graph's weight operands (lane_w16): for every lane of a 256-column
+    unit, each weight is the oracle's dequantized value rounded to FP16 (the
+    reference's round_weights, moe_quant_dot.cpp:154-157), bit for bit, and the
+    lanes cover each column once -- on random units and on units whose scales
+    make products land on FP16 rounding ties and subnormals."""
+    from flash_moe_hip.synthetic import random_tensor
+    from flash_moe_hip.quant_types import block_info
+
+    rng = np.random.default_rng(300 + t)
+    bs, pb = block_info(t)
+    unit_bytes = 8 * pb if t == 8 else pb
+    units = [random_tensor(rng, t, 1, 256, scale=s) for s in (0.01, 1.0, 1e-5, 37.0) for _ in range(8)]
+    for unit in units:
+        unit = np.ascontiguousarray(unit[:unit_bytes])
+        bits = np.zeros(256, np.uint16)
+        cols = np.zeros(256, np.int32)
+        chk.mqh_cpu_lane_w16(t, unit.ctypes.data, bits.ctypes.data, cols.ctypes.data)
+        assert sorted(cols.tolist()) == list(range(256))
+        want = oracle_mod.f32_to_f16_bits(oracle_mod.dequant(t, unit, 256))
+        np.testing.assert_array_equal(bits, np.asarray(want, np.uint16)[cols])

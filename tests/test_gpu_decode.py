@@ -416,3 +416,38 @@ def test_edge_inputs(hip, oracle_mod):
     print("non-finite token", flush=True)
     _, st = run(layer, X3, ids[:, :8], ws[:, :8] / ws[:, :8].sum(1, keepdims=True))
     assert st == -4
+
+
+@pytest.mark.parametrize("types", [(12, 14), (11, 11), (13, 12), (14, 14), (8, 8), (12, 8), (11, 14)])
+def test_fp16_graph_fast_kernels(hip, oracle_mod, types):
+    """The FP16 graph (fp16_graph=1, the reference's production decode) in the
+    integer-decode kernels' FP16 mode: every routed weight decoded with the
+    reference's arithmetic and rounded to FP16, FP16 activations, FP32 sums, and
+    the rounding points of moe_quant_dot.cpp:189-211; the shared expert in the
+    FP32 graph.  Against the oracle's FP16 graph (the reference's own check
+    allows 0.005, test_optimized_inference.py:231-290) and against the generic
+    kernels' FP16 graph, 3 tokens at several shapes, scales as the reference's
+    FP16-graph check (d ~ 0.002, x ~ 0.05)."""
+    gu, dn = types
+    t = {"gate": gu, "up": gu, "down": dn}
+    for H, I in ((256, 256), (2048, 512), (512, 1024), (1024, 2048)):
+        layer, host, shared = make_layer(41 + gu + dn, 6, H, I, t, shared_types=t, scale=0.002)
+        rng = np.random.default_rng(H + 5 * I)
+        X = (rng.standard_normal((3, H)) * 0.05).astype(np.float32)
+        ids = np.array([[0, 5, 2], [3, 3, 1], [4, 0, 5]])
+        ws = np.array([[0.5, 0.3, 0.2], [0.6, 0.2, 0.2], [0.4, 0.4, 0.2]])
+        want = [oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist(), fp16=1)
+                for tok in range(3)]
+        got = {}
+        for path in (0, 1):
+            print(f"fp16 graph types={types} H={H} I={I} path={path}", flush=True)
+            old = hip.mqh_set_decode_path(path)
+            try:
+                got[path], st = run(layer, X, ids, ws, fp16=1)
+            finally:
+                hip.mqh_set_decode_path(old)
+            assert st == 0
+            for tok in range(3):
+                err = oracle_mod.max_relative_error(got[path][tok], want[tok])
+                assert err <= 5e-3, (types, H, I, path, tok, err)
+        assert oracle_mod.max_relative_error(got[0], got[1]) <= 5e-3

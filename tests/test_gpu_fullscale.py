@@ -107,6 +107,46 @@ def test_decode_layer_full_scale(decode_layer, oracle_mod, hip):
         assert oracle_mod.max_relative_error(got[t], want[t]) <= DIGIT_TOL, t
 
 
+def test_fp16_graph_decode_full_scale(oracle_mod, hip):
+    """The decode layer in the FP16 graph (the reference's production mode) at
+    the benchmark shape: 256 experts, top-8 + shared, Q4_K/Q6_K, 8 tokens each as
+    its own call, scales of the reference's FP16-graph check (d ~ 0.002, x ~
+    0.05), against the oracle's FP16 graph (routed) and FP32 shared expert."""
+    import torch
+
+    from flash_moe_hip.layer_store import ExpertLayer
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    types = {"gate": 12, "up": 12, "down": 14}
+    layer = ExpertLayer.synthetic(types, E, H, I, seed=1002, shared_types=types, shared_intermediate=I,
+                                  gate_inp=True, scale=0.002, device="cuda")
+    host, shared, gi = _host_layer(layer)
+    rng = np.random.default_rng(2)
+    X = (rng.standard_normal((8, H)) * 0.05).astype(np.float32)
+    ids, ws = _topk(rng, 8)
+    runner = MoeRunner()
+
+    def expert(e):
+        return {r: host[r][e * layer.expert_bytes(r):(e + 1) * layer.expert_bytes(r)] for r in host}
+
+    worst = 0.0
+    for t in range(8):
+        print(f"full-scale FP16-graph decode token {t}", flush=True)
+        got, rc = runner.fetch(runner.decode(layer, torch.from_numpy(X[t:t + 1]).cuda(),
+                                             torch.from_numpy(ids[t:t + 1]).cuda(),
+                                             torch.from_numpy(ws[t:t + 1]).cuda(), fp16_graph=1))
+        assert rc == 0
+        outs = [oracle_mod.expert_forward(expert(int(e)), types, X[t], H, I, 1) for e in ids[t]]
+        gate = oracle_mod._sigmoid(np.float32(X[t] @ gi).reshape(()))
+        sh = (gate * oracle_mod.expert_forward(shared, types, X[t], H, I, 0)).astype(np.float32)
+        want = oracle_mod.combine(outs, [float(v) for v in ws[t]], sh)
+        worst = max(worst, oracle_mod.max_relative_error(got[0], want))
+    print(f"  FP16-graph decode max rel err over 8 tokens: {worst:.3e}", flush=True)
+    assert worst <= 5e-3
+    del layer
+    torch.cuda.empty_cache()
+
+
 def test_batched_decode_full_scale(oracle_mod, hip):
     import torch
 

@@ -708,7 +708,7 @@ def bench_dequant(dev, reps: int, cpu_seconds: float) -> dict:
                     "types Q3_K (11), Q4_K (12), Q6_K (14), Q8_0 (8)",
         "metric": "GB/s (quantized bytes read + FP16 bytes written)", "per_type": res,
         "value": res[worst]["gbs"], "unit": "GB/s",
-        "roofline": _hbm_roofline("mqh::k_dequant<%s, true>" % worst, res[worst]["bytes"], res[worst]["us"]),
+        "roofline": _hbm_roofline("mqh::k_dequant_lds<%s, true>" % worst, res[worst]["bytes"], res[worst]["us"]),
     }
     if cpu_seconds > 0:
         t = 12

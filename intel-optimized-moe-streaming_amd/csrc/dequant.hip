@@ -61,8 +61,97 @@ __global__ __launch_bounds__(DQ_THREADS) void k_dequant(const uint8_t* __restric
     }
 }
 
+// LDS-staged form.  A workgroup owns one chunk of DQ_CHUNK_VALUES consecutive
+// values (16 K-quant blocks, or 128 blocks of the 32-value types), staged in
+// LDS one block per slot (slot_bytes/slot_offset: the 16-byte fields land on
+// 16-byte boundaries).  Every thread then decodes two adjacent 8-value groups
+// of one block -- the two share the block header and, for the K-quants, the
+// sub-block scale -- and stores 16 consecutive values.
+constexpr int DQ_CHUNK_VALUES = DQ_THREADS * 16;
+
+// Copy one chunk into its LDS slots with aligned, coalesced 16-byte loads.
+// Where slot and block coincide (Q4_K, Q5_K: 144 and 176 bytes) the words go
+// to LDS as they are; otherwise each 16-byte word (which spans at most two
+// blocks: every block is longer than 16 bytes) is written as 2-byte pieces,
+// each at its block's slot -- naturally aligned LDS writes, where 16-byte
+// writes at 2 mod 4 addresses would stall.
+template <int T>
+__device__ __forceinline__ void stage_chunk(const uint8_t* __restrict__ src, uint8_t* lds) {
+    constexpr int PB = block_bytes(T), SL = slot_bytes(T), OFF = slot_offset(T);
+    constexpr int NB = DQ_CHUNK_VALUES / block_size(T);
+    static_assert(PB > 16, "a 16-byte word meets at most two blocks");
+#pragma unroll
+    for (int i = threadIdx.x; i < NB * PB / 16; i += DQ_THREADS) {
+        const uint4 w = ((const uint4*)src)[i];
+        if constexpr (SL == PB && OFF == 0) {
+            ((uint4*)lds)[i] = w;
+        } else {
+            // pieces m < mb belong to block b0, the rest to block b0 + 1
+            const int x = 16 * i, b0 = x / PB, mb = ((b0 + 1) * PB - x) / 2;
+            uint16_t* at0 = (uint16_t*)(lds + x + b0 * (SL - PB) + OFF);
+            uint16_t* at1 = at0 + (SL - PB) / 2;
+            const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int m = 0; m < 8; ++m) (m < mb ? at0 : at1)[m] = (uint16_t)(q[m >> 1] >> (16 * (m & 1)));
+        }
+    }
+}
+
+template <bool F16>
+__device__ __forceinline__ void store16(const float v[16], int64_t gi, void* dst) {
+    if constexpr (F16) {
+        uint4 o[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            o[h].x = pack_f2h_rn(v[8 * h + 0], v[8 * h + 1]);
+            o[h].y = pack_f2h_rn(v[8 * h + 2], v[8 * h + 3]);
+            o[h].z = pack_f2h_rn(v[8 * h + 4], v[8 * h + 5]);
+            o[h].w = pack_f2h_rn(v[8 * h + 6], v[8 * h + 7]);
+        }
+        ((uint4*)dst)[gi] = o[0];
+        ((uint4*)dst)[gi + 1] = o[1];
+    } else {
+        float4* o = (float4*)dst + 2 * gi;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    }
+}
+
+template <int T, bool F16>
+__global__ __launch_bounds__(DQ_THREADS) void k_dequant_lds(const uint8_t* __restrict__ src, void* __restrict__ dst) {
+    constexpr int PB = block_bytes(T), G = block_size(T) / 8, SL = slot_bytes(T);
+    constexpr int NB = DQ_CHUNK_VALUES / block_size(T);
+    static_assert(SL % 16 == 0 && G % 2 == 0 && PB % 2 == 0, "16-byte slots, group pairs in one block");
+    __shared__ __attribute__((aligned(16))) uint8_t buf[NB * SL];
+    const int64_t chunk = blockIdx.x;
+    stage_chunk<T>(src + chunk * (NB * PB), buf);
+    __syncthreads();
+    const int b = 2 * threadIdx.x / G, t = 2 * threadIdx.x - b * G;
+    float v[16];
+    decode16<T>(buf + b * SL + slot_offset(T), t, v);
+    store16<F16>(v, chunk * (DQ_CHUNK_VALUES / 8) + 2 * threadIdx.x, dst);
+}
+
 template <int T>
 static hipError_t launch_t(const uint8_t* src, void* dst, int64_t n, int want_f16, hipStream_t stream) {
+    // whole chunks from a 16-byte aligned source go through LDS; the rest (a
+    // tail of fewer than DQ_CHUNK_VALUES values, or an unaligned source)
+    // through the per-thread kernel
+    const int64_t n_chunks = ((uintptr_t)src & 15) ? 0 : n / DQ_CHUNK_VALUES;
+    if (n_chunks > 0) {
+        if (want_f16)
+            hipLaunchKernelGGL((k_dequant_lds<T, true>), dim3((unsigned)n_chunks), dim3(DQ_THREADS), 0, stream, src, dst);
+        else
+            hipLaunchKernelGGL((k_dequant_lds<T, false>), dim3((unsigned)n_chunks), dim3(DQ_THREADS), 0, stream, src,
+                               dst);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t done = n_chunks * DQ_CHUNK_VALUES;
+        if (done == n) return hipSuccess;
+        src += done / block_size(T) * block_bytes(T);
+        dst = (uint8_t*)dst + done * (want_f16 ? 2 : 4);
+        n -= done;
+    }
     const int64_t n_groups = n / 8;
     const int threads = DQ_THREADS;
     int64_t blocks = (n_groups + threads - 1) / threads;

@@ -83,6 +83,15 @@ __device__ __forceinline__ uint32_t f2h_rn(float f) {
     return (uint32_t)__half_as_ushort(__float2half_rn(opaque(f)));
 }
 
+// two values rounded to FP16 (RNE), packed low then high: one v_cvt_pk_f16_f32
+__device__ __forceinline__ uint32_t pack_f2h_rn(float lo, float hi) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = {opaque(lo), opaque(hi)};
+    const f16x2 h = __builtin_convertvector(v, f16x2);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
 __device__ __forceinline__ float round16(float f) { return __half2float(__float2half_rn(opaque(f))); }
 
 // byte k of a 64-bit word
@@ -231,7 +240,8 @@ __device__ __forceinline__ void decode8<T_Q3_K>(const uint8_t* blk, int t, float
     // byte 92 at the latest, inside the block) and bytes 108..109 on their own,
     // then shift down by 0 or 16 bits.
     const uintptr_t a = (uintptr_t)(blk + 94);
-    const uint4 w = *(const uint4*)(a & ~(uintptr_t)3);
+    // (pointer arithmetic, not an integer cast, so an LDS source stays an LDS read)
+    const uint4 w = *(const uint4*)(blk + 94 - (a & 3));
     const uint32_t d16 = ld_u16(blk + 108);
     const bool mis = (a & 3) != 0;
     uint4 v;
@@ -257,6 +267,122 @@ __device__ __forceinline__ void decode8<T_Q3_K>(const uint8_t* blk, int t, float
     const uint32_t u1 =
         (((uint32_t)(lo >> 32) >> (2 * s)) & 0x03030303u) | ((((uint32_t)(hm >> 32) >> hb) & 0x01010101u) << 2);
     per_byte8(u0, u1, out, [&](float u) { return __fmul_rn(ds, u - 4.0f); });
+}
+
+// ---------------------------------------------------- 16 consecutive values
+//
+// decode16<T>(blk, t, out): values 8t .. 8t+15 of the block at blk (t even),
+// bit-identical to decode8<T>(blk, t, out) then decode8<T>(blk, t + 1, out + 8).
+// The two groups share one sub-block, so the header and scale work is done
+// once.  blk is an LDS block in its slot (slot_bytes/slot_offset below): every
+// 16-byte read is 16-byte aligned, which LDS serves without the stall of an
+// unaligned wide read, and the slot's padding after the block is readable.
+//
+// The signed-quant types (Q3_K, Q6_K, Q8_0) put each quant q, times a power of
+// two 2^e, in the top bits of a byte, as an int8: one sign-extending byte
+// conversion (v_cvt_f32_i32 with an SDWA byte operand) yields 2^e q as a float
+// and the scale s is divided by 2^e once.  Both steps are exact -- these scales
+// are an FP16 value times a small integer, so when not zero they are at least
+// 2^-24 in magnitude, far from FP32's subnormal range -- hence
+// RN((s / 2^e) (2^e q)) = RN(s q) bit for bit, signed zeros, infinities and
+// NaNs included.
+
+// LDS slot of one block: slot_bytes(T), a multiple of 16, with the block at
+// byte slot_offset(T), placed so that the 16-byte fields decode16 reads (the
+// quants, the Q3_K scales) start on 16-byte boundaries.
+__host__ __device__ constexpr int slot_bytes(int t) {
+    return t == T_Q8_0 ? 48 : t == T_IQ4_NL ? 32 : t == T_Q3_K ? 112 : t == T_Q6_K ? 224 : block_bytes(t);
+}
+__host__ __device__ constexpr int slot_offset(int t) { return (t == T_Q8_0 || t == T_IQ4_NL) ? 14 : 0; }
+
+// w rotated right by n (mod 32) bits: one v_alignbit_b32
+__device__ __forceinline__ uint32_t rotr32(uint32_t w, uint32_t n) { return __builtin_amdgcn_alignbit(w, w, n); }
+
+// byte k (a compile-time 0..3) of w as a signed integer, as a float
+template <int k>
+__device__ __forceinline__ float sbyte_f(uint32_t w) { return (float)(int32_t)(int8_t)(w >> (8 * k)); }
+
+// out[4 i + k] = RN(s * (int8) byte k of w[i]) for the 16 bytes of w
+__device__ __forceinline__ void scale_sbytes16(const uint32_t w[4], float s, float out[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        out[4 * i + 0] = __fmul_rn(s, sbyte_f<0>(w[i]));
+        out[4 * i + 1] = __fmul_rn(s, sbyte_f<1>(w[i]));
+        out[4 * i + 2] = __fmul_rn(s, sbyte_f<2>(w[i]));
+        out[4 * i + 3] = __fmul_rn(s, sbyte_f<3>(w[i]));
+    }
+}
+
+template <int T>
+__device__ __forceinline__ void decode16(const uint8_t* blk, int t, float out[16]) {
+    if constexpr (T == T_Q8_0) {
+        const float d = h2f(ld_u16(blk));
+        const uint4 q = *(const uint4*)(blk + 2 + 8 * t);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+        scale_sbytes16(w, d, out);
+    } else if constexpr (T == T_Q6_K) {
+        const int h = t >> 4, s = (t >> 2) & 3, lq = 8 * (t & 3);
+        const float d = h2f(ld_u16(blk + 208));
+        // q = u - 32 for the 6-bit u; its 6-bit two's complement is u ^ 32, which
+        // sits in bits 2..7 of the byte, so the byte is 4q as an int8
+        const float ds4 = __fmul_rn(d, (float)(int8_t)blk[192 + (t >> 1)]) * 0.25f;
+        const uint4 lo = *(const uint4*)(blk + 64 * h + 32 * (s & 1) + lq);
+        const uint4 hq = *(const uint4*)(blk + 128 + 32 * h + lq);
+        const uint32_t ra = (30 + 4 * (s >> 1)) & 31;   // low nibble field -> bits 2..5
+        const uint32_t rb = (26 + 2 * s) & 31;          // 2-bit high field -> bits 6..7
+        const uint32_t l[4] = {lo.x, lo.y, lo.z, lo.w}, hh[4] = {hq.x, hq.y, hq.z, hq.w};
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = ((rotr32(l[i], ra) & 0x3C3C3C3Cu) | (rotr32(hh[i], rb) & 0xC0C0C0C0u)) ^ 0x80808080u;
+        scale_sbytes16(w, ds4, out);
+    } else if constexpr (T == T_Q3_K) {
+        const int h = t >> 4, s = (t >> 2) & 3, lq = 8 * (t & 3), j = t >> 1, hb = t >> 2;
+        // bytes 96..111: the 12 scale bytes, d, two bytes of slot padding
+        const uint4 v = *(const uint4*)(blk + 96);
+        const float d = h2f(v.w & 0xFFFFu);
+        // 6-bit scale j: low nibble j & 7 of bytes 0..7 (high nibble for j >= 8),
+        // high two bits from bytes 8..11 (dequant_k.cpp scale layout)
+        const uint32_t lw = (j & 4) ? v.y : v.x;
+        const int sc = (int)(__builtin_amdgcn_ubfe(lw, 8 * (j & 3) + 4 * (j >> 3), 4) |
+                             (__builtin_amdgcn_ubfe(v.z, 8 * (j & 3) + 2 * (j >> 2), 2) << 4)) - 32;
+        const float ds32 = __fmul_rn(d, (float)sc) * 0.03125f;
+        // q = low - 4 when the hmask bit is clear, low when set: the 3-bit two's
+        // complement (~hbit, low1, low0), placed in bits 7..5, so the byte is 32q
+        const uint4 lo = *(const uint4*)(blk + 32 + 32 * h + lq);
+        const uint4 hm = *(const uint4*)(blk + lq);
+        const uint32_t ra = (27 + 2 * s) & 31;   // 2-bit field -> bits 5..6
+        const uint32_t rb = (25 + hb) & 31;      // hmask bit -> bit 7
+        const uint32_t l[4] = {lo.x, lo.y, lo.z, lo.w}, m[4] = {hm.x, hm.y, hm.z, hm.w};
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = (rotr32(l[i], ra) & 0x60606060u) | (~rotr32(m[i], rb) & 0x80808080u);
+        scale_sbytes16(w, ds32, out);
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        const int j = t >> 2, g = t >> 3, hi = (t >> 2) & 1, lq = 8 * (t & 3);
+        const uint4 h = *(const uint4*)blk;
+        const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
+        int sc, mn;
+        scale_min_k4_regs(h.y, h.z, h.w, j, sc, mn);
+        const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
+        const uint32_t sh = 4 * hi;
+        auto f = [&](float q) { return __fsub_rn(__fmul_rn(d1, q), m1); };
+        if constexpr (T == T_Q4_K) {
+            const uint4 q = *(const uint4*)(blk + 16 + 32 * g + lq);
+            per_byte8((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu, out, f);
+            per_byte8((q.z >> sh) & 0x0F0F0F0Fu, (q.w >> sh) & 0x0F0F0F0Fu, out + 8, f);
+        } else {
+            const uint4 lo = *(const uint4*)(blk + 48 + 32 * g + lq);
+            const uint4 hb = *(const uint4*)(blk + 16 + lq);
+            const uint32_t rb = (28 + j) & 31;   // high bit j -> bit 4
+            auto u = [&](uint32_t l, uint32_t m) { return ((l >> sh) & 0x0F0F0F0Fu) | (rotr32(m, rb) & 0x10101010u); };
+            per_byte8(u(lo.x, hb.x), u(lo.y, hb.y), out, f);
+            per_byte8(u(lo.z, hb.z), u(lo.w, hb.w), out + 8, f);
+        }
+    } else {
+        decode8<T>(blk, t, out);
+        decode8<T>(blk, t + 1, out + 8);
+    }
 }
 
 // Runtime-type dispatch; `type` is uniform across the wavefront, so the

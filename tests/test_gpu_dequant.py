@@ -74,6 +74,50 @@ def test_device_dequant_bit_exact(hip, oracle_mod, t):
         assert np.array_equal(got, want)
 
 
+def _same_bits_or_nan(got, want, f16):
+    """Bit equality, except that two NaNs match whatever their sign and payload."""
+    ftype = np.float16 if f16 else np.float32
+    nan = np.isnan(got.view(ftype)) & np.isnan(want.view(ftype))
+    return np.nonzero((got != want) & ~nan)[0]
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_chunked_path_edge_blocks(hip, oracle_mod, t):
+    """Edge blocks (zero, signed-zero, subnormal, max, infinite and NaN scales;
+    saturated and patterned quant bytes) tiled into whole 4096-value chunks, so
+    every one of them goes through the LDS-staged kernel, at both alignments a
+    block can start on inside a chunk; FP16 and FP32 against the oracle."""
+    import torch
+
+    from flash_moe_hip.dequant import dequant_device
+    from test_oracle_pin import D_OFF
+
+    bs, pb = BLOCK[t]
+    edge = edge_blocks(t)
+    extra = []
+    for db in (0x7C00, 0xFC00, 0x7E00):   # +inf, -inf, NaN
+        for f in (0x00, 0x55, 0xFF):
+            blk = np.full(pb, f, np.uint8)
+            blk[D_OFF[t]:D_OFF[t] + 2] = np.array([db], np.uint16).view(np.uint8)
+            extra.append(blk)
+    blocks = np.concatenate([edge, np.stack(extra)])
+    per_chunk = 4096 // bs
+    reps = -(-2 * per_chunk // len(blocks))
+    # twice over, the second copy shifted by one block, so each edge block sits
+    # at an even and at an odd block index (2-byte vs 4-byte aligned for Q3_K,
+    # Q6_K, Q8_0)
+    tiled = np.concatenate([np.tile(blocks, (reps, 1)), blocks[1:], blocks[:1]])
+    tiled = tiled[: len(tiled) // per_chunk * per_chunk].reshape(-1)
+    src = torch.from_numpy(tiled).cuda()
+    print(f"chunked edge dequant type={t} blocks={tiled.size // pb}", flush=True)
+    for dtype, view in ((torch.float16, np.uint16), (torch.float32, np.uint32)):
+        f16 = dtype == torch.float16
+        got = dequant_device(src, t, dtype=dtype).cpu().numpy().view(view)
+        want = oracle_mod.dequant(t, tiled, want_f16=f16).view(view)
+        bad = _same_bits_or_nan(got, want, f16)
+        assert bad.size == 0, (str(dtype), bad.size, bad[:5])
+
+
 @pytest.mark.parametrize("t", [11, 12, 14, 8])
 def test_full_workload_every_value(hip, oracle_mod, t):
     """256 experts x (gate, up, down) = 768 matrices of 1,048,576 values, generated on

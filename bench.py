@@ -172,9 +172,9 @@ def roofline(kern: dict, layer, floor=None) -> dict:
     a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
     b_bytes = (K + 1) * layer.expert_bytes("down")
     if kern["a_us"] >= kern["b_us"]:
-        name, nbytes, us = "mqh::k_fast_gate_up<12, 12, 32>", a_bytes, kern["a_us"]
+        name, nbytes, us = "mqh::k_fast_gate_up<12, 12, 32, false>", a_bytes, kern["a_us"]
     else:
-        name, nbytes, us = "mqh::k_fast_down<14, 14, 8, 1>", b_bytes, kern["b_us"]
+        name, nbytes, us = "mqh::k_fast_down<14, 14, 8, 1, false>", b_bytes, kern["b_us"]
     return _hbm_roofline(name, nbytes, us, floor(nbytes) if floor else None)
 
 
@@ -555,23 +555,17 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
         replay = _graph(lambda: [call(l) for l in range(n_layers)], dev)
         ms = _time(replay, max(1, steps // n_layers)) / n_layers
         kern = _kernel_pair_times([lambda l=l: call(l) for l in range(n_layers)], 2)
-        single = name == "decode" and kern["kernels"] == 1
         res[name] = {"us_per_layer": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                      "parity_max_rel_err": float(f"{err:.3e}"),
-                     "kernels_us": {"AB": round(kern["a_us"], 2)} if single else
-                     {"A": round(kern["a_us"], 2), "B": round(kern["b_us"], 2)}}
+                     "kernels_us": {"A": round(kern["a_us"], 2), "B": round(kern["b_us"], 2)}}
         log(f"batched decode via {name}: {ms * 1e3:.2f} us/layer, parity {err:.2e}")
     best = min(res, key=lambda k: res[k]["us_per_layer"])
     kb = res[best]["kernels_us"]
     frac_a = (layers[0].expert_bytes("gate") + layers[0].expert_bytes("up")) / layers[0].bytes_per_expert()
-    if "AB" in kb:
-        dom, frac = "AB", 1.0
-    else:
-        dom = "A" if kb["A"] >= kb["B"] else "B"
-        frac = frac_a if dom == "A" else 1 - frac_a
+    dom = "A" if kb["A"] >= kb["B"] else "B"
+    frac = frac_a if dom == "A" else 1 - frac_a
     kname = {"prefill": {"A": "mqh::k_prefill_gate_up<11, 8, false, 1>", "B": "mqh::k_prefill_down<11, 2, 1>"},
-             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32>", "B": "mqh::k_fast_down<11, 11, 8, 4>",
-                        "AB": "mqh::k_fast_layer<11, 11, 32, 8>"}}[best][dom]
+             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32, false>", "B": "mqh::k_fast_down<11, 11, 8, 4, false>"}}[best][dom]
     out = {
         "workload": f"batched decode: {T} tokens, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
                     f"logits + shared, all Q3_K, {n_layers} resident layers rotated",
@@ -811,7 +805,8 @@ def bench_fp16_graph_decode(dev, n_layers: int, reps: int, cpu_seconds: float) -
         "metric": "quant-weight GB/s per layer-step", "value": round(step_bytes(L0) / (ms * 1e-3) / 1e9, 1),
         "unit": "GB/s", "us_per_layer": round(ms * 1e3, 3), "parity_max_rel_err": float(f"{err:.3e}"),
         "kernels_us": {"A": round(kern["a_us"], 3), "B": round(kern["b_us"], 3)},
-        "roofline": _hbm_roofline("mqh::k_gate_up" if dom == "A" else "mqh::k_down_combine",
+        "roofline": _hbm_roofline("mqh::k_fast_gate_up<12, 12, 32, true>" if dom == "A" else
+                                  "mqh::k_fast_down<14, 14, 8, 1, true>",
                                   a_bytes if dom == "A" else step_bytes(L0) - a_bytes,
                                   kern["a_us"] if dom == "A" else kern["b_us"]),
     }

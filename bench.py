@@ -153,15 +153,38 @@ def step_bytes(layer) -> int:
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "kernel_traffic.json"
+COUNTERS_FILE = ROOT / "profiles" / "kernel_counters.json"
+DURATIONS_FILE = ROOT / "profiles" / "kernel_durations.json"
+
+
+def _profiled(path, instance: str):
+    """The committed per-dispatch record of a kernel instance (keyed "name | grid
+    N"), taking the largest launch when several workloads run the instance."""
+    try:
+        kernels = json.loads(path.read_text())["kernels"]
+    except (OSError, KeyError, ValueError):
+        return None
+    rows = [v for k, v in kernels.items() if k.split(" | ")[0] == instance]
+    size = lambda v: v.get("hbm_bytes", v.get("active_cycles", v.get("grid_threads", 0)))
+    return max(rows, key=size) if rows else None
 
 
 def measured_traffic(instance: str):
     """HBM bytes per dispatch of a kernel instance from the committed counter
     runs (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), or None."""
-    try:
-        return json.loads(TRAFFIC_FILE.read_text())["kernels"][instance]["hbm_bytes"]
-    except (OSError, KeyError, ValueError):
+    row = _profiled(TRAFFIC_FILE, instance)
+    return row["hbm_bytes"] if row else None
+
+
+def measured_mfma(instance: str):
+    """Matrix-core counters per dispatch of a kernel instance from the committed
+    counter run: MFMA busy fraction of the SIMDs and FLOPs issued, or None."""
+    row = _profiled(COUNTERS_FILE, instance)
+    if not row:
         return None
+    return {"mfma_busy_frac": row["mfma_busy_frac"], "mfma_flop_per_dispatch": round(row["mfma_flop"]),
+            "mfma_instructions_per_dispatch": round(row["mfma_instructions"]),
+            "source": "profiles/prefill_mfma_counters.md"}
 
 
 def roofline(kern: dict, layer, floor=None) -> dict:
@@ -172,7 +195,7 @@ def roofline(kern: dict, layer, floor=None) -> dict:
     a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
     b_bytes = (K + 1) * layer.expert_bytes("down")
     if kern["a_us"] >= kern["b_us"]:
-        name, nbytes, us = "mqh::k_fast_gate_up<12, 12, 32, false>", a_bytes, kern["a_us"]
+        name, nbytes, us = "mqh::k_fast_gate_up<12, 12, 32, false, 1>", a_bytes, kern["a_us"]
     else:
         name, nbytes, us = "mqh::k_fast_down<14, 14, 8, 1, false>", b_bytes, kern["b_us"]
     return _hbm_roofline(name, nbytes, us, floor(nbytes) if floor else None)
@@ -461,11 +484,15 @@ def read_floor_us(nbytes: int, reps: int = 40) -> float:
 
 def _hbm_roofline(name: str, nbytes: float, us: float, floor_us: float | None = None) -> dict:
     """name: the kernel instance as the profiler names it; floor_us: the
-    streaming-read time of the same byte count (read_floor_us)."""
+    streaming-read time of the same byte count (read_floor_us).  Beside the
+    live event time, the committed kernel trace's average duration of the same
+    instance (its largest launch, graph-replayed in the full benchmark)."""
     gbs = nbytes / (us * 1e-6) / 1e9
+    traced = _profiled(DURATIONS_FILE, name)
     out = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name), "kernel": name,
-           "algorithmic_bytes": int(nbytes), "kernel_us": round(us, 3)}
+           "algorithmic_bytes": int(nbytes), "kernel_us": round(us, 3),
+           "kernel_us_profiled": traced["mean_us"] if traced else None}
     if floor_us is not None:
         out["read_floor_us"] = round(floor_us, 3)
         out["frac_of_read_floor"] = round(floor_us / us, 4)
@@ -565,7 +592,7 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
     dom = "A" if kb["A"] >= kb["B"] else "B"
     frac = frac_a if dom == "A" else 1 - frac_a
     kname = {"prefill": {"A": "mqh::k_prefill_gate_up<11, 8, false, 1>", "B": "mqh::k_prefill_down<11, 2, 1>"},
-             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32, false>", "B": "mqh::k_fast_down<11, 11, 8, 4, false>"}}[best][dom]
+             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32, false, 2>", "B": "mqh::k_fast_down<11, 11, 8, 4, false>"}}[best][dom]
     out = {
         "workload": f"batched decode: {T} tokens, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
                     f"logits + shared, all Q3_K, {n_layers} resident layers rotated",
@@ -649,6 +676,9 @@ def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
         "kernels_us": {"k_prefill_gate_up": round(kern["a_us"], 2), "k_prefill_down": round(kern["b_us"], 2)},
         "roofline": roof,
         "mfma_ceiling": {"peak_tflops_fp16_dense": 2500.0, "frac": round(tflops / 2500.0, 5)},
+        # matrix-core activity of the gate/up GEMM from the committed counter run
+        # (useful FLOPs are about a quarter of those issued: ~4 of 16 token columns)
+        "mfma_counters": measured_mfma("mqh::k_prefill_gate_up<12, 8, true, 1>"),
     }
     if cpu_seconds > 0:
         L0 = layers[0]
@@ -805,7 +835,7 @@ def bench_fp16_graph_decode(dev, n_layers: int, reps: int, cpu_seconds: float) -
         "metric": "quant-weight GB/s per layer-step", "value": round(step_bytes(L0) / (ms * 1e-3) / 1e9, 1),
         "unit": "GB/s", "us_per_layer": round(ms * 1e3, 3), "parity_max_rel_err": float(f"{err:.3e}"),
         "kernels_us": {"A": round(kern["a_us"], 3), "B": round(kern["b_us"], 3)},
-        "roofline": _hbm_roofline("mqh::k_fast_gate_up<12, 12, 32, true>" if dom == "A" else
+        "roofline": _hbm_roofline("mqh::k_fast_gate_up<12, 12, 32, true, 1>" if dom == "A" else
                                   "mqh::k_fast_down<14, 14, 8, 1, true>",
                                   a_bytes if dom == "A" else step_bytes(L0) - a_bytes,
                                   kern["a_us"] if dom == "A" else kern["b_us"]),

@@ -282,8 +282,10 @@ __device__ __forceinline__ void item_loads(const uint8_t* Gm, const uint8_t* Um,
 
 // SGT: the shared expert's gate/up type (its waves take that code path).
 // ROUTED: the router's select step first (p.route_scores set, at most
-// ROUTE_PROLOGUE_MAX_EXPERTS experts).
-template <int GT, int SGT, int LPR, bool ROUTED, bool F16G>
+// ROUTE_PROLOGUE_MAX_EXPERTS experts).  IPW: consecutive items per wave (the
+// same slot: items per slot are a multiple of it), loaded together and
+// sharing the wave's token operand.
+template <int GT, int SGT, int LPR, bool ROUTED, bool F16G, int IPW = 1>
 __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodeParams& p, SharedX<64 * LPR, F16G>& sh) {
     constexpr int H = 64 * LPR, RPI = 64 / LPR, NX = H / 4;   // NX threads hold the token, four values each
     constexpr int NA = LaneGeo<GT>::NRAW > LaneGeo<SGT>::NRAW ? LaneGeo<GT>::NRAW : LaneGeo<SGT>::NRAW;
@@ -293,7 +295,7 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     // (h.a_waves = blockDim.x / 64: blockDim.x is a 16-bit field that takes a
     // vector load and a full wait); items per slot are a power of two
     const int per_slot = h.a_inter / RPI;
-    const int item = uniform((int)blockIdx.x * h.a_waves + wave);
+    const int item = uniform(((int)blockIdx.x * h.a_waves + wave) * IPW);
     const bool live = item < h.S * per_slot;
     const int s = live ? item >> __builtin_ctz(per_slot) : 0;
     const int row0 = live ? (item & (per_slot - 1)) * RPI : 0;
@@ -360,12 +362,15 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     const bool sw = SGT != GT && shared;   // wave-uniform
 
     // then every weight load of this lane (waiting for x does not wait for them)
-    uint32_t rg[NA], ru[NA];
-    if constexpr (SGT == GT) {
-        item_loads<GT, H>(Gm, Um, row, blk, k, rg, ru);
-    } else {
-        if (sw) item_loads<SGT, H>(Gm, Um, row, blk, k, rg, ru);
-        else item_loads<GT, H>(Gm, Um, row, blk, k, rg, ru);
+    uint32_t rg[IPW][NA], ru[IPW][NA];
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+        if constexpr (SGT == GT) {
+            item_loads<GT, H>(Gm, Um, row + i * RPI, blk, k, rg[i], ru[i]);
+        } else {
+            if (sw) item_loads<SGT, H>(Gm, Um, row + i * RPI, blk, k, rg[i], ru[i]);
+            else item_loads<GT, H>(Gm, Um, row + i * RPI, blk, k, rg[i], ru[i]);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     // 2. token digits (in the FP16 graph also the token rounded to FP16), and
@@ -383,16 +388,17 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     // only one operand set is live; the weight loads are all issued already,
     // so the waits inside stay exact)
     const bool f16w = F16G && !shared;   // wave-uniform
-    float g = 0.0f, u = 0.0f;
+    float g[IPW], u[IPW];
     if (f16w) {
         if constexpr (F16G) {
+            static_assert(IPW == 1, "one item per wave in the FP16 graph");
             LaneH XH;
             lane_xh<GT>(sh.x16, blk, k, XH);
             __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
             // 3. gate and up dot products
-            g = lane_dot_f16<GT>(rg, k, XH);
-            u = lane_dot_f16<GT>(ru, k, XH);
+            g[0] = lane_dot_f16<GT>(rg[0], k, XH);
+            u[0] = lane_dot_f16<GT>(ru[0], k, XH);
         }
     } else {
         DigitsRef xd;
@@ -403,31 +409,36 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         // 3. gate and up dot products
-        if (sw) {
-            g = lane_dot<SGT>(rg, k, X);
-            u = lane_dot<SGT>(ru, k, X);
-        } else {
-            g = lane_dot<GT>(rg, k, X);
-            u = lane_dot<GT>(ru, k, X);
+#pragma unroll
+        for (int i = 0; i < IPW; ++i) {
+            if (sw) {
+                g[i] = lane_dot<SGT>(rg[i], k, X);
+                u[i] = lane_dot<SGT>(ru[i], k, X);
+            } else {
+                g[i] = lane_dot<GT>(rg[i], k, X);
+                u[i] = lane_dot<GT>(ru[i], k, X);
+            }
         }
     }
 
     // SwiGLU: one FP32 activation per row
     if (live) {
-        g = lane_group_sum<LPR>(g);
-        u = lane_group_sum<LPR>(u);
-        if (li == 0) {
-            float a;
-            if (f16w) {
-                // the FP16 graph's rounding points (moe_quant_dot.cpp:197-206)
-                g = round16(g);
-                u = round16(u);
-                const float sig = round16(1.0f / (1.0f + expf(-g)));
-                a = round16(round16(g * sig) * u);
-            } else {
-                a = silu_mul(g, u);
+#pragma unroll
+        for (int i = 0; i < IPW; ++i) {
+            float gs = lane_group_sum<LPR>(g[i]), us = lane_group_sum<LPR>(u[i]);
+            if (li == 0) {
+                float a;
+                if (f16w) {
+                    // the FP16 graph's rounding points (moe_quant_dot.cpp:197-206)
+                    gs = round16(gs);
+                    us = round16(us);
+                    const float sig = round16(1.0f / (1.0f + expf(-gs)));
+                    a = round16(round16(gs * sig) * us);
+                } else {
+                    a = silu_mul(gs, us);
+                }
+                h.act[((int64_t)t * h.S + s) * h.a_inter + row + i * RPI] = bad ? 0.0f : a;
             }
-            h.act[((int64_t)t * h.S + s) * h.a_inter + row] = bad ? 0.0f : a;
         }
         if (bad && lane == 0 && row0 == 0) atomicOr(&p.flags[FLAG_BAD_ID], 1);
     }
@@ -454,13 +465,13 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     }
 }
 
-template <int GT, int SGT, int LPR, bool F16G>
+template <int GT, int SGT, int LPR, bool F16G, int IPW = 1>
 __global__ __launch_bounds__(1024) void k_fast_gate_up(const float* x, const int32_t* ids, float* act, const float* sh_gate_inp, int top_k,
                                                   int S, int has_shared, int n_experts, int a_inter, int a_waves,
                                                   DecodeParams p) {
     __shared__ SharedX<64 * LPR, F16G> sh;
     const DecodeHot h{x, ids, act, nullptr, sh_gate_inp, top_k, S, has_shared, n_experts, a_inter, a_waves};
-    gate_up_items<GT, SGT, LPR, false, F16G>(h, p, sh);
+    gate_up_items<GT, SGT, LPR, false, F16G, IPW>(h, p, sh);
 }
 
 // Kernel A with the router's select step in its prologue: the same work as
@@ -668,8 +679,31 @@ static int gate_up_waves(int items, int tokens, int hidden, int cus) {
     return best;
 }
 
+#ifndef FAST_A_PAIR_TOKENS
+#define FAST_A_PAIR_TOKENS 4   // tokens from which kernel A gives each wave two items
+#endif
+
+template <int GT, int SGT, int LPR, bool F16G, int IPW>
+static void launch_a_ipw(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
+    const int items = p.S * (p.inter / (64 / LPR)) / IPW;   // wave-items
+    const int w = gate_up_waves(items, p.n_tokens, 64 * LPR, device_cus());
+    const dim3 grid((items + w - 1) / w, p.n_tokens), block(64 * w);
+    if (ev.armed_a())
+        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, IPW>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
+    else
+        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, IPW>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
+}
+
 template <int GT, int SGT, int LPR, bool F16G>
 static void launch_a(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
+    if constexpr (!F16G) {
+        // many tokens: two items a wave, so each wave has twice the weights in
+        // flight behind one prologue (the per-token launches are latency-bound)
+        if (p.route_scores == nullptr && p.n_tokens >= FAST_A_PAIR_TOKENS) {
+            launch_a_ipw<GT, SGT, LPR, F16G, 2>(p, stream, ev);
+            return;
+        }
+    }
     const int items = p.S * (p.inter / (64 / LPR));
     const int w = gate_up_waves(items, p.n_tokens, 64 * LPR, device_cus());
     const dim3 grid((items + w - 1) / w, p.n_tokens), block(64 * w);

@@ -327,29 +327,45 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     if (shared) { Gm = p.sh_gate; Um = p.sh_up; }
     bool bad = false;
     if constexpr (ROUTED) {
-        // routing in the prologue (router.py:140-170): every wave takes the top
-        // s+1 of token t's router scores (the x load above is in flight
-        // meanwhile); the token's first item takes all top_k and writes the ids
-        // and softmax weights for the down kernel and the caller.  Every wave
-        // reads the scores (no conditional load).
-        uint64_t key[ROUTE_PROLOGUE_MAX_EXPERTS / 64];
-        route_keys(p.route_scores + (int64_t)t * h.n_experts, h.n_experts, lane, key);
-        if (live && !shared) {
-            const bool publish = item == 0;
-            const int rounds = publish ? h.top_k : s + 1;
-            int e = 0;
-            float mine = 0.0f;
-            for (int r = 0; r < rounds; ++r) {
-                const uint64_t win = route_next(key);
-                if (r == s) e = key_expert(win);
-                if (lane == r) mine = key_score(win);
-                if (publish && lane == 0) p.route_ids[t * h.top_k + r] = key_expert(win);
+        // routing in the prologue (router.py:140-170).  A workgroup's items are
+        // consecutive, so its routed waves need the experts of ranks s_first ..
+        // s_last: its first wave takes the top s_last + 1 of token t's router
+        // scores (all top_k in the token's first workgroup, which also writes
+        // the ids and softmax weights for the down kernel and the caller) while
+        // the token's load is in flight, and hands the experts to the other
+        // waves through LDS.
+        __shared__ int s_rank[FAST_MAX_SLOTS];
+        const int sh_ps = __builtin_ctz(per_slot);
+        const int it_first = (int)blockIdx.x * h.a_waves * IPW;
+        const int it_last = min(it_first + h.a_waves * IPW - 1, h.S * per_slot - 1);
+        if ((it_first >> sh_ps) < h.top_k) {   // the workgroup has a routed item (uniform)
+            if (wave == 0) {
+                const bool publish = blockIdx.x == 0;
+                const int rounds = publish ? h.top_k : min(it_last >> sh_ps, h.top_k - 1) + 1;
+                uint64_t key[ROUTE_PROLOGUE_MAX_EXPERTS / 64];
+                route_keys(p.route_scores + (int64_t)t * h.n_experts, h.n_experts, lane, key);
+                float mine = 0.0f;
+                for (int r = 0; r < rounds; ++r) {
+                    const uint64_t win = route_next(key);
+                    if (lane == r) mine = key_score(win);
+                    if (lane == 0) {
+                        s_rank[r] = key_expert(win);
+                        if (publish) p.route_ids[t * h.top_k + r] = key_expert(win);
+                    }
+                }
+                if (publish) {
+                    const float w = route_weight(mine, h.top_k, lane);
+                    if (lane < h.top_k) p.route_weights[t * h.top_k + lane] = w;
+                }
             }
-            if (publish) {
-                const float w = route_weight(mine, h.top_k, lane);
-                if (lane < h.top_k) p.route_weights[t * h.top_k + lane] = w;
+            // (LDS only: the token's and id loads stay in flight)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            if (live && !shared) {
+                const int e = s_rank[s];
+                Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
             }
-            Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
         }
     } else if (live && !shared) {
         int e = id_raw;

@@ -16,9 +16,11 @@ gap between graph nodes.  roofline: the dominant kernel's algorithmic bytes /
 its average duration, from HIP events the runtime records at each kernel's
 start and end during a second, eager pass over the same layers.
 
-cpu_baseline: the CPU oracle (a restatement of the reference's AVX2 kernel)
-running the same layer as 9 moe_quant_expert calls on 4 worker threads -- the
-reference's expert-worker policy -- on the host cores, for a bounded sample.
+cpu_baseline: the oracle's AVX2 form of the reference's fused expert (direct
+Q3_K/Q6_K bit-field decoding into an 8-lane FMA accumulator, the reference's
+quant_dot; bit-identical to the scalar oracle) running the same layer as 9
+moe_quant_expert calls on 4 worker threads -- the reference's expert-worker
+policy -- on the host cores, for a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -224,14 +226,9 @@ def cpu_baseline(layers, xs, ids, ws, seconds: float, workers: int = 4):
         experts = [L.host_expert(int(e)) for e in ids[l]] + [L.host_shared()]
         jobs.append((experts, xs[l], ws[l]))
 
-    def one_step(job):
-        experts, x, w = job
-        outs = [oracle.expert_forward(t, TYPES, x, H, I, 0) for t in experts[:K]]
-        return oracle.combine(outs, [float(v) for v in w], oracle.expert_forward(experts[K], TYPES, x, H, I, 0))
-
     def one_step_parallel(pool, job):
         experts, x, w = job
-        futs = [pool.submit(oracle.expert_forward, t, TYPES, x, H, I, 0) for t in experts]
+        futs = [pool.submit(oracle.expert_forward, t, TYPES, x, H, I, 0, True) for t in experts]
         outs = [f.result() for f in futs]
         return oracle.combine(outs[:K], [float(v) for v in w], outs[K])
 
@@ -247,7 +244,7 @@ def cpu_baseline(layers, xs, ids, ws, seconds: float, workers: int = 4):
     with ThreadPoolExecutor(CPU_THREADS) as pool:
         calls, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < seconds / 2:
-            futs = [pool.submit(oracle.expert_forward, t, TYPES, jobs[j % n_src][1], H, I, 0)
+            futs = [pool.submit(oracle.expert_forward, t, TYPES, jobs[j % n_src][1], H, I, 0, True)
                     for j in range(4) for t in jobs[j % n_src][0]]
             for f in futs:
                 f.result()
@@ -259,7 +256,7 @@ def cpu_baseline(layers, xs, ids, ws, seconds: float, workers: int = 4):
         "unit": "GB/s",
         "cores": workers,
         "kind": "port",
-        "sample": f"{steps} token-layers (9 expert calls each, FP32 graph) over {n_src} layers, "
+        "sample": f"{steps} token-layers (9 AVX2 expert calls each, FP32 graph) over {n_src} layers, "
                   f"{dt:.1f} s on {workers} threads (the reference's expert-worker count); host has "
                   f"{os.cpu_count()} logical CPUs",
         "us_per_layer": round(per_step * 1e6, 1),
@@ -525,7 +522,7 @@ def _oracle_tokens(layer, types, X, ids, ws, t_list):
 
 
 def _cpu_pairs(jobs, seconds: float, workers: int):
-    """Run oracle expert calls (types, bytes, x) on `workers` threads for about
+    """Run AVX2 oracle expert calls (types, bytes, x) on `workers` threads for about
     `seconds`; returns (calls, elapsed)."""
     import oracle
 
@@ -534,9 +531,22 @@ def _cpu_pairs(jobs, seconds: float, workers: int):
     with ThreadPoolExecutor(workers) as pool:
         while time.perf_counter() - t0 < seconds:
             batch = [jobs[(calls + i) % len(jobs)] for i in range(4 * workers)]
-            list(pool.map(lambda j: oracle.expert_forward(j[1], j[0], j[2], H, I, 0), batch))
+            list(pool.map(lambda j: oracle.expert_forward(j[1], j[0], j[2], H, I, 0, True), batch))
             calls += len(batch)
     return calls, time.perf_counter() - t0
+
+
+def _one_thread_expert_us(job, seconds: float) -> float:
+    """Microseconds per AVX2 expert call (types, bytes, x) on one thread."""
+    import oracle
+
+    types, tensors, x = job
+    oracle.expert_forward(tensors, types, x, H, I, 0, True)
+    calls, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        oracle.expert_forward(tensors, types, x, H, I, 0, True)
+        calls += 1
+    return round((time.perf_counter() - t0) / calls * 1e6, 1)
 
 
 def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> dict:
@@ -610,7 +620,8 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
         per_step = dt / calls * T * (K + 1)
         out["cpu_baseline"] = {"value": round(nbytes / per_step / 1e9, 3), "unit": "GB/s", "cores": CPU_THREADS,
                                "kind": "port", "us_per_layer": round(per_step * 1e6, 1),
-                               "sample": f"{calls} per-token expert calls (16 tokens x 9 per step), {dt:.1f} s"}
+                               "sample": f"{calls} per-token AVX2 expert calls (16 tokens x 9 per step), {dt:.1f} s",
+                               "per_expert_us_1_thread": _one_thread_expert_us(jobs[0], cpu_seconds / 4)}
     del layers
     torch.cuda.empty_cache()
     return out
@@ -687,7 +698,7 @@ def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
         per_layer = dt / calls * T * (K + 1)
         out["cpu_baseline"] = {"value": round(flop / per_layer / 1e12, 5), "unit": "TFLOP/s",
                                "cores": CPU_THREADS, "kind": "port", "us_per_layer": round(per_layer * 1e6, 1),
-                               "sample": f"{calls} (token, expert) calls of the native-kernel port, {dt:.1f} s; "
+                               "sample": f"{calls} (token, expert) AVX2 calls of the native-kernel port, {dt:.1f} s; "
                                          "the reference prefill (OpenVINO) is not available"}
     del layers
     torch.cuda.empty_cache()
@@ -846,13 +857,13 @@ def bench_fp16_graph_decode(dev, n_layers: int, reps: int, cpu_seconds: float) -
         done, t0 = 0, time.perf_counter()
         with ThreadPoolExecutor(4) as pool:
             while time.perf_counter() - t0 < cpu_seconds:
-                list(pool.map(lambda t: oracle.expert_forward(t, TYPES, xs[0], H, I, 1), jobs))
+                list(pool.map(lambda t: oracle.expert_forward(t, TYPES, xs[0], H, I, 1, True), jobs))
                 done += 1
         dt = time.perf_counter() - t0
         per = dt / done * (K + 1) / K
         out["cpu_baseline"] = {"value": round(step_bytes(L0) / per / 1e9, 3), "unit": "GB/s", "cores": 4,
                                "kind": "port", "us_per_layer": round(per * 1e6, 1),
-                               "sample": f"{done} x 8 FP16-graph expert calls on 4 threads, {dt:.1f} s"}
+                               "sample": f"{done} x 8 FP16-graph AVX2 expert calls on 4 threads, {dt:.1f} s"}
     del layers
     torch.cuda.empty_cache()
     return out
@@ -903,11 +914,11 @@ def bench_single_expert(dev, reps: int, cpu_seconds: float) -> dict:
         oracle.lib()
         calls, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < cpu_seconds / 2:
-            oracle.expert_forward(tensors, kinds, x, H, I, 0)
+            oracle.expert_forward(tensors, kinds, x, H, I, 0, True)
             calls += 1
         dt = time.perf_counter() - t0
         out["cpu_baseline"] = {"value": round(dt / calls * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
-                               "sample": f"{calls} calls of the moe_quant_expert port (FP32 graph), one thread, "
+                               "sample": f"{calls} calls of the AVX2 moe_quant_expert port (FP32 graph), one thread, "
                                          f"{dt:.1f} s"}
     del layers
     torch.cuda.empty_cache()

@@ -7,8 +7,8 @@ it and never falls back to it.
 
 Contents
 --------
-* ``liboracle_kquant.so`` (built from ``kquant_oracle.c`` and ``delta_oracle.c``
-  by ``Makefile``): a C restatement of the reference kernels
+* ``liboracle_kquant.so`` (built from ``kquant_oracle.c``, ``kquant_avx2.c`` and
+  ``delta_oracle.c`` by ``Makefile``): a C restatement of the reference kernels
   ``cpp/dequant_k.cpp``, ``cpp/moe_quant_dot.cpp`` and ``cpp/moe_delta.cpp``.
   Wrapped here as :func:`dequant_k`, :func:`moe_quant_expert` and
   :func:`delta_heads` with the reference's argument meaning and status codes.
@@ -65,6 +65,8 @@ def lib() -> C.CDLL:
         L.oracle_moe_quant_expert.argtypes = [C.c_int, C.c_void_p, C.c_int64] * 3 + [
             C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int]
         L.oracle_moe_quant_expert.restype = C.c_int
+        L.oracle_moe_quant_expert_avx2.argtypes = L.oracle_moe_quant_expert.argtypes
+        L.oracle_moe_quant_expert_avx2.restype = C.c_int
         L.oracle_f32_to_f16.argtypes = [C.c_float]
         L.oracle_f32_to_f16.restype = C.c_uint16
         L.oracle_f16_to_f32.argtypes = [C.c_uint16]
@@ -129,9 +131,12 @@ def dequant(ggml_type: int, raw, n: int | None = None, want_f16: bool = False) -
 
 
 def moe_quant_expert(tensors: dict, kinds: dict, x, hidden: int, intermediate: int,
-                     fp16_graph: int = 0):
+                     fp16_graph: int = 0, avx2: bool = False):
     """(status, y) with the argument meaning of ``moe_quant_expert``
-    (moe_quant_dot.cpp:171-214).  ``tensors`` maps gate/up/down to raw bytes."""
+    (moe_quant_dot.cpp:171-214).  ``tensors`` maps gate/up/down to raw bytes.
+    ``avx2`` runs the AVX2 row dot of ``kquant_avx2.c`` (the reference's
+    direct Q3_K/Q6_K form, moe_quant_dot.cpp:23-169): the same result bit for
+    bit, the CPU baseline of the bench."""
     arrays = [np.ascontiguousarray(np.frombuffer(bytes(tensors[k]), np.uint8) if
                                    isinstance(tensors[k], (bytes, bytearray)) else tensors[k],
                                    dtype=np.uint8).reshape(-1) for k in ("gate", "up", "down")]
@@ -140,13 +145,13 @@ def moe_quant_expert(tensors: dict, kinds: dict, x, hidden: int, intermediate: i
         args.extend((int(kinds[name]), raw.ctypes.data, raw.nbytes))
     xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
     out = np.zeros(hidden, np.float32)
-    rc = lib().oracle_moe_quant_expert(*args, xv.ctypes.data, int(hidden), int(intermediate),
-                                       out.ctypes.data, int(fp16_graph))
+    fn = lib().oracle_moe_quant_expert_avx2 if avx2 else lib().oracle_moe_quant_expert
+    rc = fn(*args, xv.ctypes.data, int(hidden), int(intermediate), out.ctypes.data, int(fp16_graph))
     return rc, out
 
 
-def expert_forward(tensors, kinds, x, hidden, intermediate, fp16_graph=0) -> np.ndarray:
-    rc, y = moe_quant_expert(tensors, kinds, x, hidden, intermediate, fp16_graph)
+def expert_forward(tensors, kinds, x, hidden, intermediate, fp16_graph=0, avx2=False) -> np.ndarray:
+    rc, y = moe_quant_expert(tensors, kinds, x, hidden, intermediate, fp16_graph, avx2)
     if rc != 0:
         raise RuntimeError(f"oracle expert failed with status {rc}")
     return y

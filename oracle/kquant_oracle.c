@@ -227,6 +227,8 @@ static int decode_block(int type, const uint8_t* blk, float* out) {
     }
 }
 
+int oracle_decode_block(int type, const uint8_t* blk, float* out) { return decode_block(type, blk, out); }
+
 int oracle_dequant_k_supported(int type) { return oracle_block_size(type) != 0; }
 int oracle_dequant_k_block_size(int type) { return oracle_block_size(type); }
 
@@ -275,17 +277,15 @@ static float quant_dot(int type, const uint8_t* row, const float* x, int cols, i
     return r;
 }
 
-/* Same signature, argument meaning and status codes as the reference export
- * moe_quant_expert (moe_quant_dot.cpp:171-214):
- *   0 ok; -1 null pointer, hidden/intermediate <= 0 or > 65536, fp16_graph not
- *   0/1; -2 unsupported type or cols % block; -3 byte size mismatch; -4 a
- *   non-finite output (outputs up to and including that row are written);
- *   -5 allocation failure. */
-int oracle_moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes,
-                            int up_type, const uint8_t* up, int64_t up_bytes,
-                            int down_type, const uint8_t* down, int64_t down_bytes,
-                            const float* input, int hidden, int intermediate,
-                            float* output, int fp16_graph) {
+/* The fused SwiGLU expert of moe_quant_expert (moe_quant_dot.cpp:171-214) over
+ * a given row dot: its validation, its FP16-graph rounding points and its
+ * status codes (listed at oracle_moe_quant_expert below). */
+typedef float (*row_dot_fn)(int type, const uint8_t* row, const float* x, int cols, int round_w);
+
+static int expert_with(row_dot_fn quant_dot, int gate_type, const uint8_t* gate, int64_t gate_bytes,
+                       int up_type, const uint8_t* up, int64_t up_bytes,
+                       int down_type, const uint8_t* down, int64_t down_bytes,
+                       const float* input, int hidden, int intermediate, float* output, int fp16_graph) {
     const int types[3] = {gate_type, up_type, down_type};
     const int cols[3] = {hidden, hidden, intermediate};
     const int rows[3] = {intermediate, intermediate, hidden};
@@ -326,6 +326,34 @@ int oracle_moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_byt
     free(x);
     free(act);
     return status;
+}
+
+/* Same signature, argument meaning and status codes as the reference export
+ * moe_quant_expert (moe_quant_dot.cpp:171-214):
+ *   0 ok; -1 null pointer, hidden/intermediate <= 0 or > 65536, fp16_graph not
+ *   0/1; -2 unsupported type or cols % block; -3 byte size mismatch; -4 a
+ *   non-finite output (outputs up to and including that row are written);
+ *   -5 allocation failure. */
+int oracle_moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes,
+                            int up_type, const uint8_t* up, int64_t up_bytes,
+                            int down_type, const uint8_t* down, int64_t down_bytes,
+                            const float* input, int hidden, int intermediate,
+                            float* output, int fp16_graph) {
+    return expert_with(quant_dot, gate_type, gate, gate_bytes, up_type, up, up_bytes, down_type, down, down_bytes,
+                       input, hidden, intermediate, output, fp16_graph);
+}
+
+/* The same expert with the AVX2 row dot of kquant_avx2.c (bit-identical
+ * results; the CPU baseline of the bench). */
+float oracle_quant_dot_avx2(int type, const uint8_t* row, const float* x, int cols, int round_w);
+
+int oracle_moe_quant_expert_avx2(int gate_type, const uint8_t* gate, int64_t gate_bytes,
+                                 int up_type, const uint8_t* up, int64_t up_bytes,
+                                 int down_type, const uint8_t* down, int64_t down_bytes,
+                                 const float* input, int hidden, int intermediate,
+                                 float* output, int fp16_graph) {
+    return expert_with(oracle_quant_dot_avx2, gate_type, gate, gate_bytes, up_type, up, up_bytes, down_type, down,
+                       down_bytes, input, hidden, intermediate, output, fp16_graph);
 }
 
 /* ------------------------------------------ IQ4_NL (cpp/fast_dequant.cpp:40-65) */

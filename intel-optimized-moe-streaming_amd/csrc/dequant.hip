@@ -66,41 +66,64 @@ __global__ __launch_bounds__(DQ_THREADS) void k_dequant(const uint8_t* __restric
 // LDS one block per slot (slot_bytes/slot_offset: the 16-byte fields land on
 // 16-byte boundaries).  Every thread then decodes two adjacent 8-value groups
 // of one block -- the two share the block header and, for the K-quants, the
-// sub-block scale -- and stores 16 consecutive values.
+// sub-block scale -- and the wave stores its 1,024 values with coalesced
+// 16-byte pieces.  (Two or more chunks per workgroup, all their loads in
+// flight together, measured no faster.)
 constexpr int DQ_CHUNK_VALUES = DQ_THREADS * 16;
 
-// Copy one chunk into its LDS slots with aligned, coalesced 16-byte loads.
-// Where slot and block coincide (Q4_K, Q5_K: 144 and 176 bytes) the words go
-// to LDS as they are; otherwise each 16-byte word (which spans at most two
-// blocks: every block is longer than 16 bytes) is written as 2-byte pieces,
-// each at its block's slot -- naturally aligned LDS writes, where 16-byte
-// writes at 2 mod 4 addresses would stall.
-template <int T>
-__device__ __forceinline__ void stage_chunk(const uint8_t* __restrict__ src, uint8_t* lds) {
+// Copy NBK consecutive blocks into their LDS slots with aligned, coalesced
+// 16-byte loads (all issued before the first write).  Where slot and block
+// coincide (Q4_K, Q5_K: 144 and 176 bytes) the words go to LDS as they are;
+// otherwise each 16-byte word (which spans at most two blocks: every block is
+// longer than 16 bytes) is written as 2-byte pieces, each at its block's slot
+// -- naturally aligned LDS writes, where 16-byte writes at 2 mod 4 addresses
+// would stall.
+template <int T, int NBK>
+__device__ __forceinline__ void stage_blocks(const uint8_t* __restrict__ src, uint8_t* lds) {
     constexpr int PB = block_bytes(T), SL = slot_bytes(T), OFF = slot_offset(T);
-    constexpr int NB = DQ_CHUNK_VALUES / block_size(T);
+    constexpr int NW = NBK * PB / 16, IT = (NW + DQ_THREADS - 1) / DQ_THREADS;
     static_assert(PB > 16, "a 16-byte word meets at most two blocks");
+    uint4 w[IT];
 #pragma unroll
-    for (int i = threadIdx.x; i < NB * PB / 16; i += DQ_THREADS) {
-        const uint4 w = ((const uint4*)src)[i];
+    for (int k = 0; k < IT; ++k) {
+        const int i = threadIdx.x + k * DQ_THREADS;
+        if (NW % DQ_THREADS == 0 || i < NW) w[k] = ((const uint4*)src)[i];
+    }
+#pragma unroll
+    for (int k = 0; k < IT; ++k) {
+        const int i = threadIdx.x + k * DQ_THREADS;
+        if (NW % DQ_THREADS != 0 && i >= NW) break;
         if constexpr (SL == PB && OFF == 0) {
-            ((uint4*)lds)[i] = w;
+            ((uint4*)lds)[i] = w[k];
         } else {
             // pieces m < mb belong to block b0, the rest to block b0 + 1
             const int x = 16 * i, b0 = x / PB, mb = ((b0 + 1) * PB - x) / 2;
             uint16_t* at0 = (uint16_t*)(lds + x + b0 * (SL - PB) + OFF);
             uint16_t* at1 = at0 + (SL - PB) / 2;
-            const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+            const uint32_t q[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
 #pragma unroll
             for (int m = 0; m < 8; ++m) (m < mb ? at0 : at1)[m] = (uint16_t)(q[m >> 1] >> (16 * (m & 1)));
         }
     }
 }
 
+// A wave's 64 x 16 decoded values (lane l: values 16l .. 16l+15 of the wave's
+// run) to dst, through the wave's LDS exchange area xw, so that every store
+// instruction writes 64 consecutive 16-byte pieces (lane l piece l): stores of
+// 32 contiguous bytes per lane, half-filled lines per instruction, ran 3-13 %
+// slower on the full-size workload.  LDS operations of one wave complete in
+// order; the wave fences only keep the compiler from moving them.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <bool F16>
-__device__ __forceinline__ void store16(const float v[16], int64_t gi, void* dst) {
+__device__ __forceinline__ void store16_wave(const float v[16], uint4* xw, uint4* dst_wave, int lane) {
+    constexpr int P = F16 ? 2 : 4;   // 16-byte pieces per lane
+    uint4 o[P];
     if constexpr (F16) {
-        uint4 o[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             o[h].x = pack_f2h_rn(v[8 * h + 0], v[8 * h + 1]);
@@ -108,13 +131,20 @@ __device__ __forceinline__ void store16(const float v[16], int64_t gi, void* dst
             o[h].z = pack_f2h_rn(v[8 * h + 4], v[8 * h + 5]);
             o[h].w = pack_f2h_rn(v[8 * h + 6], v[8 * h + 7]);
         }
-        ((uint4*)dst)[gi] = o[0];
-        ((uint4*)dst)[gi + 1] = o[1];
     } else {
-        float4* o = (float4*)dst + 2 * gi;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) o[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        for (int q = 0; q < 4; ++q)
+            o[q] = make_uint4(__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]), __float_as_uint(v[4 * q + 2]),
+                              __float_as_uint(v[4 * q + 3]));
     }
+#pragma unroll
+    for (int k = 0; k < P; ++k) xw[P * lane + k] = o[k];
+    wave_lds_sync();
+#pragma unroll
+    for (int k = 0; k < P; ++k) o[k] = xw[64 * k + lane];
+#pragma unroll
+    for (int k = 0; k < P; ++k) dst_wave[64 * k + lane] = o[k];
+    wave_lds_sync();   // the next call's writes follow this call's reads
 }
 
 template <int T, bool F16>
@@ -124,12 +154,15 @@ __global__ __launch_bounds__(DQ_THREADS) void k_dequant_lds(const uint8_t* __res
     static_assert(SL % 16 == 0 && G % 2 == 0 && PB % 2 == 0, "16-byte slots, group pairs in one block");
     __shared__ __attribute__((aligned(16))) uint8_t buf[NB * SL];
     const int64_t chunk = blockIdx.x;
-    stage_chunk<T>(src + chunk * (NB * PB), buf);
+    stage_blocks<T, NB>(src + chunk * (NB * PB), buf);
     __syncthreads();
+    __shared__ uint4 xch[DQ_THREADS / 64][F16 ? 128 : 256];
     const int b = 2 * threadIdx.x / G, t = 2 * threadIdx.x - b * G;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     float v[16];
     decode16<T>(buf + b * SL + slot_offset(T), t, v);
-    store16<F16>(v, chunk * (DQ_CHUNK_VALUES / 8) + 2 * threadIdx.x, dst);
+    // the wave's 1,024 values start at value chunk * 4096 + 1024 wv
+    store16_wave<F16>(v, xch[wv], (uint4*)dst + (chunk * DQ_CHUNK_VALUES + 1024 * wv) / (F16 ? 8 : 4), lane);
 }
 
 template <int T>

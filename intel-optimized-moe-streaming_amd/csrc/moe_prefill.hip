@@ -10,10 +10,10 @@
 // Four launches, no inter-workgroup synchronisation:
 //   P0 k_prefill_route     one workgroup: buckets the (token, slot) pairs by expert
 //                          and cuts each expert's tokens into tiles of 16.
-//   P1 k_prefill_gate_up   grid (I/64, max_tiles): 64 intermediate rows x one tile,
+//   P1 k_prefill_gate_up   (I/64) x max_tiles workgroups: 64 intermediate rows x one tile,
 //                          SwiGLU fused; the shared expert's tiles also produce its
 //                          sigmoid gate.
-//   P2 k_prefill_down      grid (H/64, max_tiles): 64 output rows x one tile.
+//   P2 k_prefill_down      (H/128) x max_tiles workgroups: 128 output rows x one tile.
 //   P3 k_prefill_combine   grid (H/256, T): the weighted sum in top-k order.
 //
 // P1/P2 are MFMA GEMMs (v_mfma_f32_16x16x32_f16, FP32 accumulate) whose weight
@@ -95,64 +95,112 @@ __device__ __forceinline__ float pf_wave_sum(float v) {
 // j of the B operand: high plane xh[j][K + PF_PAD], low plane xl (SPLIT only),
 // and the 32-column sub-block sums / 32 as [block][j][hi 0..7 | lo 0..7] in xs
 // (block-major, so the 16 token columns of one block sit in distinct banks).
-// A lane owns 8 consecutive values per 512-column pass.  With gvec set, the
-// wave also returns x_row . gvec (FP32, unscaled) in every lane.
-template <int K, bool BF16, bool SPLIT>
-__device__ __forceinline__ float pf_stage(const void* src, int64_t row, int j, _Float16* xh, _Float16* xl,
-                                          _Float16* xs, int* s_exp, const float* gvec) {
-    constexpr int NIT = K >= 512 ? K / 512 : 1, KP = K + PF_PAD;
+// A lane owns 8 consecutive values per 512-column pass.  The loads
+// (pf_stage_load) and the rest (pf_stage_finish) are separate, so that a
+// kernel can issue a tile's token loads ahead of its weight prefetch: vector
+// loads complete in issue order, and staging behind the prefetch would wait
+// for it.
+template <int K, bool BF16>
+struct PfStageRaw {
+    static constexpr int NIT = K >= 512 ? K / 512 : 1;
+    uint4 r[NIT][BF16 ? 1 : 2];
+};
+
+// live = false (a token column past the tile's count): every lane reads the
+// row's first values, one request per instruction instead of a row's worth
+template <int K, bool BF16>
+__device__ __forceinline__ void pf_stage_load(const void* src, int64_t row, bool live, PfStageRaw<K, BF16>& raw) {
     const int lane = threadIdx.x & 63;
-    float v[NIT][8];
+#pragma unroll
+    for (int it = 0; it < PfStageRaw<K, BF16>::NIT; ++it) {
+        // lanes past K (K = 256) read the row's first values again (in bounds, unused)
+        const int c = live ? (512 * it + 8 * lane) % K : 0;
+        if constexpr (BF16) {
+            raw.r[it][0] = *(const uint4*)((const uint16_t*)src + row * K + c);
+        } else {
+            raw.r[it][0] = *(const uint4*)((const float*)src + row * K + c);
+            raw.r[it][1] = *(const uint4*)((const float*)src + row * K + c + 4);
+        }
+    }
+}
+
+// Hands the loaded words through an empty asm statement placed after the
+// weight prefetch: everything computed from them is then ordered after the
+// prefetch (the instruction selector is otherwise free to put the row's
+// arithmetic, and its wait for the row, ahead of the prefetch loads).
+template <int K, bool BF16>
+__device__ __forceinline__ void pf_stage_pin(PfStageRaw<K, BF16>& raw) {
+#pragma unroll
+    for (int it = 0; it < PfStageRaw<K, BF16>::NIT; ++it)
+#pragma unroll
+        for (int j = 0; j < (BF16 ? 1 : 2); ++j)
+            __asm__ volatile("" : "+v"(raw.r[it][j].x), "+v"(raw.r[it][j].y), "+v"(raw.r[it][j].z), "+v"(raw.r[it][j].w));
+}
+
+// The values of pass `it` (8 per lane) from the loaded words; zero past K
+template <int K, bool BF16>
+__device__ __forceinline__ void pf_raw_vals(const PfStageRaw<K, BF16>& raw, int it, int c, float v[8]) {
+    if constexpr (BF16) {
+        const uint32_t w[4] = {raw.r[it][0].x, raw.r[it][0].y, raw.r[it][0].z, raw.r[it][0].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = __uint_as_float(w[e] << 16);
+            v[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+        }
+    } else {
+        const uint4 a = raw.r[it][0], b = raw.r[it][1];
+        v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+        v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y); v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
+    }
+    if (c >= K) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+    }
+}
+
+// The arithmetic runs for a dead column too (live = false), with its LDS
+// writes skipped.  With gvec set, also returns x_row . gvec (FP32, unscaled)
+// in every lane.
+template <int K, bool BF16, bool SPLIT>
+__device__ __forceinline__ float pf_stage_finish(const PfStageRaw<K, BF16>& raw, int j, bool live, _Float16* xh,
+                                                 _Float16* xl, _Float16* xs, int* s_exp, const float* gvec) {
+    constexpr int NIT = PfStageRaw<K, BF16>::NIT, KP = K + PF_PAD;
+    const int lane = threadIdx.x & 63;
     float amax = 0.0f, gdot = 0.0f;
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int c = 512 * it + 8 * lane;
-        if (c < K) {
-            if constexpr (BF16) {
-                const uint4 raw = *(const uint4*)((const uint16_t*)src + row * K + c);
-                const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+        float v[8];
+        pf_raw_vals(raw, it, c, v);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    v[it][2 * e] = __uint_as_float(w[e] << 16);
-                    v[it][2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
-                }
-            } else {
-                const float4 a = *(const float4*)((const float*)src + row * K + c);
-                const float4 b = *(const float4*)((const float*)src + row * K + c + 4);
-                v[it][0] = a.x; v[it][1] = a.y; v[it][2] = a.z; v[it][3] = a.w;
-                v[it][4] = b.x; v[it][5] = b.y; v[it][6] = b.z; v[it][7] = b.w;
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[it][e] = 0.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[it][e]));
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
         if (gvec != nullptr && c < K) {
             const float4 g0 = *(const float4*)(gvec + c), g1 = *(const float4*)(gvec + c + 4);
-            gdot = fmaf(v[it][0], g0.x, gdot); gdot = fmaf(v[it][1], g0.y, gdot);
-            gdot = fmaf(v[it][2], g0.z, gdot); gdot = fmaf(v[it][3], g0.w, gdot);
-            gdot = fmaf(v[it][4], g1.x, gdot); gdot = fmaf(v[it][5], g1.y, gdot);
-            gdot = fmaf(v[it][6], g1.z, gdot); gdot = fmaf(v[it][7], g1.w, gdot);
+            gdot = fmaf(v[0], g0.x, gdot); gdot = fmaf(v[1], g0.y, gdot);
+            gdot = fmaf(v[2], g0.z, gdot); gdot = fmaf(v[3], g0.w, gdot);
+            gdot = fmaf(v[4], g1.x, gdot); gdot = fmaf(v[5], g1.y, gdot);
+            gdot = fmaf(v[6], g1.z, gdot); gdot = fmaf(v[7], g1.w, gdot);
         }
     }
     const int k = frag_exp(pf_wave_max(amax));
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int c = 512 * it + 8 * lane;
+        float v[8];
+        pf_raw_vals(raw, it, c, v);
         h8_t hi, lo;
         float s = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             _Float16 h, l;
-            frag_split(v[it][e], k, h, l);
+            frag_split(v[e], k, h, l);
             hi[e] = h;
             lo[e] = l;
-            s += ldexpf(v[it][e], -k);
+            s += ldexpf(v[e], -k);
         }
         s += __shfl_xor(s, 1, 64);
         s += __shfl_xor(s, 2, 64);
-        if (c < K) {
+        if (live && c < K) {
             *(h8_t*)(xh + j * KP + c) = hi;
             if constexpr (SPLIT) *(h8_t*)(xl + j * KP + c) = lo;
             if ((lane & 3) == 0) {
@@ -164,7 +212,7 @@ __device__ __forceinline__ float pf_stage(const void* src, int64_t row, int j, _
             }
         }
     }
-    if (lane == 0) s_exp[j] = k;
+    if (live && lane == 0) s_exp[j] = k;
     return pf_wave_sum(gdot);
 }
 
@@ -283,7 +331,40 @@ struct PfRows {
     }
 };
 
-__device__ __forceinline__ int4 pf_tile(const PrefillParams& p, int tile) { return ((const int4*)p.tiles)[tile]; }
+// Workgroup -> (tile, row chunk).  Workgroup i runs on XCD i % 8 (the
+// dispatcher deals workgroups to the eight XCDs in turn), so the nch row
+// chunks of one tile are given indices that agree mod 8: the tile's token rows
+// are then fetched into one XCD's L2 and read there by all of its chunks,
+// instead of once per XCD (8 x the token bytes through the fabric).  Launches
+// are 1-D, nch x round_up(max_tiles, 8) workgroups.
+constexpr int PF_XCDS = 8;
+__device__ __forceinline__ void pf_wg(int nch, int& tile, int& chunk) {
+    const int i = blockIdx.x, r = i / PF_XCDS;
+    chunk = r % nch;
+    tile = (r / nch) * PF_XCDS + i % PF_XCDS;
+}
+// The tile's descriptor, when tile is below the launch's tile count: the
+// count and the descriptor are loaded together (every slot below max_tiles
+// exists; past the count it holds stale words, never used).  The test reads
+// the descriptor too (a live tile has at least one pair), so that the compiler
+// cannot move its load behind the branch.
+__device__ __forceinline__ bool pf_live_tile(const int* n_tiles, const int4* tiles, int max_tiles, int tile, int4& td) {
+    const int n = *n_tiles;
+    td = tiles[min(tile, max_tiles - 1)];
+    return (tile < n) & (td.z > 0);
+}
+
+// The GEMM kernels take what their first loads need (the tile list, the token
+// source) as leading scalar arguments, which the build preloads into scalar
+// registers: the first loads need no round trip to the argument block.
+struct PfHot {
+    const int* n_tiles;
+    const int4* tiles;
+    const int* pair_tok;
+    const void* src;   // P1: the tokens x; P2: the activations
+    int max_tiles;
+};
+static int pf_grid(int nch, int max_tiles) { return nch * ((max_tiles + PF_XCDS - 1) / PF_XCDS * PF_XCDS); }
 
 // ------------------------------------------------------------ P0
 
@@ -352,7 +433,9 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
 // ------------------------------------------------------------ P1
 
 template <int GT, int NBH, bool XBF16, int CPW>
-__global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(PrefillParams p) {
+__global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(const int* n_tiles, const int4* tiles,
+                                                                             const int* pair_tok, const void* xsrc,
+                                                                             int max_tiles, int nch, PrefillParams p) {
     constexpr int H = NBH * 256, KP = H + PF_PAD;
     constexpr bool SPLIT = !XBF16;   // BF16 tokens are exact in the high plane
     __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
@@ -360,28 +443,60 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(Pre
     __shared__ __attribute__((aligned(16))) _Float16 xs[PREFILL_TILE * NBH * 16];
     __shared__ __attribute__((aligned(16))) float s_up[PF_WAVES / 2][64][4];
     __shared__ int s_exp[PREFILL_TILE];
-    const int tile = blockIdx.y;
-    if (tile >= *p.n_tiles) return;
-    const int4 td = pf_tile(p, tile);
+    int tile, chunk;
+    pf_wg(nch, tile, chunk);
+    int4 td;
+    const bool live = pf_live_tile(n_tiles, tiles, max_tiles, tile, td);
+    // the argument-block fields the weight addresses need, awaited together
+    // with the tile (each would otherwise be loaded after the branch below)
+    const uint8_t *gate = p.gate, *up = p.up, *sh_gate = p.sh_gate, *sh_up = p.sh_up;
+    const int64_t gate_eb = p.gate_eb, up_eb = p.up_eb;
+    __asm__ volatile("" ::"s"(gate), "s"(up), "s"(sh_gate), "s"(sh_up), "s"(gate_eb), "s"(up_eb), "s"(td.x), "s"(td.y),
+                     "s"(td.z), "s"((int)live));
+    if (!live) return;
     const int e = td.x, first = td.y, cnt = td.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
     // waves 0..3: gate rows, waves 4..7: the same up rows; CPW chunks of 64 rows
-    const int mat = wave / (PF_WAVES / 2), wsub = wave % (PF_WAVES / 2);
-    const int rbase = blockIdx.x * PF_ROWS_GU * CPW + wsub * 16;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int mat = wv / (PF_WAVES / 2), wsub = wv % (PF_WAVES / 2);
+    const int rbase = chunk * PF_ROWS_GU * CPW + wsub * 16;
     const int64_t row_bytes = (int64_t)NBH * block_bytes(GT);
 
+    // (selects of wave-uniform values, no branch: each branch would load its
+    // own arguments after the tile's round trip)
     PfRows<GT, 1, NBH, CPW> g;
-    if (e < 0) g.W[0] = mat ? p.sh_up : p.sh_gate;
-    else g.W[0] = mat ? p.up + (int64_t)e * p.up_eb : p.gate + (int64_t)e * p.gate_eb;
-    g.W[0] += (int64_t)(rbase + (lane & 15)) * row_bytes;
+    const uint8_t* Ws = mat ? sh_up : sh_gate;
+    const uint8_t* Wr = (mat ? up : gate) + (int64_t)max(e, 0) * (mat ? up_eb : gate_eb);
+    g.W[0] = (e < 0 ? Ws : Wr) + (int64_t)(rbase + (lane & 15)) * row_bytes;
     g.chunk_stride = PF_ROWS_GU * row_bytes;
     g.q = q;
+    // the wave's token columns wv and wv + 8 (a column past cnt re-reads the
+    // tile's first token and stages nothing): their loads go out before the
+    // weight prefetch, so the staging below waits for them only
+    static_assert(PREFILL_TILE == 2 * PF_WAVES, "two token columns per wave");
+    const bool l0 = wv < cnt, l1 = wv + PF_WAVES < cnt;
+    // the tile's tokens in one vector load (lane j: column j, clamped to the
+    // last pair), then the wave's two picked out
+    const int pt = pair_tok[first + min(lane & (PREFILL_TILE - 1), cnt - 1)];
+    const int t0 = __builtin_amdgcn_readlane(pt, wv), t1 = __builtin_amdgcn_readlane(pt, wv + PF_WAVES);
+    PfStageRaw<H, XBF16> r0, r1;
+    pf_stage_load<H, XBF16>(xsrc, t0, l0, r0);
+    pf_stage_load<H, XBF16>(xsrc, t1, l1, r1);
+    __builtin_amdgcn_sched_barrier(0);
     g.prefetch();
-    const bool gate_out = e < 0 && blockIdx.x == 0;
-    for (int j = wave; j < cnt; j += PF_WAVES) {
-        const int t = p.pair_tok[first + j];
-        const float gd = pf_stage<H, XBF16, SPLIT>(p.x, t, j, xh, xl, xs, s_exp, gate_out ? p.sh_gate_inp : nullptr);
-        if (gate_out && lane == 0) p.sh_scale[t] = p.sh_gate_inp != nullptr ? pf_sigmoid(gd) : 1.0f;
+    // (a compiler memory barrier: the prefetched values are first used after
+    // the staging's branches, and hipcc would otherwise sink their loads there)
+    __asm__ volatile("" ::: "memory");
+    pf_stage_pin(r0);
+    pf_stage_pin(r1);
+    __builtin_amdgcn_sched_barrier(0);
+    const bool gate_out = e < 0 && chunk == 0;
+    const float* gv = gate_out ? p.sh_gate_inp : nullptr;
+    const float gd0 = pf_stage_finish<H, XBF16, SPLIT>(r0, wv, l0, xh, xl, xs, s_exp, gv);
+    const float gd1 = pf_stage_finish<H, XBF16, SPLIT>(r1, wv + PF_WAVES, l1, xh, xl, xs, s_exp, gv);
+    if (gate_out && lane == 0) {
+        if (l0) p.sh_scale[t0] = p.sh_gate_inp != nullptr ? pf_sigmoid(gd0) : 1.0f;
+        if (l1) p.sh_scale[t1] = p.sh_gate_inp != nullptr ? pf_sigmoid(gd1) : 1.0f;
     }
     __syncthreads();
 
@@ -411,26 +526,40 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(Pre
 // ------------------------------------------------------------ P2
 
 template <int DT, int NBI, int CPW>
-__global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(PrefillParams p) {
+__global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(const int* n_tiles, const int4* tiles,
+                                                                           const int* pair_tok, const void* act,
+                                                                           int max_tiles, int nch, PrefillParams p) {
     constexpr int I = NBI * 256, KP = I + PF_PAD;
     __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
     __shared__ __attribute__((aligned(16))) _Float16 xl[PREFILL_TILE * KP];
     __shared__ __attribute__((aligned(16))) _Float16 xs[PREFILL_TILE * NBI * 16];
     __shared__ int s_exp[PREFILL_TILE];
-    const int tile = blockIdx.y;
-    if (tile >= *p.n_tiles) return;
-    const int4 td = pf_tile(p, tile);
+    int tile, chunk;
+    pf_wg(nch, tile, chunk);
+    int4 td;
+    const bool live = pf_live_tile(n_tiles, tiles, max_tiles, tile, td);
+    const uint8_t *down = p.down, *sh_down = p.sh_down;
+    const int64_t down_eb = p.down_eb;
+    __asm__ volatile("" ::"s"(down), "s"(sh_down), "s"(down_eb), "s"(td.x), "s"(td.y), "s"(td.z), "s"((int)live));
+    if (!live) return;
     const int e = td.x, first = td.y, cnt = td.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
-    const int rbase = blockIdx.x * PF_ROWS_DOWN * CPW + wave * 16;
+    const int rbase = chunk * PF_ROWS_DOWN * CPW + wave * 16;
     const int64_t row_bytes = (int64_t)NBI * block_bytes(DT);
 
     PfRows<DT, 1, NBI, CPW> g;
-    g.W[0] = (e < 0 ? p.sh_down : p.down + (int64_t)e * p.down_eb) + (int64_t)(rbase + (lane & 15)) * row_bytes;
+    g.W[0] = (e < 0 ? sh_down : down + (int64_t)max(e, 0) * down_eb) + (int64_t)(rbase + (lane & 15)) * row_bytes;
     g.chunk_stride = PF_ROWS_DOWN * row_bytes;
     g.q = q;
+    // (here the live activation rows follow the prefetch: issuing the tile's
+    // rows first, as the gate/up kernel does with its tokens, measured 66 ->
+    // 72 us for this kernel at the 128-token prompt)
     g.prefetch();
-    for (int j = wave; j < cnt; j += PF_WAVES) pf_stage<I, false, true>(p.act, first + j, j, xh, xl, xs, s_exp, nullptr);
+    for (int j = wave; j < cnt; j += PF_WAVES) {
+        PfStageRaw<I, false> r;
+        pf_stage_load<I, false>(act, first + j, true, r);
+        pf_stage_finish<I, false, true>(r, j, true, xh, xl, xs, s_exp, nullptr);
+    }
     __syncthreads();
 
     const int col = lane & 15;
@@ -494,10 +623,14 @@ PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden,
 }
 
 // a kernel launch, bracketed by the profiling events when they are armed
-#define PF_LAUNCH(kernel, grid, armed, e0, e1, s, p)                                    \
-    do {                                                                                \
-        if (armed) hipExtLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, e0, e1, 0, p); \
-        else hipLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, p);                      \
+#define PF_LAUNCH(kernel, grid, armed, e0, e1, s, src, nch, p)                                                       \
+    do {                                                                                                      \
+        if (armed)                                                                                            \
+            hipExtLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, e0, e1, 0, (const int*)p.n_tiles,   \
+                                  (const int4*)p.tiles, (const int*)p.pair_tok, (const void*)(src), p.max_tiles, nch, p); \
+        else                                                                                                  \
+            hipLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, (const int*)p.n_tiles,                 \
+                               (const int4*)p.tiles, (const int*)p.pair_tok, (const void*)(src), p.max_tiles, nch, p); \
     } while (0)
 
 // chunks per workgroup: gate/up rows CPW x 64, down rows CPW x 128
@@ -506,9 +639,10 @@ constexpr int pf_cpw_down(int hidden) { return hidden / PF_ROWS_DOWN < PF_CPW_DO
 
 template <int GT, int NBH, int CPW>
 static void launch_p1(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
-    const dim3 grid(p.inter / (PF_ROWS_GU * CPW), p.max_tiles);
-    if (p.x_bf16) PF_LAUNCH((k_prefill_gate_up<GT, NBH, true, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p);
-    else PF_LAUNCH((k_prefill_gate_up<GT, NBH, false, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p);
+    const int nch = p.inter / (PF_ROWS_GU * CPW);
+    const dim3 grid(pf_grid(nch, p.max_tiles));
+    if (p.x_bf16) PF_LAUNCH((k_prefill_gate_up<GT, NBH, true, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p.x, nch, p);
+    else PF_LAUNCH((k_prefill_gate_up<GT, NBH, false, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p.x, nch, p);
 }
 
 template <int GT, int NBH>
@@ -529,8 +663,9 @@ static void launch_p1_h(const PrefillParams& p, hipStream_t s, const KernelEvent
 
 template <int DT, int NBI, int CPW>
 static void launch_p2(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
-    const dim3 grid(p.hidden / (PF_ROWS_DOWN * CPW), p.max_tiles);
-    PF_LAUNCH((k_prefill_down<DT, NBI, CPW>), grid, ev.armed_b(), ev.b_start, ev.b_stop, s, p);
+    const int nch = p.hidden / (PF_ROWS_DOWN * CPW);
+    const dim3 grid(pf_grid(nch, p.max_tiles));
+    PF_LAUNCH((k_prefill_down<DT, NBI, CPW>), grid, ev.armed_b(), ev.b_start, ev.b_stop, s, p.act, nch, p);
 }
 
 template <int DT, int NBI>

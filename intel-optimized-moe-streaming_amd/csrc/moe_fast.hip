@@ -523,19 +523,26 @@ struct SharedB {
 // s = slot s; waves at or past S only join the barriers), combined in top-k
 // order.  down_slot is the calling wave's part (its slot's rows into LDS, with
 // the slot's weight type DT), down_combine the workgroup's.
-template <int DT, int LPR, int NPB_, bool F16G>
+// BAL (balanced, FP32 graph, NPB row groups a wave, a shared expert): the
+// workgroup has one wave per routed slot, and the shared slot's NPB row groups
+// go to waves 0 .. NPB-1, one each, after their own slot.  With eight routed
+// slots and four row groups, waves w and w + 4 (one SIMD) then hold nine row
+// groups between them on every SIMD, where nine waves (one per slot) put three
+// on one SIMD.  SDT is the shared expert's down type.
+template <int DT, int LPR, int NPB_, bool F16G, int SDT = DT, bool BAL = false>
 __device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams& p, int bx, int t,
                                           SharedB<GeoB<LPR, NPB_>::RB>& sh) {
-    constexpr int N = LaneGeo<DT>::NRAW;
-    constexpr int BB = unit_bytes(DT);
+    constexpr int N = LaneGeo<DT>::NRAW, NS = LaneGeo<SDT>::NRAW;
+    constexpr int BB = unit_bytes(DT), BBS = unit_bytes(SDT);
     constexpr int I = 64 * LPR;
     constexpr int RPI = GeoB<LPR, NPB_>::RPI, NPB = GeoB<LPR, NPB_>::NPB, RB = GeoB<LPR, NPB_>::RB;
-    constexpr int64_t ROW_BYTES = (int64_t)(I / 256) * BB;
+    constexpr int64_t ROW_BYTES = (int64_t)(I / 256) * BB, ROW_BYTES_S = (int64_t)(I / 256) * BBS;
+    static_assert(!BAL || !F16G, "the balanced form is the FP32 graph's");
 
     const int lane = threadIdx.x & 63, s = uniform(threadIdx.x >> 6);   // wave = slot (64 * S threads)
     const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
     const int r0 = bx * RB;
-    const bool shared = h.has_shared && s == h.top_k;
+    const bool shared = !BAL && h.has_shared && s == h.top_k;
 
     // the slot's activations first: their address needs no expert id, so the
     // loads go out while the id is still being read
@@ -598,6 +605,29 @@ __device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams
     for (int q = 0; q < NPB; ++q)
         if (li == 0) sh.s_y[s][q * RPI + rr] = bad ? 0.0f : v[q];
     if (lane == 0) sh.s_w[s] = shared ? p.sh_scale[t] : w;
+    if constexpr (BAL) {
+        if (s < NPB) {   // wave-uniform: the shared slot's row group s, from its own copy of the shared digits
+            // (loaded only now: held from the start, these registers keep the
+            // workgroup to one per CU)
+            ActRegs<I> A2;
+            act_load<I>(h.act + ((int64_t)t * h.S + h.top_k) * I, lane, A2);
+            uint32_t raw2[NS];
+            lane_load<SDT>(p.sh_down + (int64_t)(r0 + s * RPI + rr) * ROW_BYTES_S + blk * BBS, k, raw2);
+            int8_t* planes2 = (int8_t*)(b_digits + (h.top_k + s) * act_lds_bytes(I));
+            float* xs2 = (float*)(planes2 + 2 * I);
+            float* sum2 = xs2 + I / RUN;
+            act_digits_lds<I>(A2, lane, planes2, xs2, sum2);
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            DigitsRef xd;
+            xd.planes = planes2; xd.xs16 = xs2; xd.sum16 = sum2; xd.n = I;
+            LaneX X;
+            lane_x<SDT>(xd, blk, k, X);
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            const float v2 = lane_group_sum<LPR>(lane_dot<SDT>(raw2, k, X));
+            if (li == 0) sh.s_y[h.top_k][s * RPI + rr] = v2;
+            if (lane == 0 && s == 0) sh.s_w[h.top_k] = p.sh_scale[t];
+        }
+    }
 }
 
 template <int LPR, int NPB_>
@@ -629,6 +659,17 @@ __global__ __launch_bounds__(1024) void k_fast_down(const int32_t* ids, float* a
     } else {
         down_slot<DT, LPR, NPB, F16G>(h, p, blockIdx.x, blockIdx.y, sh);
     }
+    down_combine<LPR, NPB>(h, p, blockIdx.x, blockIdx.y, sh);
+}
+
+// The balanced form (down_slot BAL): one wave per routed slot, at most 8,
+// with the register budget of two such workgroups per CU (four waves a SIMD).
+template <int DT, int SDT, int LPR, int NPB>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_fast_down_bal(const int32_t* ids, float* act, const float* weights, int top_k,
+                                                      int S, int has_shared, int n_experts, DecodeParams p) {
+    __shared__ SharedB<GeoB<LPR, NPB>::RB> sh;
+    const DecodeHot h{nullptr, ids, act, weights, nullptr, top_k, S, has_shared, n_experts, 0, 0};
+    down_slot<DT, LPR, NPB, false, SDT, true>(h, p, blockIdx.x, blockIdx.y, sh);
     down_combine<LPR, NPB>(h, p, blockIdx.x, blockIdx.y, sh);
 }
 
@@ -761,6 +802,21 @@ static void launch_a_t(const DecodeParams& p, hipStream_t stream, const KernelEv
 template <int DT, int SDT, int LPR, int NPB, bool F16G>
 static void launch_b_n(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
     dim3 grid(p.hidden / GeoB<LPR, NPB>::RB, p.n_tokens);
+    if constexpr (!F16G && NPB >= 2) {
+        if (p.has_shared && p.top_k >= NPB && p.top_k <= 8 &&
+            (int64_t)(p.top_k + NPB) * act_lds_bytes(64 * LPR) <= 65536 - 4096) {   // one wave per routed slot,
+                                                                                    // shared rows to waves 0 .. NPB-1
+            const size_t lds = (size_t)(p.top_k + NPB) * act_lds_bytes(64 * LPR);
+            if (ev.armed_b())
+                hipExtLaunchKernelGGL((k_fast_down_bal<DT, SDT, LPR, NPB>), grid, dim3(64 * p.top_k), lds, stream,
+                                      ev.b_start, ev.b_stop, 0, p.ids, p.act, p.weights, p.top_k, p.S, p.has_shared,
+                                      p.n_experts, p);
+            else
+                hipLaunchKernelGGL((k_fast_down_bal<DT, SDT, LPR, NPB>), grid, dim3(64 * p.top_k), lds, stream, p.ids,
+                                   p.act, p.weights, p.top_k, p.S, p.has_shared, p.n_experts, p);
+            return;
+        }
+    }
     const size_t lds = (size_t)p.S * act_lds_bytes(64 * LPR);   // the slots' digits
     if (ev.armed_b())
         hipExtLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB, F16G>), grid, dim3(64 * p.S), lds, stream, ev.b_start,

@@ -430,6 +430,18 @@ __host__ __device__ inline void pack16_bytes(const uint32_t* q, uint32_t* out, F
         out[2 * i + 1] = pack_rn16(f(b2), f(b3));
     }
 }
+// w[j] = s * (signed byte j of the 4 dwords at w) for 16 bytes, packed as FP16
+// pairs into out[0..7] (one sign-extending byte conversion and one product a
+// weight)
+__host__ __device__ inline void pack16_sbytes(const uint32_t* w, float s, uint32_t* out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float b0 = (float)(int8_t)(w[i] & 0xFFu), b1 = (float)(int8_t)((w[i] >> 8) & 0xFFu);
+        const float b2 = (float)(int8_t)((w[i] >> 16) & 0xFFu), b3 = (float)(int8_t)(w[i] >> 24);
+        out[2 * i] = pack_rn16(mul_rn(s, b0), mul_rn(s, b1));
+        out[2 * i + 1] = pack_rn16(mul_rn(s, b2), mul_rn(s, b3));
+    }
+}
 }  // namespace detail
 
 // Piece P (0..3, 16 weights) of lane k's 64 weights as FP16 pairs, in run
@@ -465,26 +477,31 @@ __host__ __device__ inline void lane_w16_piece(const uint32_t* raw, int k, uint3
         }
         detail::pack16_bytes(q, out, [&](float b) { return detail::sub_rn(detail::mul_rn(d1, b), m1); });
     } else if constexpr (T == T_Q6_K) {
+        // q - 32 for the 6-bit u: its two's complement is u ^ 32 in bits 2..7 of a
+        // byte (low nibble rotated to bits 2..5, the two high bits to 6..7, the
+        // top bit flipped), i.e. the int8 4 (u - 32); times RN(d sc) / 4 (exact)
+        // that is RN(d sc (u - 32)), the reference decoder's product
         constexpr int r = P / 2, p = P % 2;
         const float d = f16_bits_to_f32(raw[18] & 0xFFFFu);
-        const int s = (k & 1) + 2 * r, rq = (2 * s - 4) & 31;
-        uint32_t q[4];
+        const int s = (k & 1) + 2 * r, ra = (4 * r + 30) & 31, rb = (2 * s + 26) & 31;
+        uint32_t w[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            q[i] = ((raw[4 * p + i] >> (4 * r)) & 0x0F0F0F0Fu) | (rotr(raw[8 + 4 * p + i], rq) & 0x30303030u);
+            w[i] = ((rotr(raw[4 * p + i], ra) & 0x3C3C3C3Cu) | (rotr(raw[8 + 4 * p + i], rb) & 0xC0C0C0C0u)) ^ 0x80808080u;
         const int sb = 2 * s + p;
         const int sc = (int)(int8_t)(uint8_t)((sb < 4 ? raw[16] >> (8 * sb) : raw[17] >> (8 * (sb - 4))) & 0xFFu);
-        const float ds = detail::mul_rn(d, (float)sc);
-        detail::pack16_bytes(q, out, [&](float b) { return detail::mul_rn(ds, b - 32.0f); });
+        detail::pack16_sbytes(w, detail::mul_rn(d, (float)sc) * 0.25f, out);
     } else {  // Q3_K: piece P is run s = P
+        // q - 4 = low2 - 4 (1 - hbit): the two low bits rotated to bits 5..6 and
+        // the inverted mask bit to bit 7 make the int8 32 (q - 4); times
+        // RN(d sc) / 32 (exact) that is RN(d sc (q - 4))
         const float d = f16_bits_to_f32(raw[11] & 0xFFFFu);
         const int h = k >> 1, odd = k & 1, sh = 8 * odd + 4 * h;
-        const int r = (4 * h + P - 2) & 31;
-        uint32_t q[4];
+        const int ra = (2 * P + 27) & 31, rb = (4 * h + P + 25) & 31;
+        uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q[i] = ((raw[4 + i] >> (2 * P)) & 0x03030303u) | (rotr(raw[i], r) & 0x04040404u);
-        const float ds = detail::mul_rn(d, (float)k3_scale_run(raw + 8, sh, P));
-        detail::pack16_bytes(q, out, [&](float b) { return detail::mul_rn(ds, b - 4.0f); });
+        for (int i = 0; i < 4; ++i) w[i] = (rotr(raw[4 + i], ra) & 0x60606060u) | (~rotr(raw[i], rb) & 0x80808080u);
+        detail::pack16_sbytes(w, detail::mul_rn(d, (float)k3_scale_run(raw + 8, sh, P)) * 0.03125f, out);
     }
 }
 

@@ -451,3 +451,47 @@ def test_fp16_graph_fast_kernels(hip, oracle_mod, types):
                 err = oracle_mod.max_relative_error(got[path][tok], want[tok])
                 assert err <= 5e-3, (types, H, I, path, tok, err)
         assert oracle_mod.max_relative_error(got[0], got[1]) <= 5e-3
+
+
+@pytest.mark.parametrize("T,k,sh", [(8, 4, "same"), (8, 8, "q6k"), (16, 8, "same"), (16, 4, "q6k"), (16, 2, "same"),
+                                    (12, 3, "same")])
+def test_balanced_down_kernel(hip, oracle_mod, T, k, sh):
+    """Many tokens with a shared expert (hidden 2048, intermediate 512): the down
+    kernel gives each wave two (T >= 8) or four (T >= 16) row groups and, when
+    top_k is at least that, deals the shared expert's row groups to the first
+    waves (k = 2 at T = 16 keeps one wave per slot; k = 3 at T = 12 gives
+    waves 0-1 the shared rows).  Every token against the oracle and the generic
+    kernels."""
+    H, I, E = 2048, 512, 32
+    t = {"gate": 11, "up": 11, "down": 11}
+    st = t if sh == "same" else {"gate": 14, "up": 14, "down": 14}
+    layer, host, shared = make_layer(900 + T + k, E, H, I, t, shared_types=st)
+    rng = np.random.default_rng(T * 10 + k)
+    X = rng.standard_normal((T, H)).astype(np.float32)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    ws = rng.dirichlet(np.ones(k), size=T).astype(np.float32)
+    print(f"balanced down T={T} k={k} shared={sh}", flush=True)
+    old = hip.mqh_set_decode_path(0)
+    try:
+        got, s0 = run(layer, X, ids, ws)
+        hip.mqh_set_decode_path(1)
+        gen, s1 = run(layer, X, ids, ws)
+    finally:
+        hip.mqh_set_decode_path(old)
+    assert s0 == 0 and s1 == 0
+    for tok in range(T):
+        want = oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist())
+        # the integer-digit kernels' activation error (<= 1.6e-5 of a 16-column
+        # run's max per value) reaches ~1e-4 of the output on these Q3_K layers
+        assert oracle_mod.max_relative_error(got[tok], want) <= 2e-4, (T, k, sh, tok)
+        assert oracle_mod.max_relative_error(got[tok], gen[tok]) <= TOL, (T, k, sh, tok)
+    # a token's result does not depend on the batch it came in: the first and
+    # last tokens alone (one wave per slot, one row group a wave) give the same bits
+    old = hip.mqh_set_decode_path(0)
+    try:
+        for tok in (0, T - 1):
+            one, s2 = run(layer, X[tok:tok + 1], ids[tok:tok + 1], ws[tok:tok + 1])
+            assert s2 == 0
+            assert np.array_equal(one[0].view(np.uint32), got[tok].view(np.uint32)), (T, k, sh, tok)
+    finally:
+        hip.mqh_set_decode_path(old)

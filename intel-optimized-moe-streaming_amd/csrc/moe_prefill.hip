@@ -337,12 +337,13 @@ struct PfRows {
 // chunks of one tile are given indices that agree mod 8: the tile's token rows
 // are then fetched into one XCD's L2 and read there by all of its chunks,
 // instead of once per XCD (8 x the token bytes through the fabric).  Launches
-// are 1-D, nch x round_up(max_tiles, 8) workgroups.
+// are 1-D, nch x round_up(max_tiles, 8) workgroups; nch is a power of two (its
+// log2 comes in: a division would sit ahead of the first loads).
 constexpr int PF_XCDS = 8;
-__device__ __forceinline__ void pf_wg(int nch, int& tile, int& chunk) {
+__device__ __forceinline__ void pf_wg(int nch_log2, int& tile, int& chunk) {
     const int i = blockIdx.x, r = i / PF_XCDS;
-    chunk = r % nch;
-    tile = (r / nch) * PF_XCDS + i % PF_XCDS;
+    chunk = r & ((1 << nch_log2) - 1);
+    tile = (r >> nch_log2) * PF_XCDS + i % PF_XCDS;
 }
 // The tile's descriptor, when tile is below the launch's tile count: the
 // count and the descriptor are loaded together (every slot below max_tiles
@@ -436,7 +437,7 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
 template <int GT, int NBH, bool XBF16, int CPW>
 __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(const int* n_tiles, const int4* tiles,
                                                                              const int* pair_tok, const void* xsrc,
-                                                                             int max_tiles, int nch, PrefillParams p) {
+                                                                             int max_tiles, int nch_log2, PrefillParams p) {
     constexpr int H = NBH * 256, KP = H + PF_PAD;
     constexpr bool SPLIT = !XBF16;   // BF16 tokens are exact in the high plane
     __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     __shared__ __attribute__((aligned(16))) float s_up[PF_WAVES / 2][64][4];
     __shared__ int s_exp[PREFILL_TILE];
     int tile, chunk;
-    pf_wg(nch, tile, chunk);
+    pf_wg(nch_log2, tile, chunk);
     int4 td;
     const bool live = pf_live_tile(n_tiles, tiles, max_tiles, tile, td);
     // the argument-block fields the weight addresses need, awaited together
@@ -529,14 +530,14 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
 template <int DT, int NBI, int CPW>
 __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(const int* n_tiles, const int4* tiles,
                                                                            const int* pair_tok, const void* act,
-                                                                           int max_tiles, int nch, PrefillParams p) {
+                                                                           int max_tiles, int nch_log2, PrefillParams p) {
     constexpr int I = NBI * 256, KP = I + PF_PAD;
     __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
     __shared__ __attribute__((aligned(16))) _Float16 xl[PREFILL_TILE * KP];
     __shared__ __attribute__((aligned(16))) _Float16 xs[PREFILL_TILE * NBI * 16];
     __shared__ int s_exp[PREFILL_TILE];
     int tile, chunk;
-    pf_wg(nch, tile, chunk);
+    pf_wg(nch_log2, tile, chunk);
     int4 td;
     const bool live = pf_live_tile(n_tiles, tiles, max_tiles, tile, td);
     const uint8_t *down = p.down, *sh_down = p.sh_down;
@@ -628,10 +629,10 @@ PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden,
     do {                                                                                                      \
         if (armed)                                                                                            \
             hipExtLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, e0, e1, 0, (const int*)p.n_tiles,   \
-                                  (const int4*)p.tiles, (const int*)p.pair_tok, (const void*)(src), p.max_tiles, nch, p); \
+                                  (const int4*)p.tiles, (const int*)p.pair_tok, (const void*)(src), p.max_tiles, __builtin_ctz(nch), p); \
         else                                                                                                  \
             hipLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, (const int*)p.n_tiles,                 \
-                               (const int4*)p.tiles, (const int*)p.pair_tok, (const void*)(src), p.max_tiles, nch, p); \
+                               (const int4*)p.tiles, (const int*)p.pair_tok, (const void*)(src), p.max_tiles, __builtin_ctz(nch), p); \
     } while (0)
 
 // chunks per workgroup: gate/up rows CPW x 64, down rows CPW x 128

@@ -57,14 +57,17 @@ __global__ __launch_bounds__(64) void k_delta_heads(float* __restrict__ state, c
                                                     const float* __restrict__ k, const float* __restrict__ v,
                                                     const float* __restrict__ beta, const float* __restrict__ gate,
                                                     float* __restrict__ out, int heads, int key_dim, int value_dim,
-                                                    int* __restrict__ flags) {
+                                                    unsigned vd_magic, int* __restrict__ flags) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, l = lane & 7;
     const int n_rows = heads * value_dim;
     const int R0 = blockIdx.x * 8 + (lane >> 3);
     const bool live = R0 < n_rows;
     const int R = live ? R0 : n_rows - 1;   // a row past the end computes the last row and stores nothing
-    const int h = R / value_dim;
+    // R / value_dim as one multiply-high (vd_magic = ceil(2^32 / value_dim), 0 for
+    // value_dim 1): exact while R * (vd_magic * value_dim - 2^32) < 2^32, which
+    // R < 2^18 and value_dim <= 1024 guarantee
+    const int h = vd_magic ? (int)__umulhi((unsigned)R, vd_magic) : R;
     float* row = state + (int64_t)R * key_dim;
     const float* kh = k + (int64_t)h * key_dim;
     const float* qh = q + (int64_t)h * key_dim;
@@ -154,12 +157,15 @@ static void launch_delta_nb(float* state, const float* q, const float* k, const 
                             hipStream_t stream, const KernelEvents& ev) {
     const int64_t n_rows = (int64_t)heads * value_dim;
     const dim3 grid((unsigned)((n_rows + 7) / 8));
+    // heads <= 256 and value_dim <= 1024 (the entry points' limits) keep the
+    // kernel's multiply-high division exact
+    const unsigned vd_magic = value_dim > 1 ? (unsigned)((0x100000000ull + value_dim - 1) / value_dim) : 0u;
     if (ev.armed_a())
         hipExtLaunchKernelGGL((k_delta_heads<NB>), grid, dim3(64), 0, stream, ev.a_start, ev.a_stop, 0, state, q, k,
-                              v, beta, gate, out, heads, key_dim, value_dim, flags);
+                              v, beta, gate, out, heads, key_dim, value_dim, vd_magic, flags);
     else
         hipLaunchKernelGGL((k_delta_heads<NB>), grid, dim3(64), 0, stream, state, q, k, v, beta, gate, out, heads,
-                           key_dim, value_dim, flags);
+                           key_dim, value_dim, vd_magic, flags);
 }
 
 hipError_t launch_delta_heads(float* state, const float* q, const float* k, const float* v, const float* beta,

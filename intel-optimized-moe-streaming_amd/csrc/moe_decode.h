@@ -116,11 +116,20 @@ struct PrefillParams {
     int* pos;               // [n_tokens x S]: sorted pair index of (token, slot)
     float* act;             // [P x inter] SwiGLU activations
     float* ypair;           // [P x hidden] expert outputs per pair
+    // the tokens as the gate/up kernel's B operand, made once per token by the
+    // route pass: FP16 high and low planes [n_tokens x hidden] at scale 2^-k,
+    // the 32-column sub-block sums [n_tokens x hidden / 32] as (high, low)
+    // FP16 pairs, and k [n_tokens]
+    uint16_t* xhi;
+    uint16_t* xlo;
+    uint32_t* xsum;
+    int* xexp;
     int max_tiles;
 };
 
 struct PrefillLayout {
-    int64_t flags_off, scale_off, tiles_off, ntiles_off, pair_off, pos_off, act_off, ypair_off, total;
+    int64_t flags_off, scale_off, tiles_off, ntiles_off, pair_off, pos_off, act_off, ypair_off;
+    int64_t xhi_off, xlo_off, xsum_off, xexp_off, total;
     int max_tiles;
 };
 

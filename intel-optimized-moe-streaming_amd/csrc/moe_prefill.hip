@@ -8,18 +8,20 @@
 //   y[t] = sum_s w[t,s] * Y_{ids[t,s]}[t]  (top-k order)  + sigmoid(x_t . g_inp) * shared(x_t)
 //
 // Four launches, no inter-workgroup synchronisation:
-//   P0 k_prefill_route     one workgroup: buckets the (token, slot) pairs by expert
-//                          and cuts each expert's tokens into tiles of 16.
+//   P0 k_prefill_route     workgroup 0 buckets the (token, slot) pairs by expert and
+//                          cuts each expert's tokens into tiles of 16; the others
+//                          stage every token once as the B operand (token planes)
+//                          and the shared expert's sigmoid gate.
 //   P1 k_prefill_gate_up   (I/64) x max_tiles workgroups: 64 intermediate rows x one tile,
-//                          SwiGLU fused; the shared expert's tiles also produce its
-//                          sigmoid gate.
+//                          SwiGLU fused.
 //   P2 k_prefill_down      (H/128) x max_tiles workgroups: 128 output rows x one tile.
 //   P3 k_prefill_combine   grid (H/256, T): the weighted sum in top-k order.
 //
 // P1/P2 are MFMA GEMMs (v_mfma_f32_16x16x32_f16, FP32 accumulate) whose weight
 // operand is built in registers straight from the quantized blocks as exact
-// integers (kquant_frag.h); the tile's tokens are the other operand, staged
-// once per workgroup in LDS as FP16 planes with a power-of-two scale per token.
+// integers (kquant_frag.h); the tile's tokens are the other operand, FP16
+// planes with a power-of-two scale per token, in LDS (P1 copies the planes P0
+// made; P2 stages its activation rows itself).
 #include <hip/hip_ext.h>
 
 #include <utility>
@@ -97,10 +99,8 @@ __device__ __forceinline__ float pf_wave_sum(float v) {
 // and the 32-column sub-block sums / 32 as [block][j][hi 0..7 | lo 0..7] in xs
 // (block-major, so the 16 token columns of one block sit in distinct banks).
 // A lane owns 8 consecutive values per 512-column pass.  The loads
-// (pf_stage_load) and the rest (pf_stage_finish) are separate, so that a
-// kernel can issue a tile's token loads ahead of its weight prefetch: vector
-// loads complete in issue order, and staging behind the prefetch would wait
-// for it.
+// (pf_stage_load) and the rest (pf_stage_finish, or pf_stage_planes into
+// device memory) are separate.
 template <int K, bool BF16>
 struct PfStageRaw {
     static constexpr int NIT = K >= 512 ? K / 512 : 1;
@@ -159,13 +159,11 @@ __device__ __forceinline__ void pf_raw_vals(const PfStageRaw<K, BF16>& raw, int 
     }
 }
 
-// The arithmetic runs for a dead column too (live = false), with its LDS
-// writes skipped.  With gvec set, also returns x_row . gvec (FP32, unscaled)
-// in every lane.
-template <int K, bool BF16, bool SPLIT>
-__device__ __forceinline__ float pf_stage_finish(const PfStageRaw<K, BF16>& raw, int j, bool live, _Float16* xh,
-                                                 _Float16* xl, _Float16* xs, int* s_exp, const float* gvec) {
-    constexpr int NIT = PfStageRaw<K, BF16>::NIT, KP = K + PF_PAD;
+// The row's scale exponent k (its max |value| to [2^13, 2^14), frag_exp); with
+// gvec set, also x_row . gvec (FP32, unscaled) in every lane, else 0.
+template <int K, bool BF16>
+__device__ __forceinline__ int pf_row_exp(const PfStageRaw<K, BF16>& raw, const float* gvec, float& gdot_out) {
+    constexpr int NIT = PfStageRaw<K, BF16>::NIT;
     const int lane = threadIdx.x & 63;
     float amax = 0.0f, gdot = 0.0f;
 #pragma unroll
@@ -183,38 +181,148 @@ __device__ __forceinline__ float pf_stage_finish(const PfStageRaw<K, BF16>& raw,
             gdot = fmaf(v[6], g1.z, gdot); gdot = fmaf(v[7], g1.w, gdot);
         }
     }
-    const int k = frag_exp(pf_wave_max(amax));
+    gdot_out = pf_wave_sum(gdot);
+    return frag_exp(pf_wave_max(amax));
+}
+
+// Pass `it` of the row at scale 2^-k: the lane's 8 values as FP16 high and low
+// parts, and the sum of its 32-column sub-block (the same in lanes 4m .. 4m+3)
+// as an FP16 (high, low) pair.
+template <int K, bool BF16>
+__device__ __forceinline__ void pf_split_pass(const PfStageRaw<K, BF16>& raw, int it, int k, h8_t& hi, h8_t& lo,
+                                              _Float16& sh, _Float16& sl) {
+    const int c = 512 * it + 8 * (threadIdx.x & 63);
+    float v[8];
+    pf_raw_vals(raw, it, c, v);
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        _Float16 h, l;
+        frag_split(v[e], k, h, l);
+        hi[e] = h;
+        lo[e] = l;
+        s += ldexpf(v[e], -k);
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    frag_split(s, 5, sh, sl);
+}
+
+// Stages the row as LDS column j; the arithmetic runs for a dead column too
+// (live = false), with its LDS writes skipped.
+template <int K, bool BF16, bool SPLIT>
+__device__ __forceinline__ void pf_stage_finish(const PfStageRaw<K, BF16>& raw, int j, bool live, _Float16* xh,
+                                                _Float16* xl, _Float16* xs, int* s_exp) {
+    constexpr int NIT = PfStageRaw<K, BF16>::NIT, KP = K + PF_PAD;
+    const int lane = threadIdx.x & 63;
+    float unused;
+    const int k = pf_row_exp(raw, nullptr, unused);
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int c = 512 * it + 8 * lane;
-        float v[8];
-        pf_raw_vals(raw, it, c, v);
         h8_t hi, lo;
-        float s = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            _Float16 h, l;
-            frag_split(v[e], k, h, l);
-            hi[e] = h;
-            lo[e] = l;
-            s += ldexpf(v[e], -k);
-        }
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
+        _Float16 sh, sl;
+        pf_split_pass(raw, it, k, hi, lo, sh, sl);
         if (live && c < K) {
             *(h8_t*)(xh + j * KP + c) = hi;
             if constexpr (SPLIT) *(h8_t*)(xl + j * KP + c) = lo;
             if ((lane & 3) == 0) {
                 const int sb = c >> 5;   // sub-block: block sb / 8, slot sb % 8
-                _Float16 h, l;
-                frag_split(s, 5, h, l);
-                xs[((sb >> 3) * PREFILL_TILE + j) * 16 + (sb & 7)] = h;
-                xs[((sb >> 3) * PREFILL_TILE + j) * 16 + 8 + (sb & 7)] = l;
+                xs[((sb >> 3) * PREFILL_TILE + j) * 16 + (sb & 7)] = sh;
+                xs[((sb >> 3) * PREFILL_TILE + j) * 16 + 8 + (sb & 7)] = sl;
             }
         }
     }
     if (live && lane == 0) s_exp[j] = k;
-    return pf_wave_sum(gdot);
+}
+
+// The same staging of token t into the token planes in device memory (the
+// route pass makes them once per token; every gate/up workgroup of the token's
+// tiles then copies them into LDS with no arithmetic).  Returns x_t . gvec.
+template <int K, bool BF16, bool SPLIT>
+__device__ __forceinline__ float pf_stage_planes(const PfStageRaw<K, BF16>& raw, int64_t t, const PrefillParams& p,
+                                                 const float* gvec) {
+    constexpr int NIT = PfStageRaw<K, BF16>::NIT;
+    const int lane = threadIdx.x & 63;
+    float gdot;
+    const int k = pf_row_exp(raw, gvec, gdot);
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int c = 512 * it + 8 * lane;
+        h8_t hi, lo;
+        _Float16 sh, sl;
+        pf_split_pass(raw, it, k, hi, lo, sh, sl);
+        if (c < K) {
+            *(h8_t*)((_Float16*)p.xhi + t * K + c) = hi;
+            if constexpr (SPLIT) *(h8_t*)((_Float16*)p.xlo + t * K + c) = lo;
+            if ((lane & 3) == 0)
+                p.xsum[t * (K / 32) + (c >> 5)] =
+                    (uint32_t)__builtin_bit_cast(uint16_t, sh) | (uint32_t)__builtin_bit_cast(uint16_t, sl) << 16;
+        }
+    }
+    if (lane == 0) p.xexp[t] = k;
+    return gdot;
+}
+
+// A token column of the gate/up kernel's B operand as the route pass left it:
+// the lane's 8 columns per 512-column pass of the high (and low) plane, the
+// lane's sub-block sum pair (lanes below K / 32) and the exponent.
+template <int K, bool SPLIT>
+struct PfPlanes {
+    static constexpr int NIT = K >= 512 ? K / 512 : 1;
+    uint4 h[NIT];
+    uint4 l[SPLIT ? NIT : 1];
+    uint32_t s;
+    int e;
+};
+
+// live = false: every lane reads the row's first words (in bounds, unused)
+template <int K, bool SPLIT>
+__device__ __forceinline__ void pf_planes_load(const uint16_t* xhi, const uint16_t* xlo, const uint32_t* xsum,
+                                               const int* xexp, int64_t t, bool live, PfPlanes<K, SPLIT>& r) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int it = 0; it < PfPlanes<K, SPLIT>::NIT; ++it) {
+        // lanes past K (K = 256) read the row's first columns again
+        const int c = live ? (512 * it + 8 * lane) % K : 0;
+        r.h[it] = *(const uint4*)(xhi + t * K + c);
+        if constexpr (SPLIT) r.l[it] = *(const uint4*)(xlo + t * K + c);
+    }
+    r.s = xsum[t * (K / 32) + (live ? min(lane, K / 32 - 1) : 0)];
+    r.e = xexp[t];
+}
+
+template <int K, bool SPLIT>
+__device__ __forceinline__ void pf_planes_pin(PfPlanes<K, SPLIT>& r) {
+#pragma unroll
+    for (int it = 0; it < PfPlanes<K, SPLIT>::NIT; ++it) {
+        __asm__ volatile("" : "+v"(r.h[it].x), "+v"(r.h[it].y), "+v"(r.h[it].z), "+v"(r.h[it].w));
+        if constexpr (SPLIT) __asm__ volatile("" : "+v"(r.l[it].x), "+v"(r.l[it].y), "+v"(r.l[it].z), "+v"(r.l[it].w));
+    }
+    __asm__ volatile("" : "+v"(r.s), "+v"(r.e));
+}
+
+// The column's LDS copy (the layout pf_stage_finish writes)
+template <int K, bool SPLIT>
+__device__ __forceinline__ void pf_planes_store(const PfPlanes<K, SPLIT>& r, int j, bool live, _Float16* xh,
+                                                _Float16* xl, _Float16* xs, int* s_exp) {
+    constexpr int KP = K + PF_PAD;
+    const int lane = threadIdx.x & 63;
+    if (!live) return;
+#pragma unroll
+    for (int it = 0; it < PfPlanes<K, SPLIT>::NIT; ++it) {
+        const int c = 512 * it + 8 * lane;
+        if (c < K) {
+            *(uint4*)(xh + j * KP + c) = r.h[it];
+            if constexpr (SPLIT) *(uint4*)(xl + j * KP + c) = r.l[it];
+        }
+    }
+    if (lane < K / 32) {
+        const int sb = lane;
+        xs[((sb >> 3) * PREFILL_TILE + j) * 16 + (sb & 7)] = __builtin_bit_cast(_Float16, (uint16_t)(r.s & 0xFFFFu));
+        xs[((sb >> 3) * PREFILL_TILE + j) * 16 + 8 + (sb & 7)] = __builtin_bit_cast(_Float16, (uint16_t)(r.s >> 16));
+    }
+    if (lane == 0) s_exp[j] = r.e;
 }
 
 // ------------------------------------------------------------ the GEMM core
@@ -372,11 +480,30 @@ static int pf_grid(int nch, int max_tiles) { return nch * ((max_tiles + PF_XCDS 
 
 constexpr int PF_ROUTE_THREADS = 1024;   // one workgroup (a constant: blockDim.x costs a memory round trip)
 
+// Tokens a staging workgroup takes: one wave each on waves 0..3 (one a SIMD;
+// sixteen a workgroup measured 1.2 us longer for the route pass at 128 tokens)
+constexpr int PF_STAGE_TOKENS = 4;
+
+// Workgroup 0 routes; workgroup b > 0 stages tokens 4 (b - 1) .. 4 b - 1 into
+// the token planes, one wave a token, and sets the shared expert's gate per
+// token (sigmoid(x . g_inp), shared_expert.py:221-251).
+template <int NBH, bool XBF16>
 __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParams p) {
     __shared__ int cnt[PREFILL_MAX_EXPERTS], off[PREFILL_MAX_EXPERTS], fill[PREFILL_MAX_EXPERTS];
     __shared__ int wsum[16][2];
     const int T = p.n_tokens, K = p.top_k, E = p.n_experts, TK = T * K;
     const int e = threadIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (blockIdx.x > 0) {
+        constexpr int H = NBH * 256;
+        const int t = (blockIdx.x - 1) * PF_STAGE_TOKENS + wave;
+        if (wave >= PF_STAGE_TOKENS || t >= T) return;
+        PfStageRaw<H, XBF16> r;
+        pf_stage_load<H, XBF16>(p.x, t, true, r);
+        const float* gv = p.has_shared ? p.sh_gate_inp : nullptr;
+        const float gd = pf_stage_planes<H, XBF16, !XBF16>(r, t, p, gv);
+        if (p.has_shared && lane == 0) p.sh_scale[t] = gv != nullptr ? pf_sigmoid(gd) : 1.0f;
+        return;
+    }
     if (e < E) { cnt[e] = 0; fill[e] = 0; }
     __syncthreads();
     for (int i = threadIdx.x; i < TK; i += PF_ROUTE_THREADS) {
@@ -453,8 +580,11 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     // with the tile (each would otherwise be loaded after the branch below)
     const uint8_t *gate = p.gate, *up = p.up, *sh_gate = p.sh_gate, *sh_up = p.sh_up;
     const int64_t gate_eb = p.gate_eb, up_eb = p.up_eb;
-    __asm__ volatile("" ::"s"(gate), "s"(up), "s"(sh_gate), "s"(sh_up), "s"(gate_eb), "s"(up_eb), "s"(td.x), "s"(td.y),
-                     "s"(td.z), "s"((int)live));
+    const uint16_t *xhi = (const uint16_t*)xsrc, *xlo = p.xlo;
+    const uint32_t* xsum = p.xsum;
+    const int* xexp = p.xexp;
+    __asm__ volatile("" ::"s"(gate), "s"(up), "s"(sh_gate), "s"(sh_up), "s"(gate_eb), "s"(up_eb), "s"(xlo), "s"(xsum),
+                     "s"(xexp), "s"(td.x), "s"(td.y), "s"(td.z), "s"((int)live));
     if (!live) return;
     const int e = td.x, first = td.y, cnt = td.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
@@ -481,25 +611,19 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     // last pair), then the wave's two picked out
     const int pt = pair_tok[first + min(lane & (PREFILL_TILE - 1), cnt - 1)];
     const int t0 = __builtin_amdgcn_readlane(pt, wv), t1 = __builtin_amdgcn_readlane(pt, wv + PF_WAVES);
-    PfStageRaw<H, XBF16> r0, r1;
-    pf_stage_load<H, XBF16>(xsrc, t0, l0, r0);
-    pf_stage_load<H, XBF16>(xsrc, t1, l1, r1);
+    PfPlanes<H, SPLIT> r0, r1;
+    pf_planes_load<H, SPLIT>(xhi, xlo, xsum, xexp, t0, l0, r0);
+    pf_planes_load<H, SPLIT>(xhi, xlo, xsum, xexp, t1, l1, r1);
     __builtin_amdgcn_sched_barrier(0);
     g.prefetch();
     // (a compiler memory barrier: the prefetched values are first used after
     // the staging's branches, and hipcc would otherwise sink their loads there)
     __asm__ volatile("" ::: "memory");
-    pf_stage_pin(r0);
-    pf_stage_pin(r1);
+    pf_planes_pin(r0);
+    pf_planes_pin(r1);
     __builtin_amdgcn_sched_barrier(0);
-    const bool gate_out = e < 0 && chunk == 0;
-    const float* gv = gate_out ? p.sh_gate_inp : nullptr;
-    const float gd0 = pf_stage_finish<H, XBF16, SPLIT>(r0, wv, l0, xh, xl, xs, s_exp, gv);
-    const float gd1 = pf_stage_finish<H, XBF16, SPLIT>(r1, wv + PF_WAVES, l1, xh, xl, xs, s_exp, gv);
-    if (gate_out && lane == 0) {
-        if (l0) p.sh_scale[t0] = p.sh_gate_inp != nullptr ? pf_sigmoid(gd0) : 1.0f;
-        if (l1) p.sh_scale[t1] = p.sh_gate_inp != nullptr ? pf_sigmoid(gd1) : 1.0f;
-    }
+    pf_planes_store(r0, wv, l0, xh, xl, xs, s_exp);
+    pf_planes_store(r1, wv + PF_WAVES, l1, xh, xl, xs, s_exp);
     __syncthreads();
 
     const int col = lane & 15;
@@ -560,7 +684,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(cons
     for (int j = wave; j < cnt; j += PF_WAVES) {
         PfStageRaw<I, false> r;
         pf_stage_load<I, false>(act, first + j, true, r);
-        pf_stage_finish<I, false, true>(r, j, true, xh, xl, xs, s_exp, nullptr);
+        pf_stage_finish<I, false, true>(r, j, true, xh, xl, xs, s_exp);
     }
     __syncthreads();
 
@@ -620,7 +744,11 @@ PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden,
     L.pos_off = align256(L.pair_off + P * 4);
     L.act_off = align256(L.pos_off + P * 4);
     L.ypair_off = align256(L.act_off + P * inter * 4);
-    L.total = align256(L.ypair_off + P * hidden * 4);
+    L.xhi_off = align256(L.ypair_off + P * hidden * 4);
+    L.xlo_off = align256(L.xhi_off + (int64_t)n_tokens * hidden * 2);
+    L.xsum_off = align256(L.xlo_off + (int64_t)n_tokens * hidden * 2);
+    L.xexp_off = align256(L.xsum_off + (int64_t)n_tokens * (hidden / 32) * 4);
+    L.total = align256(L.xexp_off + (int64_t)n_tokens * 4);
     return L;
 }
 
@@ -643,8 +771,8 @@ template <int GT, int NBH, int CPW>
 static void launch_p1(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
     const int nch = p.inter / (PF_ROWS_GU * CPW);
     const dim3 grid(pf_grid(nch, p.max_tiles));
-    if (p.x_bf16) PF_LAUNCH((k_prefill_gate_up<GT, NBH, true, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p.x, nch, p);
-    else PF_LAUNCH((k_prefill_gate_up<GT, NBH, false, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p.x, nch, p);
+    if (p.x_bf16) PF_LAUNCH((k_prefill_gate_up<GT, NBH, true, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p.xhi, nch, p);
+    else PF_LAUNCH((k_prefill_gate_up<GT, NBH, false, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p.xhi, nch, p);
 }
 
 template <int GT, int NBH>
@@ -688,7 +816,17 @@ static void launch_p2_i(const PrefillParams& p, hipStream_t s, const KernelEvent
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
     if (p.n_tokens <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_prefill_route, dim3(1), dim3(PF_ROUTE_THREADS), 0, s, p);
+    const dim3 route_grid(1 + (p.n_tokens + PF_STAGE_TOKENS - 1) / PF_STAGE_TOKENS);
+#define MQH_ROUTE(NBH)                                                                                               \
+    if (p.x_bf16) hipLaunchKernelGGL((k_prefill_route<NBH, true>), route_grid, dim3(PF_ROUTE_THREADS), 0, s, p);     \
+    else hipLaunchKernelGGL((k_prefill_route<NBH, false>), route_grid, dim3(PF_ROUTE_THREADS), 0, s, p)
+    switch (p.hidden) {
+        case 256: MQH_ROUTE(1); break;
+        case 512: MQH_ROUTE(2); break;
+        case 1024: MQH_ROUTE(4); break;
+        default: MQH_ROUTE(8); break;
+    }
+#undef MQH_ROUTE
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     switch (p.gate_type) {

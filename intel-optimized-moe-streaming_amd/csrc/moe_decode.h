@@ -112,7 +112,7 @@ struct PrefillParams {
     float* sh_scale;        // [n_tokens]
     int* tiles;             // [max_tiles x 4]: expert, first pair, token count, 0
     int* n_tiles;           // [1]
-    int* pair_tok;          // [P]: token of sorted pair p (P = n_tokens * S)
+    int* tile_tok;          // [max_tiles x 16]: token of column c of tile i (stale past the tile's count)
     int* pos;               // [n_tokens x S]: sorted pair index of (token, slot)
     float* act;             // [P x inter] SwiGLU activations
     float* ypair;           // [P x hidden] expert outputs per pair
@@ -128,7 +128,7 @@ struct PrefillParams {
 };
 
 struct PrefillLayout {
-    int64_t flags_off, scale_off, tiles_off, ntiles_off, pair_off, pos_off, act_off, ypair_off;
+    int64_t flags_off, scale_off, tiles_off, ntiles_off, tok_off, pos_off, act_off, ypair_off;
     int64_t xhi_off, xlo_off, xsum_off, xexp_off, total;
     int max_tiles;
 };

@@ -24,6 +24,7 @@
 // made; P2 stages its activation rows itself).
 #include <hip/hip_ext.h>
 
+#include <algorithm>
 #include <utility>
 
 #include "kquant_frag.h"
@@ -36,9 +37,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int PF_WAVES = 8;      // waves per workgroup of the GEMM kernels
 constexpr int PF_ROWS_GU = 64;   // gate/up rows per workgroup: 4 waves on gate, 4 on up
 constexpr int PF_ROWS_DOWN = 128; // down rows per workgroup chunk: 8 waves x 16
-#ifndef PF_CPW_GU
-#define PF_CPW_GU 2              // gate/up row chunks per workgroup (one continuous load ring; 1: 89.8,
-                                 // 2: 86.4, 4: 93.2 us at the 128-token prompt)
+// Gate/up workgroups take two 64-row chunks on one continuous load ring (one
+// chunk each: 89.8, two: 86.4, four: 93.2 us at the 128-token prompt), except
+// PF_SMALL_GU one-chunk workgroups per tile launched after all the others.
+#ifndef PF_SMALL_GU
+#define PF_SMALL_GU 2
 #endif
 #ifndef PF_CPW_DOWN
 #define PF_CPW_DOWN 1            // down row chunks per workgroup
@@ -341,10 +344,12 @@ struct PfRows {
     static constexpr bool UNROLLED = NBT <= PF_RING;
     static constexpr int R = UNROLLED ? NBT + 1 : PF_RING;
     static_assert(UNROLLED || NBT % R == 0, "blocks per wave must be a multiple of the ring size");
+    static_assert(UNROLLED || NB % R == 0, "a chunk's blocks must be a multiple of the ring size");
     uint32_t raw[R][NMAT][NW];
     const uint8_t* W[NMAT];
     int64_t chunk_stride;
     int q;
+    int nbt = NBT;   // blocks this workgroup runs: NB x its chunks (at most CPW)
 
     __device__ __forceinline__ void load(int b, uint32_t (&dst)[NMAT][NW]) {
         const int64_t off = (int64_t)(b / NB) * chunk_stride + (b % NB) * BB;
@@ -352,9 +357,10 @@ struct PfRows {
         for (int mt = 0; mt < NMAT; ++mt) frag_load<T>(W[mt] + off, q, dst[mt]);
     }
 
+    // (a ring slot past nbt re-reads the last block: in bounds, unused)
     __device__ __forceinline__ void prefetch() {
 #pragma unroll
-        for (int b = 0; b < (NBT < R - 1 ? NBT : R - 1); ++b) load(b, raw[b]);
+        for (int b = 0; b < (NBT < R - 1 ? NBT : R - 1); ++b) load(min(b, nbt - 1), raw[b]);
     }
 
     // one super-block (block kb of its row): P = sum over its 8 steps of the exact
@@ -419,6 +425,7 @@ struct PfRows {
         if constexpr (UNROLLED) {
 #pragma unroll
             for (int b = 0; b < NBT; ++b) {
+                if (b >= nbt) break;
                 if (b + R - 1 < NBT) load(b + R - 1, raw[(b + R - 1) % R]);
                 __builtin_amdgcn_sched_barrier(0);
                 block<SPLIT>(raw[b % R], b % NB, xh, xl, xs, acc);
@@ -426,12 +433,12 @@ struct PfRows {
             }
         } else {
 #pragma unroll 1
-            for (int b0 = 0; b0 < NBT; b0 += R)
+            for (int b0 = 0; b0 < nbt; b0 += R)
 #pragma unroll
             for (int bi = 0; bi < R; ++bi) {
                 const int b = b0 + bi;
                 // the tail re-reads the last block (in bounds, unused)
-                load(min(b + R - 1, NBT - 1), raw[(bi + R - 1) % R]);
+                load(min(b + R - 1, nbt - 1), raw[(bi + R - 1) % R]);
                 __builtin_amdgcn_sched_barrier(0);
                 block<SPLIT>(raw[bi], b % NB, xh, xl, xs, acc);
                 if ((b + 1) % NB == 0) end(b / NB, acc);
@@ -453,6 +460,32 @@ __device__ __forceinline__ void pf_wg(int nch_log2, int& tile, int& chunk) {
     chunk = r & ((1 << nch_log2) - 1);
     tile = (r >> nch_log2) * PF_XCDS + i % PF_XCDS;
 }
+// The gate/up kernel's workgroups: the first nbig x mt (mt = max_tiles rounded
+// up to 8) take two 64-row chunks of a tile, the rest one, in that order, so
+// the dispatcher's last workgroups are the short ones (a launch runs ~2
+// workgroups a slot, and its end waits for the last started).  Per tile, nbig
+// workgroups cover chunks 0 .. 2 nbig - 1 and nsmall the remaining ones; the
+// chunks of one tile again agree mod 8.  r / d is one multiply-high by
+// m = ceil(2^32 / d) (0 for d = 1), exact for every r a launch reaches.
+struct PfSplit {
+    int nbig, nsmall;
+    unsigned mbig, msmall;
+};
+__device__ __forceinline__ void pf_wg_split(int max_tiles, const PfSplit& sp, int& tile, int& chunk0, int& nch) {
+    const int mt = (max_tiles + PF_XCDS - 1) & ~(PF_XCDS - 1);
+    const int i = blockIdx.x, na = sp.nbig * mt;
+    const bool big = i < na;
+    const int j = big ? i : i - na, r = j / PF_XCDS;
+    const int d = big ? sp.nbig : sp.nsmall;
+    const unsigned m = big ? sp.mbig : sp.msmall;
+    const int g = m ? (int)__umulhi((unsigned)r, m) : r;
+    const int k = r - g * d;
+    tile = g * PF_XCDS + j % PF_XCDS;
+    chunk0 = big ? 2 * k : 2 * sp.nbig + k;
+    nch = big ? 2 : 1;
+}
+static unsigned pf_magic(int d) { return d > 1 ? (unsigned)((0x100000000ull + d - 1) / d) : 0u; }
+
 // The tile's descriptor, when tile is below the launch's tile count: the
 // count and the descriptor are loaded together (every slot below max_tiles
 // exists; past the count it holds stale words, never used).  The test reads
@@ -470,7 +503,7 @@ __device__ __forceinline__ bool pf_live_tile(const int* n_tiles, const int4* til
 struct PfHot {
     const int* n_tiles;
     const int4* tiles;
-    const int* pair_tok;
+    const int* tile_tok;
     const void* src;   // P1: the tokens x; P2: the activations
     int max_tiles;
 };
@@ -490,6 +523,7 @@ constexpr int PF_STAGE_TOKENS = 4;
 template <int NBH, bool XBF16>
 __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParams p) {
     __shared__ int cnt[PREFILL_MAX_EXPERTS], off[PREFILL_MAX_EXPERTS], fill[PREFILL_MAX_EXPERTS];
+    __shared__ int toff[PREFILL_MAX_EXPERTS];
     __shared__ int wsum[16][2];
     const int T = p.n_tokens, K = p.top_k, E = p.n_experts, TK = T * K;
     const int e = threadIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -530,6 +564,7 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
     const int first = bc + ic - c, tfirst = bt + it - tc;
     if (e < E) {
         off[e] = first;
+        toff[e] = tfirst;
         for (int j = 0; j < tc; ++j)
             ((int4*)p.tiles)[tfirst + j] =
                 make_int4(e, first + PREFILL_TILE * j, min(PREFILL_TILE, c - PREFILL_TILE * j), 0);
@@ -547,24 +582,28 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
         const int id = p.ids[i];
         int pp = -1;
         if (id >= 0 && id < E) {
-            pp = off[id] + atomicAdd(&fill[id], 1);
-            p.pair_tok[pp] = i / K;
+            const int k = atomicAdd(&fill[id], 1);
+            pp = off[id] + k;
+            p.tile_tok[(toff[id] + k / PREFILL_TILE) * PREFILL_TILE + k % PREFILL_TILE] = i / K;
         }
         p.pos[(i / K) * p.S + (i % K)] = pp;
     }
-    if (p.has_shared)
-        for (int t = threadIdx.x; t < T; t += PF_ROUTE_THREADS) {
-            p.pair_tok[TK + t] = t;
-            p.pos[t * p.S + K] = TK + t;
-        }
+    if (p.has_shared) {
+        for (int t = threadIdx.x; t < T; t += PF_ROUTE_THREADS) p.pos[t * p.S + K] = TK + t;
+        // the shared tiles follow the routed ones: column c of shared tile j is token 16 j + c
+        for (int t = threadIdx.x; t < T; t += PF_ROUTE_THREADS) p.tile_tok[tott * PREFILL_TILE + t] = t;
+    }
 }
 
 // ------------------------------------------------------------ P1
 
 template <int GT, int NBH, bool XBF16, int CPW>
 __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(const int* n_tiles, const int4* tiles,
-                                                                             const int* pair_tok, const void* xsrc,
-                                                                             int max_tiles, int nch_log2, PrefillParams p) {
+                                                                             const int* tile_tok, const void* xsrc,
+                                                                             int max_tiles, int nbig, int nsmall,
+                                                                             unsigned mbig, unsigned msmall,
+                                                                             PrefillParams p) {
+    static_assert(CPW == 2, "workgroups take one or two chunks");
     constexpr int H = NBH * 256, KP = H + PF_PAD;
     constexpr bool SPLIT = !XBF16;   // BF16 tokens are exact in the high plane
     __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
@@ -572,8 +611,11 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     __shared__ __attribute__((aligned(16))) _Float16 xs[PREFILL_TILE * NBH * 16];
     __shared__ __attribute__((aligned(16))) float s_up[PF_WAVES / 2][64][4];
     __shared__ int s_exp[PREFILL_TILE];
-    int tile, chunk;
-    pf_wg(nch_log2, tile, chunk);
+    int tile, chunk0, nch;
+    pf_wg_split(max_tiles, PfSplit{nbig, nsmall, mbig, msmall}, tile, chunk0, nch);
+    // the tile's tokens, one a lane (lane j: column j), need the tile index only,
+    // so their load goes out ahead of the descriptor's
+    const int pt = tile_tok[min(tile, max_tiles - 1) * PREFILL_TILE + (threadIdx.x & (PREFILL_TILE - 1))];
     int4 td;
     const bool live = pf_live_tile(n_tiles, tiles, max_tiles, tile, td);
     // the argument-block fields the weight addresses need, awaited together
@@ -588,10 +630,10 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     if (!live) return;
     const int e = td.x, first = td.y, cnt = td.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
-    // waves 0..3: gate rows, waves 4..7: the same up rows; CPW chunks of 64 rows
+    // waves 0..3: gate rows, waves 4..7: the same up rows; nch chunks of 64 rows
     const int wv = __builtin_amdgcn_readfirstlane(wave);
     const int mat = wv / (PF_WAVES / 2), wsub = wv % (PF_WAVES / 2);
-    const int rbase = chunk * PF_ROWS_GU * CPW + wsub * 16;
+    const int rbase = chunk0 * PF_ROWS_GU + wsub * 16;
     const int64_t row_bytes = (int64_t)NBH * block_bytes(GT);
 
     // (selects of wave-uniform values, no branch: each branch would load its
@@ -602,15 +644,15 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     g.W[0] = (e < 0 ? Ws : Wr) + (int64_t)(rbase + (lane & 15)) * row_bytes;
     g.chunk_stride = PF_ROWS_GU * row_bytes;
     g.q = q;
-    // the wave's token columns wv and wv + 8 (a column past cnt re-reads the
-    // tile's first token and stages nothing): their loads go out before the
+    g.nbt = NBH * nch;
+    // the wave's token columns wv and wv + 8 (a column past cnt reads token 0's
+    // first words and stages nothing): their loads go out before the
     // weight prefetch, so the staging below waits for them only
     static_assert(PREFILL_TILE == 2 * PF_WAVES, "two token columns per wave");
     const bool l0 = wv < cnt, l1 = wv + PF_WAVES < cnt;
-    // the tile's tokens in one vector load (lane j: column j, clamped to the
-    // last pair), then the wave's two picked out
-    const int pt = pair_tok[first + min(lane & (PREFILL_TILE - 1), cnt - 1)];
-    const int t0 = __builtin_amdgcn_readlane(pt, wv), t1 = __builtin_amdgcn_readlane(pt, wv + PF_WAVES);
+    // (columns at or past cnt hold stale words: token 0 stands in)
+    const int t0 = l0 ? __builtin_amdgcn_readlane(pt, wv) : 0;
+    const int t1 = l1 ? __builtin_amdgcn_readlane(pt, wv + PF_WAVES) : 0;
     PfPlanes<H, SPLIT> r0, r1;
     pf_planes_load<H, SPLIT>(xhi, xlo, xsum, xexp, t0, l0, r0);
     pf_planes_load<H, SPLIT>(xhi, xlo, xsum, xexp, t1, l1, r1);
@@ -653,7 +695,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
 
 template <int DT, int NBI, int CPW>
 __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(const int* n_tiles, const int4* tiles,
-                                                                           const int* pair_tok, const void* act,
+                                                                           const int* tile_tok, const void* act,
                                                                            int max_tiles, int nch_log2, PrefillParams p) {
     constexpr int I = NBI * 256, KP = I + PF_PAD;
     __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
@@ -740,8 +782,8 @@ PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden,
     L.scale_off = align256(WS_HEAD_BYTES);
     L.tiles_off = align256(L.scale_off + (int64_t)n_tokens * 4);
     L.ntiles_off = align256(L.tiles_off + (int64_t)std::max(L.max_tiles, 1) * 16);
-    L.pair_off = align256(L.ntiles_off + 4);
-    L.pos_off = align256(L.pair_off + P * 4);
+    L.tok_off = align256(L.ntiles_off + 4);
+    L.pos_off = align256(L.tok_off + (int64_t)std::max(L.max_tiles, 1) * PREFILL_TILE * 4);
     L.act_off = align256(L.pos_off + P * 4);
     L.ypair_off = align256(L.act_off + P * inter * 4);
     L.xhi_off = align256(L.ypair_off + P * hidden * 4);
@@ -757,28 +799,38 @@ PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden,
     do {                                                                                                      \
         if (armed)                                                                                            \
             hipExtLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, e0, e1, 0, (const int*)p.n_tiles,   \
-                                  (const int4*)p.tiles, (const int*)p.pair_tok, (const void*)(src), p.max_tiles, __builtin_ctz(nch), p); \
+                                  (const int4*)p.tiles, (const int*)p.tile_tok, (const void*)(src), p.max_tiles, __builtin_ctz(nch), p); \
         else                                                                                                  \
             hipLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, (const int*)p.n_tiles,                 \
-                               (const int4*)p.tiles, (const int*)p.pair_tok, (const void*)(src), p.max_tiles, __builtin_ctz(nch), p); \
+                               (const int4*)p.tiles, (const int*)p.tile_tok, (const void*)(src), p.max_tiles, __builtin_ctz(nch), p); \
     } while (0)
 
-// chunks per workgroup: gate/up rows CPW x 64, down rows CPW x 128
-constexpr int pf_cpw_gu(int inter) { return inter / PF_ROWS_GU < PF_CPW_GU ? inter / PF_ROWS_GU : PF_CPW_GU; }
+// down row chunks per workgroup (CPW x 128 rows)
 constexpr int pf_cpw_down(int hidden) { return hidden / PF_ROWS_DOWN < PF_CPW_DOWN ? hidden / PF_ROWS_DOWN : PF_CPW_DOWN; }
 
-template <int GT, int NBH, int CPW>
+template <int GT, int NBH, bool XBF16>
 static void launch_p1(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
-    const int nch = p.inter / (PF_ROWS_GU * CPW);
-    const dim3 grid(pf_grid(nch, p.max_tiles));
-    if (p.x_bf16) PF_LAUNCH((k_prefill_gate_up<GT, NBH, true, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p.xhi, nch, p);
-    else PF_LAUNCH((k_prefill_gate_up<GT, NBH, false, CPW>), grid, ev.armed_a(), ev.a_start, ev.a_stop, s, p.xhi, nch, p);
+    // one-chunk workgroups per tile (PF_SMALL_GU, fewer when the tile has fewer
+    // chunks), the rest two-chunk ones
+    static_assert(PF_SMALL_GU % 2 == 0, "an even number of one-chunk workgroups per tile");
+    const int chunks = p.inter / PF_ROWS_GU;   // 4 .. 32
+    const int nsmall = std::min(PF_SMALL_GU, chunks), nbig = (chunks - nsmall) / 2;
+    const dim3 grid((nbig + nsmall) * ((p.max_tiles + PF_XCDS - 1) / PF_XCDS * PF_XCDS)), block(64 * PF_WAVES);
+    const unsigned mbig = pf_magic(nbig), msmall = pf_magic(nsmall);
+    if (ev.armed_a())
+        hipExtLaunchKernelGGL((k_prefill_gate_up<GT, NBH, XBF16, 2>), grid, block, 0, s, ev.a_start, ev.a_stop, 0,
+                              (const int*)p.n_tiles, (const int4*)p.tiles, (const int*)p.tile_tok, (const void*)p.xhi,
+                              p.max_tiles, nbig, nsmall, mbig, msmall, p);
+    else
+        hipLaunchKernelGGL((k_prefill_gate_up<GT, NBH, XBF16, 2>), grid, block, 0, s, (const int*)p.n_tiles,
+                           (const int4*)p.tiles, (const int*)p.tile_tok, (const void*)p.xhi, p.max_tiles, nbig, nsmall,
+                           mbig, msmall, p);
 }
 
 template <int GT, int NBH>
 static void launch_p1_i(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
-    if (p.inter == 256) launch_p1<GT, NBH, pf_cpw_gu(256)>(p, s, ev);
-    else launch_p1<GT, NBH, PF_CPW_GU>(p, s, ev);
+    if (p.x_bf16) launch_p1<GT, NBH, true>(p, s, ev);
+    else launch_p1<GT, NBH, false>(p, s, ev);
 }
 
 template <int GT>

@@ -602,7 +602,7 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
     dom = "A" if kb["A"] >= kb["B"] else "B"
     frac = frac_a if dom == "A" else 1 - frac_a
     kname = {"prefill": {"A": "mqh::k_prefill_gate_up<11, 8, false, 2>", "B": "mqh::k_prefill_down<11, 2, 1>"},
-             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32, false, 2>", "B": "mqh::k_fast_down<11, 11, 8, 4, false>"}}[best][dom]
+             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32, false, 2>", "B": "mqh::k_fast_down_bal<11, 11, 8, 4>"}}[best][dom]
     out = {
         "workload": f"batched decode: {T} tokens, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
                     f"logits + shared, all Q3_K, {n_layers} resident layers rotated",

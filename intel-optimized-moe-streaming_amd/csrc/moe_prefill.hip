@@ -343,8 +343,6 @@ struct PfRows {
     // blocks b+1 .. b+R-1 are in flight (all of them for short rows)
     static constexpr bool UNROLLED = NBT <= PF_RING;
     static constexpr int R = UNROLLED ? NBT + 1 : PF_RING;
-    static_assert(UNROLLED || NBT % R == 0, "blocks per wave must be a multiple of the ring size");
-    static_assert(UNROLLED || NB % R == 0, "a chunk's blocks must be a multiple of the ring size");
     uint32_t raw[R][NMAT][NW];
     const uint8_t* W[NMAT];
     int64_t chunk_stride;
@@ -437,6 +435,7 @@ struct PfRows {
 #pragma unroll
             for (int bi = 0; bi < R; ++bi) {
                 const int b = b0 + bi;
+                if (NB % R != 0 && b >= nbt) break;   // (a whole number of rings otherwise)
                 // the tail re-reads the last block (in bounds, unused)
                 load(min(b + R - 1, nbt - 1), raw[(bi + R - 1) % R]);
                 __builtin_amdgcn_sched_barrier(0);

@@ -333,6 +333,8 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     const uint8_t *Gm = h.top_k > 0 ? p.gate : p.sh_gate, *Um = h.top_k > 0 ? p.up : p.sh_up;
     if (shared) { Gm = p.sh_gate; Um = p.sh_up; }
     bool bad = false;
+    bool route_publish = false;   // (ROUTED: the token's first workgroup writes the ids and weights)
+    float route_mine = 0.0f;      // (its wave 0: lane r keeps the r-th selected score)
     if constexpr (ROUTED) {
         // routing in the prologue (router.py:140-170).  A workgroup's items are
         // consecutive, so its routed waves need the experts of ranks s_first ..
@@ -346,23 +348,20 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
         const int it_first = xg * h.a_waves * IPW;
         const int it_last = min(it_first + h.a_waves * IPW - 1, h.S * per_slot - 1);
         if ((it_first >> sh_ps) < h.top_k) {   // the workgroup has a routed item (uniform)
+            const bool publish = xg == 0;
+            route_publish = publish;
             if (wave == 0) {
-                const bool publish = xg == 0;
                 const int rounds = publish ? h.top_k : min(it_last >> sh_ps, h.top_k - 1) + 1;
-                uint64_t key[ROUTE_PROLOGUE_MAX_EXPERTS / 64];
-                route_keys(p.route_scores + (int64_t)t * h.n_experts, h.n_experts, lane, key);
-                float mine = 0.0f;
+                uint32_t ord[ROUTE_PROLOGUE_MAX_EXPERTS / 64];
+                route_ords(p.route_scores + (int64_t)t * h.n_experts, h.n_experts, lane, ord);
                 for (int r = 0; r < rounds; ++r) {
-                    const uint64_t win = route_next(key);
-                    if (lane == r) mine = key_score(win);
+                    uint32_t best;
+                    const int win = route_next(ord, lane, best);
+                    if (lane == r) route_mine = ord_score(best);
                     if (lane == 0) {
-                        s_rank[r] = key_expert(win);
-                        if (publish) p.route_ids[t * h.top_k + r] = key_expert(win);
+                        s_rank[r] = win;
+                        if (publish) p.route_ids[t * h.top_k + r] = win;
                     }
-                }
-                if (publish) {
-                    const float w = route_weight(mine, h.top_k, lane);
-                    if (lane < h.top_k) p.route_weights[t * h.top_k + lane] = w;
                 }
             }
             // (LDS only: the token's and id loads stay in flight)
@@ -396,6 +395,14 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    // the routing weights are read by the down kernel only: the token's first
+    // workgroup computes them here, with its weight loads in flight
+    if constexpr (ROUTED) {
+        if (route_publish && wave == 0) {
+            const float w = route_weight(route_mine, h.top_k, lane);
+            if (lane < h.top_k) p.route_weights[t * h.top_k + lane] = w;
+        }
+    }
     // 2. token digits (in the FP16 graph also the token rounded to FP16), and
     // this lane's operands out of LDS, while the weight loads are in flight
     if (threadIdx.x < NX) {

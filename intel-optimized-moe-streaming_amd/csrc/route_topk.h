@@ -3,12 +3,11 @@
 // 140-170), shared by the router's select kernel and the routed decode
 // prologue.
 //
-// Each lane holds NM scores (experts lane, lane+64, ...) as 64-bit keys: the
-// score's orderable bits above, the complemented expert index below, so a
-// larger key ranks first and, at equal scores, the lower expert wins.  Every
-// NaN ranks above every number (np.argsort places NaN last, so the reference
-// selects NaN scores first); -0.0 and +0.0 are equal.  A round takes the
-// wavefront maximum over DPP row operations and removes it.
+// Each lane holds NM scores (experts lane, lane+64, ...) as orderable 32-bit
+// values.  A round takes their wavefront maximum over DPP row operations and
+// then the lowest expert holding it (ballots), so at equal scores the lower
+// expert wins.  Every NaN ranks above every number (np.argsort places NaN
+// last, so the reference selects NaN scores first); -0.0 and +0.0 are equal.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -17,74 +16,71 @@
 
 namespace mqh {
 
-// Orderable key of (score, expert): a larger key ranks first.  Never 0.
-__device__ __forceinline__ uint64_t route_key(float s, int e) {
+// Orderable form of a score: a larger value ranks first, every NaN above
+// +inf, -0.0 equal to +0.0.  Never 0, which marks an expert already selected
+// or past n_experts.
+__device__ __forceinline__ uint32_t route_ord(float s) {
     uint32_t u = __float_as_uint(s);
-    uint32_t ord;
-    if (s != s) {
-        ord = 0xFFFFFFFFu;                            // every NaN above +inf
-    } else {
-        if (u == 0x80000000u) u = 0;                  // -0.0 == +0.0
-        ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    }
-    return ((uint64_t)ord << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+    if (s != s) return 0xFFFFFFFFu;
+    if (u == 0x80000000u) u = 0;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ float key_score(uint64_t k) {
-    const uint32_t ord = (uint32_t)(k >> 32);
+__device__ __forceinline__ float ord_score(uint32_t ord) {
     return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord);
 }
 
-__device__ __forceinline__ int key_expert(uint64_t k) { return (int)(0xFFFFFFFFu - (uint32_t)k); }
-
+// One step of the wavefront maximum: the DPP move and the maximum stay two
+// instructions (the empty asm keeps the compiler from folding them into one
+// DPP maximum).  Lanes outside ROW_MASK keep their own value.
 template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint64_t dpp_max_step(uint64_t v) {
-    const int vlo = (int)(uint32_t)v, vhi = (int)(uint32_t)(v >> 32);
-    const int lo = __builtin_amdgcn_update_dpp(vlo, vlo, CTRL, ROW_MASK, 0xF, false);
-    const int hi = __builtin_amdgcn_update_dpp(vhi, vhi, CTRL, ROW_MASK, 0xF, false);
-    const uint64_t o = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
-    return o > v ? o : v;
+__device__ __forceinline__ uint32_t dpp_max_step(uint32_t v) {
+    int o = __builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROW_MASK, 0xF, false);
+    __asm__ volatile("" : "+v"(o));
+    return (uint32_t)o > v ? (uint32_t)o : v;
 }
 
-// Maximum over the wavefront, returned uniform.  Lanes outside a step's row
-// mask keep their own value.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+// Maximum over the wavefront, returned uniform.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     v = dpp_max_step<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
     v = dpp_max_step<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
     v = dpp_max_step<0x141, 0xF>(v);   // row_half_mirror
     v = dpp_max_step<0x140, 0xF>(v);   // row_mirror: every lane holds its row's maximum
     v = dpp_max_step<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
     v = dpp_max_step<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3: lane 63 holds the maximum
-    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-    return ((uint64_t)hi << 32) | lo;
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// The keys of one token's n_experts scores (st), NM per lane; every load is
-// issued before any is used (indexes past n_experts re-read the last score
-// and get key 0).
+// The ords of one token's n_experts scores (st), NM per lane (expert
+// lane + 64 m); every load is issued before any is used (indexes past
+// n_experts re-read the last score and get 0).
 template <int NM>
-__device__ __forceinline__ void route_keys(const float* st, int n_experts, int lane, uint64_t (&key)[NM]) {
+__device__ __forceinline__ void route_ords(const float* st, int n_experts, int lane, uint32_t (&ord)[NM]) {
     float sv[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) sv[m] = st[min(lane + 64 * m, n_experts - 1)];
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-        const int e = lane + 64 * m;
-        key[m] = e < n_experts ? route_key(sv[m], e) : 0;
-    }
+    for (int m = 0; m < NM; ++m) ord[m] = lane + 64 * m < n_experts ? route_ord(sv[m]) : 0u;
 }
 
-// One round: the best remaining key (uniform), removed from the lanes' keys.
+// One round: the best remaining score (its ord, uniform, in `best`) and its
+// expert, the lowest index among equal scores (a ballot per m, smallest m
+// first, lowest lane first), removed from the lanes' ords.
 template <int NM>
-__device__ __forceinline__ uint64_t route_next(uint64_t (&key)[NM]) {
-    uint64_t b = key[0];
+__device__ __forceinline__ int route_next(uint32_t (&ord)[NM], int lane, uint32_t& best) {
+    uint32_t b = ord[0];
 #pragma unroll
-    for (int m = 1; m < NM; ++m) b = key[m] > b ? key[m] : b;
-    const uint64_t win = wave_max_u64(b);
+    for (int m = 1; m < NM; ++m) b = ord[m] > b ? ord[m] : b;
+    best = wave_max_u32(b);
+    int win = 0;
+#pragma unroll
+    for (int m = NM - 1; m >= 0; --m) {
+        const uint64_t hit = __ballot(ord[m] == best);
+        if (hit != 0) win = 64 * m + (int)__builtin_ctzll(hit);
+    }
 #pragma unroll
     for (int m = 0; m < NM; ++m)
-        if (key[m] == win) key[m] = 0;
+        if (lane + 64 * m == win) ord[m] = 0u;
     return win;
 }
 

@@ -120,13 +120,14 @@ __global__ __launch_bounds__(64 * SEL_WAVES) void k_route_select(const float* __
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * SEL_WAVES + (threadIdx.x >> 6);
     if (t >= n_tokens) return;   // the whole wave leaves: no workgroup barrier below
-    uint64_t key[NM];
-    route_keys<NM>(scores + (int64_t)t * n_experts, n_experts, lane, key);
+    uint32_t ord[NM];
+    route_ords<NM>(scores + (int64_t)t * n_experts, n_experts, lane, ord);
     float mine = 0.0f;   // lane r keeps the r-th selected score
     for (int r = 0; r < top_k; ++r) {
-        const uint64_t win = route_next<NM>(key);
-        if (lane == r) mine = key_score(win);
-        if (lane == 0) ids[(int64_t)t * top_k + r] = key_expert(win);
+        uint32_t best;
+        const int win = route_next<NM>(ord, lane, best);
+        if (lane == r) mine = ord_score(best);
+        if (lane == 0) ids[(int64_t)t * top_k + r] = win;
     }
     const float w = route_weight(mine, top_k, lane);
     if (lane < top_k) weights[(int64_t)t * top_k + lane] = w;

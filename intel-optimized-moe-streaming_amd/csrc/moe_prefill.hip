@@ -49,6 +49,9 @@ constexpr int PF_ROWS_DOWN = 128; // down rows per workgroup chunk: 8 waves x 16
 #ifndef PF_RING
 #define PF_RING 4                // register ring of super-blocks per lane (R - 1 in flight)
 #endif
+#ifndef PF_RING_DOWN
+#define PF_RING_DOWN PF_RING
+#endif
 constexpr int PF_PAD = 8;        // LDS row padding (halves)
 
 // Waves per SIMD that the LDS footprint of one workgroup (PF_WAVES waves)
@@ -336,13 +339,13 @@ __device__ __forceinline__ void pf_planes_store(const PfPlanes<K, SPLIT>& r, int
 // so the loads of the next chunk are in flight while one ends.  prefetch()
 // loads the first blocks before the caller stages the tokens, so that the two
 // overlap.  D layout: lane l holds rows 4(l/16) + i, token column l % 16.
-template <int T, int NMAT, int NB, int CPW>
+template <int T, int NMAT, int NB, int CPW, int RING = PF_RING>
 struct PfRows {
     static constexpr int NW = FragGeo<T>::NW, BB = block_bytes(T), NBT = NB * CPW;
     // R ring slots: block b lives in slot b % R; while block b is computed,
     // blocks b+1 .. b+R-1 are in flight (all of them for short rows)
-    static constexpr bool UNROLLED = NBT <= PF_RING;
-    static constexpr int R = UNROLLED ? NBT + 1 : PF_RING;
+    static constexpr bool UNROLLED = NBT <= RING;
+    static constexpr int R = UNROLLED ? NBT + 1 : RING;
     uint32_t raw[R][NMAT][NW];
     const uint8_t* W[NMAT];
     int64_t chunk_stride;
@@ -714,7 +717,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(cons
     const int rbase = chunk * PF_ROWS_DOWN * CPW + wave * 16;
     const int64_t row_bytes = (int64_t)NBI * block_bytes(DT);
 
-    PfRows<DT, 1, NBI, CPW> g;
+    PfRows<DT, 1, NBI, CPW, PF_RING_DOWN> g;
     g.W[0] = (e < 0 ? sh_down : down + (int64_t)max(e, 0) * down_eb) + (int64_t)(rbase + (lane & 15)) * row_bytes;
     g.chunk_stride = PF_ROWS_DOWN * row_bytes;
     g.q = q;

@@ -80,7 +80,9 @@ def test_prefill_bench_shape(bench_shape_layer, oracle_mod, x_bf16):
 
 
 @pytest.mark.parametrize("types", [(11, 11), (13, 12), (14, 14), (12, 13), (11, 14), (12, 11)])
-@pytest.mark.parametrize("shape", [(256, 256), (512, 1024), (1024, 256)])
+# (intermediate 256 .. 2048: 4 .. 32 row chunks, so one to fifteen two-chunk
+# workgroups a tile ahead of the one-chunk ones in the gate/up launch)
+@pytest.mark.parametrize("shape", [(256, 256), (512, 1024), (1024, 256), (256, 2048), (2048, 1024)])
 def test_prefill_type_pairs(oracle_mod, hip, types, shape):
     gt, dt = types
     H, I = shape

@@ -514,6 +514,7 @@ static int pf_grid(int nch, int max_tiles) { return nch * ((max_tiles + PF_XCDS 
 // ------------------------------------------------------------ P0
 
 constexpr int PF_ROUTE_THREADS = 1024;   // one workgroup (a constant: blockDim.x costs a memory round trip)
+constexpr int PF_ROUTE_IDS = 4;          // (token, slot) ids a routing thread keeps in registers
 
 // Tokens a staging workgroup takes: one wave each on waves 0..3 (one a SIMD;
 // sixteen a workgroup measured 1.2 us longer for the route pass at 128 tokens)
@@ -542,8 +543,17 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
     }
     if (e < E) { cnt[e] = 0; fill[e] = 0; }
     __syncthreads();
+    // a thread's first PF_ROUTE_IDS ids stay in registers for the second pass
+    // (one memory round trip fewer on the pass's path); the rest are re-read
+    int idr[PF_ROUTE_IDS];
+#pragma unroll
+    for (int j = 0; j < PF_ROUTE_IDS; ++j) {
+        const int i = threadIdx.x + j * PF_ROUTE_THREADS;
+        idr[j] = i < TK ? p.ids[i] : 0;
+    }
     for (int i = threadIdx.x; i < TK; i += PF_ROUTE_THREADS) {
-        const int id = p.ids[i];
+        const int j = (i - threadIdx.x) / PF_ROUTE_THREADS;
+        const int id = j < PF_ROUTE_IDS ? idr[j < PF_ROUTE_IDS ? j : 0] : p.ids[i];
         if (id < 0 || id >= E) atomicOr(&p.flags[FLAG_BAD_ID], 1);
         else atomicAdd(&cnt[id], 1);
     }
@@ -581,7 +591,8 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
     // pair order inside an expert follows the atomics; a pair's result does not
     // depend on its column in the tile, so outputs do not depend on it
     for (int i = threadIdx.x; i < TK; i += PF_ROUTE_THREADS) {
-        const int id = p.ids[i];
+        const int j = (i - threadIdx.x) / PF_ROUTE_THREADS;
+        const int id = j < PF_ROUTE_IDS ? idr[j < PF_ROUTE_IDS ? j : 0] : p.ids[i];
         int pp = -1;
         if (id >= 0 && id < E) {
             const int k = atomicAdd(&fill[id], 1);
@@ -745,19 +756,35 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(cons
 
 // ------------------------------------------------------------ P3
 
+// Eight slots at a time: their pair indexes and weights (scalar loads), then
+// their eight expert outputs, then the sum in top-k order; the shared
+// expert's output is loaded with the first eight and added last.
+constexpr int PF_COMBINE_SLOTS = 8;
 __global__ __launch_bounds__(256) void k_prefill_combine(PrefillParams p) {
     const int t = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
     if (h >= p.hidden) return;
+    const int* pos = p.pos + t * p.S;
+    const float* wt = p.weights + t * p.top_k;
+    const int psh = p.has_shared ? pos[p.top_k] : 0;
+    const float ssh = p.has_shared ? p.sh_scale[t] : 0.0f;
+    const float ysh = p.ypair[(int64_t)psh * p.hidden + h];
     float acc = 0.0f;
-    for (int s = 0; s < p.top_k; ++s) {
-        const int pp = p.pos[t * p.S + s];
-        if (pp < 0) continue;   // expert id out of range: flagged by the route pass
-        acc = __fadd_rn(acc, __fmul_rn(p.weights[t * p.top_k + s], p.ypair[(int64_t)pp * p.hidden + h]));
+    for (int s0 = 0; s0 < p.top_k; s0 += PF_COMBINE_SLOTS) {
+        int pp[PF_COMBINE_SLOTS];
+        float w[PF_COMBINE_SLOTS], y[PF_COMBINE_SLOTS];
+#pragma unroll
+        for (int j = 0; j < PF_COMBINE_SLOTS; ++j) {
+            const int s = min(s0 + j, p.top_k - 1);
+            pp[j] = pos[s];
+            w[j] = wt[s];
+        }
+#pragma unroll
+        for (int j = 0; j < PF_COMBINE_SLOTS; ++j) y[j] = p.ypair[(int64_t)max(pp[j], 0) * p.hidden + h];
+#pragma unroll
+        for (int j = 0; j < PF_COMBINE_SLOTS; ++j)   // (pp < 0: an expert id out of range, flagged by the route pass)
+            if (s0 + j < p.top_k && pp[j] >= 0) acc = __fadd_rn(acc, __fmul_rn(w[j], y[j]));
     }
-    if (p.has_shared) {
-        const int pp = p.pos[t * p.S + p.top_k];
-        acc = __fadd_rn(acc, __fmul_rn(p.sh_scale[t], p.ypair[(int64_t)pp * p.hidden + h]));
-    }
+    if (p.has_shared) acc = __fadd_rn(acc, __fmul_rn(ssh, ysh));
     p.y[(int64_t)t * p.hidden + h] = acc;
     if (!isfinite(acc)) atomicOr(&p.flags[FLAG_NONFINITE], 1);
 }

@@ -37,9 +37,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int PF_WAVES = 8;      // waves per workgroup of the GEMM kernels
 constexpr int PF_ROWS_GU = 64;   // gate/up rows per workgroup: 4 waves on gate, 4 on up
 constexpr int PF_ROWS_DOWN = 128; // down rows per workgroup chunk: 8 waves x 16
-// Gate/up workgroups take two 64-row chunks on one continuous load ring (one
-// chunk each: 89.8, two: 86.4, four: 93.2 us at the 128-token prompt), except
-// PF_SMALL_GU one-chunk workgroups per tile launched after all the others.
+// Gate/up workgroups take PF_BIG_GU 64-row chunks on one continuous load ring
+// (one chunk each: 89.8, two: 86.4, four: 93.2 us at the 128-token prompt),
+// except at least PF_SMALL_GU one-chunk workgroups per tile launched after all
+// the others.
+#ifndef PF_BIG_GU
+#define PF_BIG_GU 2
+#endif
 #ifndef PF_SMALL_GU
 #define PF_SMALL_GU 2
 #endif
@@ -463,16 +467,17 @@ __device__ __forceinline__ void pf_wg(int nch_log2, int& tile, int& chunk) {
     tile = (r >> nch_log2) * PF_XCDS + i % PF_XCDS;
 }
 // The gate/up kernel's workgroups: the first nbig x mt (mt = max_tiles rounded
-// up to 8) take two 64-row chunks of a tile, the rest one, in that order, so
+// up to 8) take CB 64-row chunks of a tile, the rest one, in that order, so
 // the dispatcher's last workgroups are the short ones (a launch runs ~2
 // workgroups a slot, and its end waits for the last started).  Per tile, nbig
-// workgroups cover chunks 0 .. 2 nbig - 1 and nsmall the remaining ones; the
+// workgroups cover chunks 0 .. CB nbig - 1 and nsmall the remaining ones; the
 // chunks of one tile again agree mod 8.  r / d is one multiply-high by
 // m = ceil(2^32 / d) (0 for d = 1), exact for every r a launch reaches.
 struct PfSplit {
     int nbig, nsmall;
     unsigned mbig, msmall;
 };
+template <int CB>
 __device__ __forceinline__ void pf_wg_split(int max_tiles, const PfSplit& sp, int& tile, int& chunk0, int& nch) {
     const int mt = (max_tiles + PF_XCDS - 1) & ~(PF_XCDS - 1);
     const int i = blockIdx.x, na = sp.nbig * mt;
@@ -483,8 +488,8 @@ __device__ __forceinline__ void pf_wg_split(int max_tiles, const PfSplit& sp, in
     const int g = m ? (int)__umulhi((unsigned)r, m) : r;
     const int k = r - g * d;
     tile = g * PF_XCDS + j % PF_XCDS;
-    chunk0 = big ? 2 * k : 2 * sp.nbig + k;
-    nch = big ? 2 : 1;
+    chunk0 = big ? CB * k : CB * sp.nbig + k;
+    nch = big ? CB : 1;
 }
 static unsigned pf_magic(int d) { return d > 1 ? (unsigned)((0x100000000ull + d - 1) / d) : 0u; }
 
@@ -616,7 +621,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
                                                                              int max_tiles, int nbig, int nsmall,
                                                                              unsigned mbig, unsigned msmall,
                                                                              PrefillParams p) {
-    static_assert(CPW == 2, "workgroups take one or two chunks");
+    static_assert(CPW >= 1, "workgroups take one or CPW chunks");
     constexpr int H = NBH * 256, KP = H + PF_PAD;
     constexpr bool SPLIT = !XBF16;   // BF16 tokens are exact in the high plane
     __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
@@ -625,7 +630,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     __shared__ __attribute__((aligned(16))) float s_up[PF_WAVES / 2][64][4];
     __shared__ int s_exp[PREFILL_TILE];
     int tile, chunk0, nch;
-    pf_wg_split(max_tiles, PfSplit{nbig, nsmall, mbig, msmall}, tile, chunk0, nch);
+    pf_wg_split<CPW>(max_tiles, PfSplit{nbig, nsmall, mbig, msmall}, tile, chunk0, nch);
     // the tile's tokens, one a lane (lane j: column j), need the tile index only,
     // so their load goes out ahead of the descriptor's
     const int pt = tile_tok[min(tile, max_tiles - 1) * PREFILL_TILE + (threadIdx.x & (PREFILL_TILE - 1))];
@@ -839,19 +844,19 @@ constexpr int pf_cpw_down(int hidden) { return hidden / PF_ROWS_DOWN < PF_CPW_DO
 
 template <int GT, int NBH, bool XBF16>
 static void launch_p1(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
-    // one-chunk workgroups per tile (PF_SMALL_GU, fewer when the tile has fewer
-    // chunks), the rest two-chunk ones
-    static_assert(PF_SMALL_GU % 2 == 0, "an even number of one-chunk workgroups per tile");
+    // per tile, PF_BIG_GU-chunk workgroups over all but at least PF_SMALL_GU
+    // chunks, one-chunk workgroups for the rest
+    constexpr int CB = PF_BIG_GU;
     const int chunks = p.inter / PF_ROWS_GU;   // 4 .. 32
-    const int nsmall = std::min(PF_SMALL_GU, chunks), nbig = (chunks - nsmall) / 2;
+    const int nbig = std::max(chunks - PF_SMALL_GU, 0) / CB, nsmall = chunks - CB * nbig;
     const dim3 grid((nbig + nsmall) * ((p.max_tiles + PF_XCDS - 1) / PF_XCDS * PF_XCDS)), block(64 * PF_WAVES);
     const unsigned mbig = pf_magic(nbig), msmall = pf_magic(nsmall);
     if (ev.armed_a())
-        hipExtLaunchKernelGGL((k_prefill_gate_up<GT, NBH, XBF16, 2>), grid, block, 0, s, ev.a_start, ev.a_stop, 0,
+        hipExtLaunchKernelGGL((k_prefill_gate_up<GT, NBH, XBF16, CB>), grid, block, 0, s, ev.a_start, ev.a_stop, 0,
                               (const int*)p.n_tiles, (const int4*)p.tiles, (const int*)p.tile_tok, (const void*)p.xhi,
                               p.max_tiles, nbig, nsmall, mbig, msmall, p);
     else
-        hipLaunchKernelGGL((k_prefill_gate_up<GT, NBH, XBF16, 2>), grid, block, 0, s, (const int*)p.n_tiles,
+        hipLaunchKernelGGL((k_prefill_gate_up<GT, NBH, XBF16, CB>), grid, block, 0, s, (const int*)p.n_tiles,
                            (const int4*)p.tiles, (const int*)p.tile_tok, (const void*)p.xhi, p.max_tiles, nbig, nsmall,
                            mbig, msmall, p);
 }

@@ -214,3 +214,37 @@ def test_backend_moe_tokens_uses_prefill(oracle_mod, hip):
         worst = max(worst, oracle_mod.max_relative_error(got[t], want))
     print(f"  run_moe_sequence via prefill: max rel err {worst:.3e}", flush=True)
     assert worst <= TIGHT
+
+
+def _sweep_case(seed):
+    rng = np.random.default_rng(5000 + seed)
+    gt, dt = (int(v) for v in rng.choice([11, 12, 13, 14], 2))
+    T = int(rng.choice([5, 17, 33]))
+    H = int(rng.choice([256, 512, 1024]))
+    I = int(rng.choice([256, 512]))
+    E = int(rng.choice([8, 32, 96]))
+    k = int(rng.choice([1, 3, 8]))
+    sh = str(rng.choice(["none", "same", "q6k"]))
+    return gt, dt, T, H, I, E, k, sh, bool(rng.integers(2))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_prefill_sweep(oracle_mod, hip, seed):
+    """Seeded prefill cases with ragged token counts (the route pass stages four
+    tokens a workgroup and cuts 16-token tiles, so 5, 17 and 33 tokens leave
+    partial staging groups and tiles), BF16 or FP32 tokens, every prefill type
+    as gate/up and as down, with no shared expert, one of the routed types or a
+    Q6_K one: every token against the oracle."""
+    gt, dt, T, H, I, E, k, sh, xb = _sweep_case(seed)
+    kinds = {"gate": gt, "up": gt, "down": dt}
+    st = None if sh == "none" else (kinds if sh == "same" else {"gate": 14, "up": 14, "down": 14})
+    layer, host, shared = make_layer(7000 + seed, E, H, I, kinds, shared_types=st)
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((T, H)).astype(np.float32)
+    if xb:
+        X = bf16(X)
+    ids, ws = routing(rng, T, E, k)
+    print(f"prefill sweep {seed}: types {gt}/{dt} T={T} H={H} I={I} E={E} k={k} shared={sh} bf16={xb}", flush=True)
+    got, st_ = run_prefill(layer, X, ids, ws, x_bf16=xb)
+    assert st_ == 0
+    check(oracle_mod, layer, host, shared, X, ids, ws, got, f"sweep {seed}")

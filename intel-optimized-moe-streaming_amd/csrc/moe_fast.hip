@@ -323,6 +323,12 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     const int id_raw = *(id_item ? h.ids + (t * h.top_k + s) : (const int32_t*)xt);
     const float4 xv = *(const float4*)(xt + xi);
     const float4 gi = *(const float4*)((gate_wg ? h.sh_gate_inp : xt) + xi);   // the shared expert's gate vector
+    // the argument-block fields the weight addresses need, awaited together
+    // with the expert id (left to itself the compiler loads the id inside the
+    // branch below, after a round trip of its own for these fields)
+    const uint8_t *p_gate = p.gate, *p_up = p.up, *p_sh_gate = p.sh_gate, *p_sh_up = p.sh_up;
+    const int64_t gate_eb = p.gate_eb, up_eb = p.up_eb;
+    __asm__ volatile("" ::"s"(p_gate), "s"(p_up), "s"(p_sh_gate), "s"(p_sh_up), "s"(gate_eb), "s"(up_eb), "s"(id_raw));
     __builtin_amdgcn_sched_barrier(0);
 
     // The expert slices: routed expert e, the shared expert, or -- for a wave
@@ -330,8 +336,8 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     // Every wave issues the same loads with no branch around them: a
     // conditional load makes the compiler's wait counts conservative at the
     // join, and the token digits below would then wait for the weights.
-    const uint8_t *Gm = h.top_k > 0 ? p.gate : p.sh_gate, *Um = h.top_k > 0 ? p.up : p.sh_up;
-    if (shared) { Gm = p.sh_gate; Um = p.sh_up; }
+    const uint8_t *Gm = h.top_k > 0 ? p_gate : p_sh_gate, *Um = h.top_k > 0 ? p_up : p_sh_up;
+    if (shared) { Gm = p_sh_gate; Um = p_sh_up; }
     bool bad = false;
     bool route_publish = false;   // (ROUTED: the token's first workgroup writes the ids and weights)
     float route_mine = 0.0f;      // (its wave 0: lane r keeps the r-th selected score)
@@ -370,13 +376,13 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
             if (live && !shared) {
                 const int e = s_rank[s];
-                Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
+                Gm = p_gate + (int64_t)e * gate_eb; Um = p_up + (int64_t)e * up_eb;
             }
         }
     } else if (live && !shared) {
         int e = id_raw;
         if (e < 0 || e >= h.n_experts) { bad = true; e = 0; }
-        Gm = p.gate + (int64_t)e * p.gate_eb; Um = p.up + (int64_t)e * p.up_eb;
+        Gm = p_gate + (int64_t)e * gate_eb; Um = p_up + (int64_t)e * up_eb;
     }
 
     const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;

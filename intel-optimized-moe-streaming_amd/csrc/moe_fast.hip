@@ -575,9 +575,25 @@ __device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams
     float w = 0.0f;
     if (!shared) {
         int e = h.ids[t * h.top_k + s];
-        if (e < 0 || e >= h.n_experts) { bad = true; e = 0; }
-        D = p.down + (int64_t)e * p.down_eb;
-        w = bad ? 0.0f : h.weights[t * h.top_k + s];
+        if constexpr (BAL) {
+            // (the balanced form keeps the compiler's order: the form below
+            // measured 17.4 -> 17.8 us for its 16-token launch)
+            if (e < 0 || e >= h.n_experts) { bad = true; e = 0; }
+            D = p.down + (int64_t)e * p.down_eb;
+            w = bad ? 0.0f : h.weights[t * h.top_k + s];
+        } else {
+            // the id, the routing weight and the argument-block fields the
+            // weight address needs in one round trip (the compiler would
+            // otherwise load the routing weight after the id, ahead of the
+            // weight loads: one token 9.78 -> 9.67 us per layer)
+            const float w_raw = h.weights[t * h.top_k + s];
+            const uint8_t* down = p.down;
+            const int64_t down_eb = p.down_eb;
+            __asm__ volatile("" ::"s"(e), "s"(w_raw), "s"(down), "s"(down_eb));
+            if (e < 0 || e >= h.n_experts) { bad = true; e = 0; }
+            D = down + (int64_t)e * down_eb;
+            w = bad ? 0.0f : w_raw;
+        }
     }
 
     // then every weight load, with no branch around them (a conditional load

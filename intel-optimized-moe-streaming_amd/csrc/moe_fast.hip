@@ -141,6 +141,15 @@ __device__ __forceinline__ void act_load(const float* a, int lane, ActRegs<I>& r
     for (int i = 0; i < ActRegs<I>::NQ; ++i) r.q[i] = *(const float4*)(src + 4 * i);
 }
 
+// r.q[g] for a lane-dependent g < RUN / 4, by selects (an indexed read of the
+// register array makes the compiler put it in scratch memory)
+template <int NQ>
+__device__ __forceinline__ float4 pick_group(const float4 (&q)[NQ], int g) {
+    static_assert(NQ == RUN / 4, "one run of float4 groups");
+    const float4 lo = (g & 1) ? q[1] : q[0], hi = (g & 1) ? q[3] : q[2];
+    return (g & 2) ? hi : lo;
+}
+
 template <int I>
 __device__ __forceinline__ void act_digits_lds(const ActRegs<I>& r, int lane, int8_t* planes, float* xs16,
                                                float* sum16) {
@@ -170,10 +179,7 @@ __device__ __forceinline__ void act_digits_lds(const ActRegs<I>& r, int lane, in
         uint32_t lo[V / 4], hi[V / 4];
 #pragma unroll
         for (int j = 0; j < V / 4; ++j) {
-            float4 v = r.q[0];
-#pragma unroll
-            for (int m = 1; m < RUN / 4; ++m)
-                if (g0 + j == m) v = r.q[m];
+            const float4 v = pick_group(r.q, g0 + j);
             const uint2 w = split4(v, inv);
             lo[j] = w.x;
             hi[j] = w.y;
@@ -212,10 +218,7 @@ __device__ __forceinline__ void act_halves_lds(const ActRegs<I>& r, int lane, ui
         uint32_t w[V / 2];
 #pragma unroll
         for (int j = 0; j < V / 4; ++j) {
-            float4 v = r.q[0];
-#pragma unroll
-            for (int m = 1; m < RUN / 4; ++m)
-                if (g0 + j == m) v = r.q[m];
+            const float4 v = pick_group(r.q, g0 + j);
             w[2 * j] = pack_rn16(v.x, v.y);
             w[2 * j + 1] = pack_rn16(v.z, v.w);
         }

@@ -804,9 +804,14 @@ static void launch_a_ipw(const DecodeParams& p, hipStream_t stream, const Kernel
 
 template <int GT, int SGT, int LPR, bool F16G>
 static void launch_a(const DecodeParams& p, hipStream_t stream, const KernelEvents& ev) {
-    if constexpr (!F16G) {
+    if constexpr (!F16G && SGT == GT && GT != T_Q5_K && GT != T_Q6_K) {
         // many tokens: two items a wave, so each wave has twice the weights in
-        // flight behind one prologue (the per-token launches are latency-bound)
+        // flight behind one prologue (the per-token launches are latency-bound).
+        // Only where two items fit in 128 VGPRs (two workgroups a SIMD): Q5_K
+        // and Q6_K items, and a shared expert of another type (both types'
+        // operands live at once), spill 14-53 VGPRs to scratch, and one item a
+        // wave is faster (16 tokens: Q5_K 85 -> 65, Q6_K 96 -> 78, Q4_K with a
+        // Q6_K shared expert 97 -> 78 us per layer)
         if (p.route_scores == nullptr && p.n_tokens >= FAST_A_PAIR_TOKENS) {
             launch_a_ipw<GT, SGT, LPR, F16G, 2>(p, stream, ev);
             return;

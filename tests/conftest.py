@@ -21,6 +21,22 @@ for p in (str(ROOT), str(PKG_DIR)):
 REFERENCE = Path(os.environ.get("MQH_REFERENCE_TREE", "/root/reference"))
 
 
+def build_check_library(src: Path, out: Path, deps: list) -> Path:
+    """Compile a host-side check library (`hipcc -x hip`, host code only runs) when it
+    is missing or older than any of `deps`.  The compiler writes a name of this
+    process's own and the result is renamed into place, so parallel test workers
+    never load a half-written file."""
+    import subprocess
+
+    if not out.exists() or out.stat().st_mtime < max(Path(d).stat().st_mtime for d in deps):
+        out.parent.mkdir(exist_ok=True)
+        tmp = out.with_name(f"{out.stem}.{os.getpid()}{out.suffix}")
+        subprocess.run(["hipcc", "-O2", "-std=c++17", "-fPIC", "-shared", "-x", "hip", "--offload-arch=gfx950",
+                        f"-I{PKG_DIR / 'csrc'}", str(src), "-o", str(tmp)], check=True, capture_output=True)
+        os.replace(tmp, out)
+    return out
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP GPU (gfx950)")
 

@@ -10,12 +10,11 @@ row within the digit error (two int8 digits: |x - x'| <= 1.6e-5 of each
 from __future__ import annotations
 
 import ctypes as C
-import subprocess
 
 import numpy as np
 import pytest
 
-from conftest import PKG_DIR, ROOT
+from conftest import PKG_DIR, ROOT, build_check_library
 
 # |x - (s/254)(254 x0 + x1)| <= s/508 with s = run max / 127, plus FP32 rounding of X = x * 127/max
 DIGIT_ERR = 1.0 / (127 * 508) + 2.0 ** -22
@@ -27,11 +26,7 @@ OUT = ROOT / "tests" / "cpu" / "_build" / "liblanecheck.so"
 @pytest.fixture(scope="module")
 def chk():
     deps = [SRC, PKG_DIR / "csrc" / "kquant_lane.h", PKG_DIR / "csrc" / "kquant_device.h"]
-    if not OUT.exists() or OUT.stat().st_mtime < max(d.stat().st_mtime for d in deps):
-        OUT.parent.mkdir(exist_ok=True)
-        subprocess.run(["hipcc", "-O2", "-std=c++17", "-fPIC", "-shared", "-x", "hip", "--offload-arch=gfx950",
-                        f"-I{PKG_DIR / 'csrc'}", str(SRC), "-o", str(OUT)], check=True, capture_output=True)
-    L = C.CDLL(str(OUT))
+    L = C.CDLL(str(build_check_library(SRC, OUT, deps)))
     L.mqh_cpu_row_dot.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p]
     L.mqh_cpu_row_dot.restype = C.c_float
     L.mqh_cpu_digit_roundtrip.argtypes = [C.c_void_p, C.c_int, C.c_void_p]

@@ -15,12 +15,11 @@ rounding: the decomposition itself is exact, unlike FP16-rounded weights
 from __future__ import annotations
 
 import ctypes as C
-import subprocess
 
 import numpy as np
 import pytest
 
-from conftest import PKG_DIR, ROOT
+from conftest import PKG_DIR, ROOT, build_check_library
 
 SRC = ROOT / "tests" / "cpu" / "frag_check.cpp"
 OUT = ROOT / "tests" / "cpu" / "_build" / "libfragcheck.so"
@@ -29,11 +28,7 @@ OUT = ROOT / "tests" / "cpu" / "_build" / "libfragcheck.so"
 @pytest.fixture(scope="module")
 def chk():
     deps = [SRC, PKG_DIR / "csrc" / "kquant_frag.h", PKG_DIR / "csrc" / "kquant_device.h"]
-    if not OUT.exists() or OUT.stat().st_mtime < max(d.stat().st_mtime for d in deps):
-        OUT.parent.mkdir(exist_ok=True)
-        subprocess.run(["hipcc", "-O2", "-std=c++17", "-fPIC", "-shared", "-x", "hip", "--offload-arch=gfx950",
-                        f"-I{PKG_DIR / 'csrc'}", str(SRC), "-o", str(OUT)], check=True, capture_output=True)
-    L = C.CDLL(str(OUT))
+    L = C.CDLL(str(build_check_library(SRC, OUT, deps)))
     L.mqh_cpu_frag_gemm.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
     L.mqh_cpu_frag_gemm.restype = None
     L.mqh_cpu_frag_cover.argtypes = [C.c_int, C.c_void_p]

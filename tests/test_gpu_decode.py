@@ -495,3 +495,37 @@ def test_balanced_down_kernel(hip, oracle_mod, T, k, sh):
             assert np.array_equal(one[0].view(np.uint32), got[tok].view(np.uint32)), (T, k, sh, tok)
     finally:
         hip.mqh_set_decode_path(old)
+
+
+@pytest.mark.parametrize("gt", [12, 13, 14, 8])
+def test_batched_uniform_types(hip, oracle_mod, gt):
+    """Uniform-type layers (gate/up type gt, down Q6_K, the shared expert of the
+    routed types) at 4 and 16 tokens, where kernel A gives each wave two items
+    (Q4_K, Q8_0) or one (Q5_K, Q6_K: two would spill): every token against the
+    oracle and the generic kernels, and the first and last tokens run alone give
+    the same bits."""
+    H, I, E, K = 2048, 512, 24, 8
+    t = {"gate": gt, "up": gt, "down": 14}
+    layer, host, shared = make_layer(700 + gt, E, H, I, t, shared_types=t)
+    rng = np.random.default_rng(gt)
+    for T in (4, 16):
+        X = rng.standard_normal((T, H)).astype(np.float32)
+        ids = np.stack([rng.permutation(E)[:K] for _ in range(T)])
+        ws = rng.dirichlet(np.ones(K), size=T).astype(np.float32)
+        print(f"batched uniform gate/up type {gt} T={T}", flush=True)
+        old = hip.mqh_set_decode_path(0)
+        try:
+            got, s0 = run(layer, X, ids, ws)
+            hip.mqh_set_decode_path(1)
+            gen, s1 = run(layer, X, ids, ws)
+            hip.mqh_set_decode_path(0)
+            alone = [run(layer, X[i:i + 1], ids[i:i + 1], ws[i:i + 1]) for i in (0, T - 1)]
+        finally:
+            hip.mqh_set_decode_path(old)
+        assert s0 == 0 and s1 == 0 and all(s == 0 for _, s in alone)
+        for tok in range(T):
+            want = oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist())
+            assert oracle_mod.max_relative_error(got[tok], want) <= TOL, (gt, T, tok)
+            assert oracle_mod.max_relative_error(got[tok], gen[tok]) <= TOL, (gt, T, tok)
+        for (one, _), tok in zip(alone, (0, T - 1)):
+            assert np.array_equal(one[0].view(np.uint32), got[tok].view(np.uint32)), (gt, T, tok)

@@ -807,9 +807,9 @@ static void launch_a(const DecodeParams& p, hipStream_t stream, const KernelEven
     if constexpr (!F16G && SGT == GT && GT != T_Q5_K && GT != T_Q6_K) {
         // many tokens: two items a wave, so each wave has twice the weights in
         // flight behind one prologue (the per-token launches are latency-bound).
-        // Only where two items fit in 128 VGPRs (two workgroups a SIMD): Q5_K
-        // and Q6_K items, and a shared expert of another type (both types'
-        // operands live at once), spill 14-53 VGPRs to scratch, and one item a
+        // Only where two items fit in the 128 VGPRs of the kernel's 1024-thread
+        // bound: Q5_K and Q6_K items, and a shared expert of another type (both
+        // types' operands live at once), spill 14-53 VGPRs to scratch, and one item a
         // wave is faster (16 tokens: Q5_K 85 -> 65, Q6_K 96 -> 78, Q4_K with a
         // Q6_K shared expert 97 -> 78 us per layer)
         if (p.route_scores == nullptr && p.n_tokens >= FAST_A_PAIR_TOKENS) {

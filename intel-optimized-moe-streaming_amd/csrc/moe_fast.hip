@@ -687,8 +687,12 @@ __device__ __forceinline__ void down_combine(const DecodeHot& h, const DecodePar
 
 // SDT: the shared expert's down type (its wave takes that code path).
 // Row group bx = blockIdx.x + 8 blockIdx.y of token blockIdx.z (fast_grid).
+// 64 threads a slot: at intermediate 2048 (LPR 32) at most 12 slots fit the
+// digit LDS (fast_supported), so 768 threads, which leaves the FP16 graph's
+// two-type instances the registers they need (a 1024-thread bound caps them at
+// 128 VGPRs and they spill)
 template <int DT, int SDT, int LPR, int NPB, bool F16G>
-__global__ __launch_bounds__(1024) void k_fast_down(const int32_t* ids, float* act, const float* weights, int top_k,
+__global__ __launch_bounds__(LPR == 32 ? 768 : 1024) void k_fast_down(const int32_t* ids, float* act, const float* weights, int top_k,
                                                    int S, int has_shared, int n_experts, int nbx, DecodeParams p) {
     __shared__ SharedB<GeoB<LPR, NPB>::RB> sh;
     const int bx = (int)blockIdx.y * 8 + (int)blockIdx.x;

@@ -529,3 +529,37 @@ def test_batched_uniform_types(hip, oracle_mod, gt):
             assert oracle_mod.max_relative_error(got[tok], gen[tok]) <= TOL, (gt, T, tok)
         for (one, _), tok in zip(alone, (0, T - 1)):
             assert np.array_equal(one[0].view(np.uint32), got[tok].view(np.uint32)), (gt, T, tok)
+
+
+@pytest.mark.parametrize("fp16", [0, 1])
+@pytest.mark.parametrize("routed", [(12, 12), (11, 11), (12, 14), (8, 8)])
+def test_intermediate_2048_twelve_slots(hip, oracle_mod, routed, fp16):
+    """Intermediate 2048 with the most slots kernel B's digit LDS admits there:
+    11 routed experts and a Q6_K shared expert (12 waves, 768 threads, the
+    kernel's launch bound at that width).  Both graphs, 2 tokens, against the
+    oracle and the generic kernels."""
+    gu, dn = routed
+    t = {"gate": gu, "up": gu, "down": dn}
+    sh = {"gate": 14, "up": 14, "down": 14}
+    H, I, E, K = 1024, 2048, 16, 11
+    layer, host, shared = make_layer(300 + gu + dn + fp16, E, H, I, t, shared_types=sh,
+                                     scale=0.002 if fp16 else 0.01)
+    rng = np.random.default_rng(gu + 7 * dn + fp16)
+    X = (rng.standard_normal((2, H)) * (0.05 if fp16 else 1.0)).astype(np.float32)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(2)])
+    ws = rng.dirichlet(np.ones(K), size=2).astype(np.float32)
+    tol = 5e-3 if fp16 else TOL
+    print(f"intermediate 2048, 12 slots, routed={routed} fp16={fp16}", flush=True)
+    old = hip.mqh_set_decode_path(0)
+    try:
+        got, s0 = run(layer, X, ids, ws, fp16=fp16)
+        expect_kernels(hip)
+        hip.mqh_set_decode_path(1)
+        gen, s1 = run(layer, X, ids, ws, fp16=fp16)
+    finally:
+        hip.mqh_set_decode_path(old)
+    assert s0 == 0 and s1 == 0
+    for tok in range(2):
+        want = oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist(), fp16=fp16)
+        assert oracle_mod.max_relative_error(got[tok], want) <= tol, (routed, fp16, tok)
+        assert oracle_mod.max_relative_error(got[tok], gen[tok]) <= tol, (routed, fp16, tok)

@@ -64,10 +64,8 @@ __device__ __forceinline__ float lane_dot(int type, const uint8_t* row, const Ro
                                           bool round_w) {
     const int ppb = ppb_of(type), pb = block_bytes(type);
     float acc = 0.0f;
-    const int nk = NK > 0 ? NK : m.nk;
-    for (int k = 0; k < nk; ++k) {
-        const int p = lp + k * m.L;
-        if (p >= m.P) break;
+    // part p's 32 weights against its 32 values x, in column order
+    auto part = [&](int p, const float* x) {
         const uint8_t* blk = row + (int64_t)(p / ppb) * pb;
         const int sub = p % ppb;
 #pragma unroll
@@ -75,11 +73,23 @@ __device__ __forceinline__ float lane_dot(int type, const uint8_t* row, const Ro
             float w[8];
             decode8_any(type, blk, 4 * sub + q, w);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float wv = round_w ? round16(w[j]) : w[j];
-                const float xv = NK > 0 ? xr[NK > 0 ? k : 0][8 * q + j] : xmem[32 * p + 8 * q + j];
-                acc = fmaf(wv, xv, acc);
-            }
+            for (int j = 0; j < 8; ++j) acc = fmaf(round_w ? round16(w[j]) : w[j], x[8 * q + j], acc);
+        }
+    };
+    if constexpr (NK > 0) {
+        // unrolled, so xr is indexed by constants and stays in registers (a
+        // runtime index puts the array in scratch memory); p grows with k, so
+        // the guard skips exactly the parts past the row's end
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int p = lp + k * m.L;
+            if (p < m.P) part(p, xr[k]);
+        }
+    } else {
+        for (int k = 0; k < m.nk; ++k) {
+            const int p = lp + k * m.L;
+            if (p >= m.P) break;
+            part(p, xmem + 32 * p);
         }
     }
     return acc;

@@ -475,7 +475,11 @@ __host__ __device__ inline void lane_w16_piece(const uint32_t* raw, int k, uint3
             q[i] = (raw[QS + 4 * p + i] >> (4 * r)) & 0x0F0F0F0Fu;
             if constexpr (T == T_Q5_K) q[i] |= ((raw[4 + 4 * p + i] >> (2 * k + r)) & 0x01010101u) << 4;
         }
-        detail::pack16_bytes(q, out, [&](float b) { return detail::sub_rn(detail::mul_rn(d1, b), m1); });
+        // RN(RN(d1 q) - m1) as one fused multiply-add: d1 = d sc has at most 17
+        // significant bits (FP16 d, 6-bit sc), so d1 q (q < 32) has at most 22 and
+        // RN(d1 q) = d1 q; the fused form rounds d1 q - m1 once, as the
+        // reference's subtraction does (one instruction a weight instead of two)
+        detail::pack16_bytes(q, out, [&](float b) { return fmaf(d1, b, -m1); });
     } else if constexpr (T == T_Q6_K) {
         // q - 32 for the 6-bit u: its two's complement is u ^ 32 in bits 2..7 of a
         // byte (low nibble rotated to bits 2..5, the two high bits to 6..7, the

@@ -109,3 +109,21 @@ def test_fp16_graph_lane_weights_bit_exact(chk, oracle_mod, t):
         assert sorted(cols.tolist()) == list(range(256))
         want = oracle_mod.f32_to_f16_bits(oracle_mod.dequant(t, unit, 256))
         np.testing.assert_array_equal(bits, np.asarray(want, np.uint16)[cols])
+
+
+def test_q4k_q5k_fp16_weight_product_exact():
+    """The premise that lets the FP16 graph's Q4_K/Q5_K weights be one fused
+    multiply-add, fmaf(d1, q, -m1) = RN(RN(d1 q) - m1): for every finite FP16 d,
+    every 6-bit scale sc and every 5-bit quant q, d1 = RN32(d sc) equals d sc
+    exactly and RN32(d1 q) equals d1 q exactly (so the reference's first rounding
+    never changes the value).  The min term m1 = RN32(dmin m) is the same product
+    form, covered by the first check."""
+    d = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float64)
+    d = d[np.isfinite(d)]
+    q = np.arange(32, dtype=np.float64)
+    for sc in range(64):
+        d1_64 = d * sc
+        d1 = d1_64.astype(np.float32)
+        assert np.array_equal(d1.astype(np.float64), d1_64), sc
+        prod32 = (d1[:, None] * q[None, :].astype(np.float32)).astype(np.float64)
+        assert np.array_equal(prod32, d1_64[:, None] * q[None, :]), sc

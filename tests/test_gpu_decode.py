@@ -563,3 +563,26 @@ def test_intermediate_2048_twelve_slots(hip, oracle_mod, routed, fp16):
         want = oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist(), fp16=fp16)
         assert oracle_mod.max_relative_error(got[tok], want) <= tol, (routed, fp16, tok)
         assert oracle_mod.max_relative_error(got[tok], gen[tok]) <= tol, (routed, fp16, tok)
+
+
+def test_intermediate_2048_over_slot_limit_falls_back(hip, oracle_mod):
+    """13 slots at intermediate 2048 (12 routed + shared) exceed kernel B's digit
+    LDS: the layer runs on the generic kernels instead, with status 0 and the
+    oracle's result."""
+    t = {"gate": 12, "up": 12, "down": 14}
+    H, I, E, K = 1024, 2048, 16, 12
+    layer, host, shared = make_layer(333, E, H, I, t, shared_types=t)
+    rng = np.random.default_rng(333)
+    X = rng.standard_normal((2, H)).astype(np.float32)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(2)])
+    ws = rng.dirichlet(np.ones(K), size=2).astype(np.float32)
+    print("intermediate 2048, 13 slots (generic fallback)", flush=True)
+    old = hip.mqh_set_decode_path(0)
+    try:
+        got, st = run(layer, X, ids, ws)
+    finally:
+        hip.mqh_set_decode_path(old)
+    assert st == 0
+    for tok in range(2):
+        want = oracle_layer(oracle_mod, layer, host, shared, X[tok], ids[tok].tolist(), ws[tok].tolist())
+        assert oracle_mod.max_relative_error(got[tok], want) <= TOL, tok

@@ -69,7 +69,9 @@ int dequant_k(int type, const uint8_t* src, void* dst, int64_t n, int want_f16);
  *   output = W_down (silu(W_gate input) * (W_up input)),
  * gate/up shaped [intermediate x hidden], down [hidden x intermediate].
  * fp16_graph = 1 rounds to FP16 at the reference's points.  Returns 0, -1,
- * -2, -3, -4 (non-finite output; the whole output is written) or -5. */
+ * -2, -3, -4 or -5.  On -4 (non-finite output) the output rows up to and
+ * including the first non-finite one are written and every later row is left
+ * as the caller had it, as the reference's row loop leaves them. */
 int moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes,
                      int up_type, const uint8_t* up, int64_t up_bytes,
                      int down_type, const uint8_t* down, int64_t down_bytes,
@@ -182,8 +184,10 @@ int mqh_last_route_kernels(void);
  * q, k [heads x key_dim], v [heads x value_dim], beta, gate [heads],
  * output [heads x value_dim].  Host pointers, same signature and codes: -1 for
  * a null pointer or heads outside 1..256, key_dim or value_dim outside
- * 1..1024; -2 when an output is not finite (every row's state is updated and
- * every output written, where the reference stops at the first such row);
+ * 1..1024; -2 when an output is not finite: as in the reference's row loop
+ * (heads major, value rows minor), the state rows up to and including the
+ * first such row are updated, the outputs before it written, and that row's
+ * output and every later row's state and output left as the caller had them;
  * -5 on a HIP failure.  The buffers are staged through HBM: the
  * PCIe-inclusive compatibility path. */
 int moe_delta_heads(float* state, const float* q, const float* k, const float* v, const float* beta,
@@ -233,6 +237,13 @@ int mqh_set_decode_path(int path);
  * moe_quant_expert launched; 0 before the first.  No counterpart in the
  * reference (a profiling aid). */
 int mqh_last_decode_kernels(void);
+
+/* The kernels the calling thread's last mqh_moe_decode, mqh_moe_decode_routed,
+ * mqh_moe_decode_noalloc or moe_quant_expert ran on: 0 the two integer-digit
+ * fast kernels, 1 the generic kernels (forced by mqh_set_decode_path(1), or a
+ * type, shape or slot count the fast kernels do not take); -1 before the
+ * first.  No counterpart in the reference (a test and profiling aid). */
+int mqh_last_decode_path(void);
 
 /* Top-k routing of n_tokens tokens on `stream` (replaces ExpertRouter.route,
  * src/flash_moe/router.py:140-170).  All pointers are device memory:

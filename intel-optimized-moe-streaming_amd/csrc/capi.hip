@@ -3,6 +3,8 @@
 // Host-pointer drop-ins stage their buffers through HBM with a pooled staging
 // context per concurrent call; device-resident entry points validate and
 // enqueue only.
+#include <cmath>
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -30,6 +32,9 @@ int g_decode_path = 0;
 // the number of kernels this thread's last decode launched
 thread_local KernelEvents t_events;
 thread_local int t_last_kernels = 0;
+// kernels this thread's last decode ran on: 0 the fast kernels, 1 the
+// generic ones, -1 before the first
+thread_local int t_last_path = -1;
 // router kernels of this thread's last routed decode (1: the select step ran
 // inside the gate/up kernel, 2: a select kernel of its own)
 thread_local int t_last_route_kernels = 0;
@@ -38,7 +43,11 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t s) {
     const KernelEvents ev = t_events;
     t_events = KernelEvents();
     t_last_kernels = 2;
-    if (g_decode_path != 1 && fast_supported(p)) return launch_decode_fast(p, s, ev);
+    if (g_decode_path != 1 && fast_supported(p)) {
+        t_last_path = 0;
+        return launch_decode_fast(p, s, ev);
+    }
+    t_last_path = 1;
     return launch_decode_generic(p, s, ev);
 }
 
@@ -259,6 +268,10 @@ int moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes, int
     p.sh_scale = (float*)(WS + wl.scale_off); p.act = (float*)(WS + wl.act_off);
     p.S = 1; p.Imax = intermediate;
 
+    // The rows come back into a host copy first: the reference writes output
+    // rows in order and returns -4 at the first non-finite one, leaving every
+    // later row as the caller had it (moe_quant_dot.cpp:207-211).
+    std::vector<float> y(hidden);
     if ((!fresh_ws || zero_words(WS, WS_INIT_WORDS, c->stream) == hipSuccess) &&
         hipMemcpyAsync(W, gate, gate_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
         hipMemcpyAsync(W + off_up, up, up_bytes, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
@@ -266,9 +279,16 @@ int moe_quant_expert(int gate_type, const uint8_t* gate, int64_t gate_bytes, int
         hipMemcpyAsync(IO, input, (size_t)hidden * 4, hipMemcpyHostToDevice, c->stream) == hipSuccess &&
         hipMemcpyAsync(IO + off_id, &route, sizeof(route), hipMemcpyHostToDevice, c->stream) == hipSuccess &&
         launch_decode(p, c->stream) == hipSuccess &&
-        hipMemcpyAsync(output, IO + off_y, (size_t)hidden * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess)
+        hipMemcpyAsync(y.data(), IO + off_y, (size_t)hidden * 4, hipMemcpyDeviceToHost, c->stream) == hipSuccess)
         status = read_and_clear_flags(p.flags, c->stream);
     release_ctx(c);
+    if (status == ST_OK || status == ST_NONFINITE) {
+        int bad = -1;   // the first non-finite row
+        for (int r = 0; r < hidden && bad < 0; ++r)
+            if (!std::isfinite(y[r])) bad = r;
+        std::memcpy(output, y.data(), (size_t)(bad < 0 ? hidden : bad + 1) * 4);
+        status = bad < 0 ? ST_OK : ST_NONFINITE;
+    }
     return status;
 }
 
@@ -296,6 +316,12 @@ int moe_delta_heads(float* state, const float* q, const float* k, const float* v
     float* S = (float*)IO;
     int* fl = (int*)(IO + o_fl);
     const hipStream_t s = c->stream;
+    // The reference walks the rows (head-major, value row minor) and returns -2
+    // at the first row whose output is not finite: that row's state is already
+    // updated, its output is not written, and no later row's state or output
+    // changes (moe_delta.cpp:30-66).  The outputs come back first so the host
+    // knows how many rows to hand back.
+    std::vector<float> out(n_v);
     status = ST_HIP;
     if (zero_words(fl, 3, s) == hipSuccess &&
         hipMemcpyAsync(S, state, n_state * 4, hipMemcpyHostToDevice, s) == hipSuccess &&
@@ -307,10 +333,22 @@ int moe_delta_heads(float* state, const float* q, const float* k, const float* v
         launch_delta_heads(S, (const float*)(IO + o_q), (const float*)(IO + o_k), (const float*)(IO + o_v),
                            (const float*)(IO + o_b), (const float*)(IO + o_g), (float*)(IO + o_out), heads,
                            key_dim, value_dim, fl, s, KernelEvents()) == hipSuccess &&
-        hipMemcpyAsync(state, S, n_state * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
-        hipMemcpyAsync(output, IO + o_out, n_v * 4, hipMemcpyDeviceToHost, s) == hipSuccess) {
+        hipMemcpyAsync(out.data(), IO + o_out, n_v * 4, hipMemcpyDeviceToHost, s) == hipSuccess) {
         status = read_and_clear_flags(fl, s);
-        if (status == ST_NONFINITE) status = -2;   // moe_delta.cpp:65
+        if (status == ST_OK || status == ST_NONFINITE) {
+            int64_t rows = n_v;   // the first non-finite row, or all of them
+            for (int64_t r = 0; r < n_v; ++r)
+                if (!std::isfinite(out[r])) { rows = r; break; }
+            // state rows 0 .. rows (inclusive when a row failed), outputs 0 .. rows - 1
+            const int64_t state_rows = rows < n_v ? rows + 1 : n_v;
+            if (hipMemcpyAsync(state, S, state_rows * key_dim * 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess) {
+                status = ST_HIP;
+            } else {
+                std::memcpy(output, out.data(), (size_t)rows * 4);
+                status = rows < n_v ? -2 : ST_OK;   // moe_delta.cpp:65
+            }
+        }
     }
     release_ctx(c);
     return status;
@@ -508,6 +546,7 @@ int mqh_moe_decode_routed(int gate_type, const void* gate, int up_type, const vo
         const KernelEvents ev = t_events;
         t_events = KernelEvents();
         t_last_kernels = 2;
+        t_last_path = 0;
         t_last_route_kernels = 1;
         return launch_decode_fast(p, s, ev) == hipSuccess ? ST_OK : ST_HIP;
     }
@@ -581,6 +620,8 @@ int mqh_profile_next_decode(void* a_start, void* a_stop, void* b_start, void* b_
 }
 
 int mqh_last_decode_kernels(void) { return t_last_kernels; }
+
+int mqh_last_decode_path(void) { return t_last_path; }
 
 int mqh_route(const float* x, int n_tokens, int hidden, const float* gate_weights, int n_experts, int top_k,
               float* scores, int32_t* ids, float* weights, void* stream) {

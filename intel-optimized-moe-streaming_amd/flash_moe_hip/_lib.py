@@ -34,6 +34,7 @@ EXPORTS = (
     "mqh_moe_prefill",
     "mqh_set_decode_path",
     "mqh_last_decode_kernels",
+    "mqh_last_decode_path",
     "mqh_read_floor",
     "mqh_route",
     "mqh_profile_next_decode",
@@ -123,6 +124,8 @@ def _declare(lib: C.CDLL) -> C.CDLL:
     lib.mqh_set_decode_path.restype = _I
     lib.mqh_last_decode_kernels.argtypes = []
     lib.mqh_last_decode_kernels.restype = _I
+    lib.mqh_last_decode_path.argtypes = []
+    lib.mqh_last_decode_path.restype = _I
     lib.mqh_read_floor.argtypes = [_P, C.c_int64, _P, _P, _P, _P]
     lib.mqh_read_floor.restype = _I
     lib.mqh_route.argtypes = [_P, _I, _I, _P, _I, _I, _P, _P, _P, _P]

@@ -13,6 +13,18 @@ plus two fused entry points that ``flash_moe_hip.moe_layer`` prefers:
   moe_layer(layer, activation, ids, weights)      every routed expert + shared, one launch
   moe_tokens(layer, activations, ids, weights)    the same for a batch of tokens
 
+Numerics.  The reference's decode calls its native expert in the FP16 graph
+(``native_expert.py:33-34``, reached through ``backend_ov.py:373-377``), so
+``fp16_graph`` defaults to 1: ``forward``, ``forward_batch`` and ``moe_layer``
+round to FP16 at the points of ``moe_quant_dot.cpp:189-211`` (the shared
+expert runs the FP32 graph, as the reference's NumPy shared expert does).
+``fp16_graph=0`` gives the FP32 graph.  ``moe_tokens`` (the prompt path) runs
+the grouped prefill kernels whenever they cover the layer, in either setting:
+the reference's prompt path is its OpenVINO expert graph
+(``backend_ov.py:210-237, 407-431``), not the native FP16 graph, and the
+prefill kernels' exact FP16 products with FP32 accumulation stay within 1e-4
+of the FP32 graph.
+
 All arithmetic runs in the HIP kernels; results come back as NumPy FP32 like
 the reference backend's.  Each call stages its inputs through one pinned host
 buffer (one host-to-device copy) and returns after one synchronisation, which
@@ -32,7 +44,7 @@ from .moe_gpu import MoeRunner
 
 
 class HipExpertBackend:
-    def __init__(self, layers: dict[int, ExpertLayer], fp16_graph: int = 0, device=None, expert_workers: int = 4):
+    def __init__(self, layers: dict[int, ExpertLayer], fp16_graph: int = 1, device=None, expert_workers: int = 4):
         import torch
 
         if not torch.cuda.is_available():
@@ -130,11 +142,11 @@ class HipExpertBackend:
 
     def moe_tokens(self, layer: int, activations, ids, weights, include_shared: bool = True) -> np.ndarray:
         """A prompt's tokens through the layer (run_moe_sequence): the grouped
-        prefill kernels when they cover the layer (FP32 graph, more than one
-        token), else the fused decode kernels."""
+        prefill kernels when they cover the layer (more than one token, any
+        ``fp16_graph``), else the fused decode kernels in the backend's graph."""
         L = self.layers[layer]
         x, tid, tw = self._stage(activations, L.hidden, ids, weights)
-        if self.fp16_graph == 0 and x.shape[0] > 1 and self.runner.prefill_supported(L):
+        if x.shape[0] > 1 and self.runner.prefill_supported(L):
             y = self.runner.prefill(L, x, tid, tw, use_shared=include_shared)
         else:
             y = self.runner.decode(L, x, tid, tw, fp16_graph=self.fp16_graph, use_shared=include_shared)

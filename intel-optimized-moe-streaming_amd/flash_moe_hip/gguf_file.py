@@ -224,10 +224,20 @@ class GGUFFile:
         return dict(sorted(out.items()))
 
 
-def layer_host_tensors(gf: GGUFFile, layer: int) -> dict:
+def layer_host_tensors(gf: GGUFFile, layer: int, gate_dtype=np.float16) -> dict:
     """The host-side pieces of one MoE layer: stacked expert bytes (zero-copy
     views), types and shape, the shared expert and the router weights when the
-    file has them.  Raises if the three stacks disagree in shape."""
+    file has them.  Raises if the three stacks disagree in shape.
+
+    The two gate vectors carry the reference's storage rounding, so the device
+    routes and gates exactly as the reference's host code does:
+    ``ffn_gate_inp`` is rounded to ``gate_dtype`` (FP16, the default of
+    ``routers_from_gguf``) and promoted to FP32 (src/flash_moe/router.py:51-59,
+    99, 136; built with that default by model.py:219-222), and
+    ``ffn_gate_inp_shexp`` is rounded to FP16 and promoted, as
+    ``SharedExpert._load`` stores every F32/F16 tensor (shared_expert.py:147,
+    173).  In FP16 storage a close pair of experts can swap
+    (router.py:101-104), so the rounding is part of the routing result."""
     name = f"blk.{layer}.ffn_{{}}_exps.weight"
     ts = {r: gf.tensors[name.format(r)] for r in ("gate", "up", "down")}
     g, u, d = ts["gate"], ts["up"], ts["down"]
@@ -243,7 +253,9 @@ def layer_host_tensors(gf: GGUFFile, layer: int) -> dict:
         st = {r: gf.tensors[sh.format(r)] for r in ("gate", "up", "down")}
         sh_inter = int(st["gate"].dims[1])
         gi_name = f"blk.{layer}.ffn_gate_inp_shexp.weight"
-        gate_inp = gf.float_array(gi_name).reshape(-1) if gi_name in gf.tensors else None
+        gate_inp = None
+        if gi_name in gf.tensors:
+            gate_inp = gf.float_array(gi_name).reshape(-1).astype(np.float16).astype(np.float32)
         out["shared"] = {"gate": gf.raw(st["gate"].name), "up": gf.raw(st["up"].name),
                          "down": gf.raw(st["down"].name),
                          "types": {r: t.ggml_type for r, t in st.items()},
@@ -251,14 +263,16 @@ def layer_host_tensors(gf: GGUFFile, layer: int) -> dict:
     router = f"blk.{layer}.ffn_gate_inp.weight"
     if router in gf.tensors:
         w = gf.float_array(router)            # NumPy shape (n_experts, hidden)
+        w = w.astype(np.dtype(gate_dtype)).astype(np.float32)
         out["router_weights"] = np.ascontiguousarray(w.T)   # [hidden x n_experts]
     return out
 
 
-def load_expert_layer(gf: GGUFFile, layer: int, device="cuda"):
-    """One MoE layer of the file resident in HBM (``ExpertLayer``)."""
+def load_expert_layer(gf: GGUFFile, layer: int, device="cuda", gate_dtype=np.float16):
+    """One MoE layer of the file resident in HBM (``ExpertLayer``), its router
+    weights stored as ``gate_dtype`` (the ``ExpertRouter`` default: FP16)."""
     from .layer_store import ExpertLayer
 
-    h = layer_host_tensors(gf, layer)
+    h = layer_host_tensors(gf, layer, gate_dtype=gate_dtype)
     return ExpertLayer.from_host(h["tensors"], h["types"], h["n_experts"], h["hidden"], h["intermediate"],
                                  shared=h["shared"], router_weights=h["router_weights"], device=device)

@@ -15,7 +15,13 @@ shared expert inside the same fused launch as the routed experts.
 (shared_expert.py:200-251), or ``None`` for a layer without a shared expert.
 The reference instead multiplies FP32 copies of FP16-dequantized weights
 (shared_expert.py:141-149): the two differ by at most one FP16 rounding per
-weight.
+weight.  ``gate_inp`` is stored as the reference stores it: rounded to FP16,
+then promoted to FP32 (shared_expert.py:147, 173).
+
+The three matrices must be in a quantized type the kernels decode (Q3_K,
+Q4_K, Q5_K, Q6_K, Q8_0, IQ4_NL).  The reference also accepts F32/F16 shared
+matrices (shared_expert.py:165-173); this class rejects them in the
+constructor with a ``ValueError`` naming the tensor.
 """
 from __future__ import annotations
 
@@ -24,6 +30,7 @@ import os
 import numpy as np
 
 from .layer_store import SharedWeights, _to_device_bytes
+from .quant_types import DEVICE_TYPES, name_of, tensor_bytes
 
 SHARED_ROLES = {
     "gate_inp": "ffn_gate_inp_shexp.weight",
@@ -50,6 +57,25 @@ def _reader_tensors(gguf_path, reader) -> dict:
     return {t.name: t for t in reader.tensors}
 
 
+def _quantized_bytes(tensor, name: str, shape: tuple[int, int]) -> np.ndarray:
+    """The raw block bytes of a quantized shared matrix of (rows, cols) =
+    ``shape``; a type the kernels do not decode (F32, F16, ...) or a byte count
+    that does not fit the shape raises ``ValueError`` here rather than at the
+    first forward."""
+    t = int(tensor.tensor_type)
+    if t not in DEVICE_TYPES:
+        raise ValueError(f"{name}: ggml type {name_of(t)} is not a quantized type the shared-expert kernels "
+                         f"decode (Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, IQ4_NL)")
+    data = np.asarray(tensor.data)
+    if data.dtype != np.uint8:
+        raise ValueError(f"{name}: expected the raw block bytes (uint8), got {data.dtype}")
+    raw = np.ascontiguousarray(data).reshape(-1)
+    want = tensor_bytes(t, *shape)
+    if raw.size != want:
+        raise ValueError(f"{name}: {raw.size} bytes, expected {want} for {name_of(t)} {shape}")
+    return raw
+
+
 class SharedExpert:
     def __init__(self, gguf_path, num_layers: int, hidden_size: int, intermediate_size: int,
                  dequant_fn=None, reader=None, *, device=None):
@@ -74,10 +100,13 @@ class SharedExpert:
             gi = tmap.get(f"blk.{layer}.{SHARED_ROLES['gate_inp']}")
             gate_inp = None
             if gi is not None:
-                gate_inp = torch.from_numpy(np.array(gi.data, dtype=np.float32).reshape(-1)).to(dev)
+                g16 = np.asarray(gi.data, dtype=np.float32).reshape(-1).astype(np.float16)
+                gate_inp = torch.from_numpy(g16.astype(np.float32)).to(dev)
+            mats = {r: _quantized_bytes(ts[r], f"blk.{layer}.{SHARED_ROLES[r]}",
+                                        (inter, self.hidden_size) if r != "down" else (self.hidden_size, inter))
+                    for r in ("gate", "up", "down")}
             self.layers[layer] = SharedWeights(
-                *(_to_device_bytes(np.asarray(ts[r].data, dtype=np.uint8).reshape(-1), dev)
-                  for r in ("gate", "up", "down")),
+                *(_to_device_bytes(mats[r], dev) for r in ("gate", "up", "down")),
                 types={r: int(ts[r].tensor_type) for r in ("gate", "up", "down")},
                 intermediate=inter, gate_inp=gate_inp)
         if self.missing:

@@ -131,12 +131,14 @@ def dequant(ggml_type: int, raw, n: int | None = None, want_f16: bool = False) -
 
 
 def moe_quant_expert(tensors: dict, kinds: dict, x, hidden: int, intermediate: int,
-                     fp16_graph: int = 0, avx2: bool = False):
+                     fp16_graph: int = 0, avx2: bool = False, out=None):
     """(status, y) with the argument meaning of ``moe_quant_expert``
     (moe_quant_dot.cpp:171-214).  ``tensors`` maps gate/up/down to raw bytes.
     ``avx2`` runs the AVX2 row dot of ``kquant_avx2.c`` (the reference's
     direct Q3_K/Q6_K form, moe_quant_dot.cpp:23-169): the same result bit for
-    bit, the CPU baseline of the bench."""
+    bit, the CPU baseline of the bench.  ``out`` (FP32 [hidden], written in
+    place) keeps the rows a -4 return leaves untouched; by default a zeroed
+    array."""
     arrays = [np.ascontiguousarray(np.frombuffer(bytes(tensors[k]), np.uint8) if
                                    isinstance(tensors[k], (bytes, bytearray)) else tensors[k],
                                    dtype=np.uint8).reshape(-1) for k in ("gate", "up", "down")]
@@ -144,7 +146,10 @@ def moe_quant_expert(tensors: dict, kinds: dict, x, hidden: int, intermediate: i
     for name, raw in zip(("gate", "up", "down"), arrays):
         args.extend((int(kinds[name]), raw.ctypes.data, raw.nbytes))
     xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
-    out = np.zeros(hidden, np.float32)
+    if out is None:
+        out = np.zeros(hidden, np.float32)
+    if out.dtype != np.float32 or out.size != hidden or not out.flags.c_contiguous:
+        raise ValueError("out must be a contiguous FP32 array of hidden values")
     fn = lib().oracle_moe_quant_expert_avx2 if avx2 else lib().oracle_moe_quant_expert
     rc = fn(*args, xv.ctypes.data, int(hidden), int(intermediate), out.ctypes.data, int(fp16_graph))
     return rc, out
@@ -159,7 +164,7 @@ def expert_forward(tensors, kinds, x, hidden, intermediate, fp16_graph=0, avx2=F
 
 # ------------------------------------------------------------ Python semantics
 
-def _delta_call(fn, state: np.ndarray, q, k, v, beta, gate):
+def _delta_call(fn, state: np.ndarray, q, k, v, beta, gate, out=None):
     if state.dtype != np.float32 or not state.flags.c_contiguous or state.ndim != 3:
         raise ValueError("state must be a contiguous FP32 [heads, value_dim, key_dim] array")
     nv, dv, dk = state.shape
@@ -167,16 +172,20 @@ def _delta_call(fn, state: np.ndarray, q, k, v, beta, gate):
     shapes = [(nv, dk), (nv, dk), (nv, dv), (nv,), (nv,)]
     if any(a.shape != s_ for a, s_ in zip(arrs, shapes)):
         raise ValueError("DeltaNet input shape mismatch")
-    out = np.zeros((nv, dv), np.float32)
+    if out is None:
+        out = np.zeros((nv, dv), np.float32)
+    if out.dtype != np.float32 or out.shape != (nv, dv) or not out.flags.c_contiguous:
+        raise ValueError("out must be a contiguous FP32 [heads, value_dim] array")
     rc = fn(state.ctypes.data, *[a.ctypes.data for a in arrs], out.ctypes.data, nv, dk, dv)
     return rc, out
 
 
-def delta_heads(state: np.ndarray, q, k, v, beta, gate):
+def delta_heads(state: np.ndarray, q, k, v, beta, gate, out=None):
     """``moe_delta_heads`` (cpp/moe_delta.cpp:18-69): one delta-rule step of every
     head, ``state`` [heads, value_dim, key_dim] FP32 updated in place.  Returns
-    (status, output [heads, value_dim])."""
-    return _delta_call(lib().oracle_delta_heads, state, q, k, v, beta, gate)
+    (status, output [heads, value_dim]); ``out``, when given, is written in
+    place (the rows a -2 return leaves untouched keep their values)."""
+    return _delta_call(lib().oracle_delta_heads, state, q, k, v, beta, gate, out)
 
 
 def reference_delta_lib():
@@ -189,12 +198,12 @@ def reference_delta_lib():
     return L
 
 
-def reference_delta_heads(state: np.ndarray, q, k, v, beta, gate):
+def reference_delta_heads(state: np.ndarray, q, k, v, beta, gate, out=None):
     """Like :func:`delta_heads`, through the reference's own compiled kernel."""
     L = reference_delta_lib()
     if L is None:
         raise FileNotFoundError(f"{REF_DELTA_PATH} is not built (make -C oracle ref)")
-    return _delta_call(L.moe_delta_heads, state, q, k, v, beta, gate)
+    return _delta_call(L.moe_delta_heads, state, q, k, v, beta, gate, out)
 
 
 def delta_step_numpy(S: np.ndarray, q, k, v, beta: float, gate: float) -> np.ndarray:

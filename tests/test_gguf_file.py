@@ -152,9 +152,38 @@ def test_expert_layer_slicing(tmp_path):
     sh = h["shared"]
     assert sh["types"] == {"gate": 14, "up": 14, "down": 14} and sh["intermediate"] == 256
     assert all(np.array_equal(sh[r], w) for r, w in zip(("gate", "up", "down"), want["sh"]))
-    assert np.array_equal(sh["gate_inp"], want["gate_inp_sh"])
+    # stored as the reference stores them: FP16-rounded, promoted to FP32
+    assert np.array_equal(sh["gate_inp"], want["gate_inp_sh"].astype(np.float16).astype(np.float32))
+    assert not np.array_equal(sh["gate_inp"], want["gate_inp_sh"])   # the file's F32 values do change
     assert h["router_weights"].shape == (256, 4)
     assert np.array_equal(h["router_weights"], want["router"].astype(np.float32).T)
+
+
+def test_f32_router_gate_is_stored_as_the_router_stores_it(tmp_path):
+    """An F32 ffn_gate_inp is rounded to the router's gate_dtype (FP16 by
+    default, router.py:51-59, 99, 136) and promoted: the weights the device
+    routes with equal ExpertRouter.from_gguf_tensor's gate_weights bit for bit,
+    for the FP16 default and for gate_dtype=float32 (no rounding)."""
+    from flash_moe_hip.router import ExpertRouter
+
+    from flash_moe_hip.synthetic import random_stack
+
+    rng = np.random.default_rng(9)
+    E, H = 8, 256
+    r32 = rng.standard_normal((E, H)).astype(np.float32) * 0.02
+    w = random_stack(rng, 12, E, 256, H).tobytes()        # [256 x 256] Q4_K per expert, every role
+    tensors = [("blk.1.ffn_gate_exps.weight", (H, 256, E), 12, w),
+               ("blk.1.ffn_up_exps.weight", (H, 256, E), 12, w),
+               ("blk.1.ffn_down_exps.weight", (256, H, E), 12, w),
+               ("blk.1.ffn_gate_inp.weight", (H, E), 0, r32.tobytes())]
+    gf = GGUFFile(write(tmp_path, pack_gguf([], tensors)))
+    tm = gf.tensor_map()
+    for dt in (np.float16, np.float32):
+        h = layer_host_tensors(gf, 1, gate_dtype=dt)
+        ref = ExpertRouter.from_gguf_tensor(tm["blk.1.ffn_gate_inp.weight"], H, E, 2, gate_dtype=dt)
+        assert h["router_weights"].dtype == np.float32
+        assert np.array_equal(h["router_weights"], ref.gate_weights)
+    assert not np.array_equal(layer_host_tensors(gf, 1)["router_weights"], r32.T)
 
 
 def test_mismatched_expert_stacks_rejected(tmp_path):
@@ -192,7 +221,8 @@ def test_layer_from_gguf_decodes_like_the_oracle(tmp_path, oracle_mod, hip):
     router = ExpertRouter(512, 8, top_k=4, gate_weights=layer.router_weights)
     host = {r: want[r] for r in ("gate", "up", "down")}
     shared = {"gate": want["sh"][0], "up": want["sh"][1], "down": want["sh"][2],
-              "types": {"gate": 14, "up": 14, "down": 14}, "intermediate": 512, "gate_inp": want["gate_inp_sh"]}
+              "types": {"gate": 14, "up": 14, "down": 14}, "intermediate": 512,
+              "gate_inp": want["gate_inp_sh"].astype(np.float16).astype(np.float32)}
     X = rng.standard_normal((3, 512)).astype(np.float32)
     ids, ws = router.route_batch(X)
     runner = MoeRunner()
@@ -204,3 +234,96 @@ def test_layer_from_gguf_decodes_like_the_oracle(tmp_path, oracle_mod, hip):
         err = oracle_mod.max_relative_error(y[t], ref)
         print(f"  gguf layer token {t}: max rel err {err:.3e}", flush=True)
         assert err <= TOL
+
+
+def near_tie_file(tmp_path, rng, E=16, H=512, I=256, k=4, a=7, b=12, top=(2, 5, 9)):
+    """A layer file whose F32 ffn_gate_inp ranks expert b above expert a for
+    the returned token, while the same weights rounded to FP16 rank a above b;
+    a and b sit at ranks k and k+1 (the k-1 experts of ``top`` score far
+    above, the rest far below), so the two storages select different sets.
+
+    The token has x[0] = x[1] = 4; a and b share every other weight, so
+    s(b) - s(a) = 4 (2^-12 - 2^-13) > 0 in FP32, while FP16 rounds row a's
+    1 + 2^-11 + 2^-14 up to 1 + 2^-10 and row b's 1 + 2^-12 and
+    1 + 2^-11 - 2^-14 down to 1, so s16(a) - s16(b) = 4 * 2^-10 > 0."""
+    from flash_moe_hip.synthetic import random_stack
+
+    x = rng.standard_normal(H).astype(np.float32)
+    x[0] = x[1] = 4.0
+    W = (rng.standard_normal((E, H)) * 0.01).astype(np.float32)
+    sgn = np.sign(x).astype(np.float32)
+    for e in top:
+        W[e] = 0.08 * sgn + (rng.standard_normal(H) * 0.005).astype(np.float32)
+        W[e, :2] = 1.0
+    base = 0.05 * sgn
+    W[a], W[b] = base, base
+    W[a, 0], W[a, 1] = 1.0, 1.0 + 2.0 ** -11 + 2.0 ** -14
+    W[b, 0], W[b, 1] = 1.0 + 2.0 ** -12, 1.0 + 2.0 ** -11 - 2.0 ** -14
+    g, u, d = (random_stack(rng, t, E, *shape) for t, shape in ((12, (I, H)), (12, (I, H)), (14, (H, I))))
+    sg, su, sd = (random_stack(rng, 14, 1, *shape) for shape in ((I, H), (I, H), (H, I)))
+    gi = (rng.standard_normal(H) * 0.02).astype(np.float32)
+    tensors = [("blk.0.ffn_gate_exps.weight", (H, I, E), 12, g.tobytes()),
+               ("blk.0.ffn_up_exps.weight", (H, I, E), 12, u.tobytes()),
+               ("blk.0.ffn_down_exps.weight", (I, H, E), 14, d.tobytes()),
+               ("blk.0.ffn_gate_shexp.weight", (H, I), 14, sg.tobytes()),
+               ("blk.0.ffn_up_shexp.weight", (H, I), 14, su.tobytes()),
+               ("blk.0.ffn_down_shexp.weight", (I, H), 14, sd.tobytes()),
+               ("blk.0.ffn_gate_inp_shexp.weight", (H,), 0, gi.tobytes()),
+               ("blk.0.ffn_gate_inp.weight", (H, E), 0, W.tobytes())]
+    path = write(tmp_path, pack_gguf([], tensors), "near_tie.gguf")
+    host = {"gate": g, "up": u, "down": d}
+    shared = {"gate": sg, "up": su, "down": sd, "types": {"gate": 14, "up": 14, "down": 14}, "intermediate": I,
+              "gate_inp": gi.astype(np.float16).astype(np.float32)}   # as SharedExpert._load stores it
+    return path, x, W, host, shared
+
+
+def test_near_tie_file_flips_under_fp16_storage(tmp_path):
+    """The construction above does what it says, on the host: the FP32 and the
+    FP16 router of the file choose different expert sets for the token."""
+    from flash_moe_hip.router import routers_from_gguf
+
+    path, x, W, _, _ = near_tie_file(tmp_path, np.random.default_rng(31))
+    tm = GGUFFile(path).tensor_map()
+    r16 = routers_from_gguf(tm, 1, 512, 16, 4)[0]
+    r32 = routers_from_gguf(tm, 1, 512, 16, 4, gate_dtype=np.float32)[0]
+    ids16, ids32 = r16.route(x)[0], r32.route(x)[0]
+    assert ids16[:3] == ids32[:3] and set(ids16[:3]) == {2, 5, 9}
+    assert ids16[3] == 7 and ids32[3] == 12
+
+
+@pytest.mark.gpu
+def test_device_routes_a_file_layer_as_the_reference_router(tmp_path, oracle_mod, hip):
+    """A GGUF layer whose F32 router gate flips a near-tie under FP16 storage:
+    the device router (mqh_moe_decode_routed over the uploaded gate) selects
+    exactly the experts, in the order, of the reference's default
+    ExpertRouter built by routers_from_gguf (FP16 storage), not those of the
+    unrounded FP32 gate; outputs within 1e-3 of the oracle's layer."""
+    import torch
+
+    from flash_moe_hip.gguf_file import load_expert_layer
+    from flash_moe_hip.moe_gpu import MoeRunner
+    from flash_moe_hip.router import routers_from_gguf
+    from test_gpu_decode import TOL, oracle_layer
+
+    rng = np.random.default_rng(31)
+    path, x, W, host, shared = near_tie_file(tmp_path, rng)
+    gf = GGUFFile(path)
+    layer = load_expert_layer(gf, 0, device="cuda")
+    router = routers_from_gguf(gf.tensor_map(), 1, 512, 16, 4)[0]
+    X = np.stack([x] + [rng.standard_normal(512).astype(np.float32) for _ in range(2)])
+    runner = MoeRunner()
+    print("near-tie GGUF layer: routed decode of 3 tokens", flush=True)
+    y, ids, wts = runner.decode_routed(layer, torch.from_numpy(X).cuda(), 4)
+    torch.cuda.synchronize()
+    assert runner.status() == 0
+    y, ids, wts = y.cpu().numpy(), ids.cpu().numpy(), wts.cpu().numpy()
+    assert sorted(ids[0].tolist()[:3]) == [2, 5, 9] and ids[0, 3] == 7
+    for t in range(3):
+        r_ids, r_w = router.route(X[t])
+        assert ids[t].tolist() == r_ids, f"token {t}: device {ids[t].tolist()} reference {r_ids}"
+        np.testing.assert_allclose(wts[t], r_w, rtol=0, atol=2e-6)
+        ref = oracle_layer(oracle_mod, layer, host, shared, X[t], r_ids, r_w)
+        err = oracle_mod.max_relative_error(y[t], ref)
+        print(f"  token {t}: ids {r_ids} max rel err {err:.3e}", flush=True)
+        assert err <= TOL
+    assert 12 not in ids[0].tolist()

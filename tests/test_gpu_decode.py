@@ -181,7 +181,7 @@ def test_fp16_graph_routed_experts(hip, oracle_mod):
     want = oracle_layer(oracle_mod, layer, host, shared, x, ids, ws, fp16=1)
     err = oracle_mod.max_relative_error(got[0], want)
     print(f"fp16 graph max rel err {err:.3e}", flush=True)
-    assert err <= 5e-3
+    assert err <= TOL
 
 
 @pytest.mark.parametrize("types", [(12, 14), (11, 11), (13, 12), (14, 14), (12, 13), (11, 14)])
@@ -424,9 +424,9 @@ def test_fp16_graph_fast_kernels(hip, oracle_mod, types):
     integer-decode kernels' FP16 mode: every routed weight decoded with the
     reference's arithmetic and rounded to FP16, FP16 activations, FP32 sums, and
     the rounding points of moe_quant_dot.cpp:189-211; the shared expert in the
-    FP32 graph.  Against the oracle's FP16 graph (the reference's own check
-    allows 0.005, test_optimized_inference.py:231-290) and against the generic
-    kernels' FP16 graph, 3 tokens at several shapes, scales as the reference's
+    FP32 graph.  Against the oracle's FP16 graph at the north star's 1e-3 (the
+    reference's own check allows 0.005, test_optimized_inference.py:231-290;
+    observed ~1e-4) and against the generic kernels' FP16 graph, 3 tokens at several shapes, scales as the reference's
     FP16-graph check (d ~ 0.002, x ~ 0.05)."""
     gu, dn = types
     t = {"gate": gu, "up": gu, "down": dn}
@@ -449,8 +449,8 @@ def test_fp16_graph_fast_kernels(hip, oracle_mod, types):
             assert st == 0
             for tok in range(3):
                 err = oracle_mod.max_relative_error(got[path][tok], want[tok])
-                assert err <= 5e-3, (types, H, I, path, tok, err)
-        assert oracle_mod.max_relative_error(got[0], got[1]) <= 5e-3
+                assert err <= TOL, (types, H, I, path, tok, err)
+        assert oracle_mod.max_relative_error(got[0], got[1]) <= TOL
 
 
 @pytest.mark.parametrize("T,k,sh", [(8, 4, "same"), (8, 8, "q6k"), (16, 8, "same"), (16, 4, "q6k"), (16, 2, "same"),
@@ -548,14 +548,16 @@ def test_intermediate_2048_twelve_slots(hip, oracle_mod, routed, fp16):
     X = (rng.standard_normal((2, H)) * (0.05 if fp16 else 1.0)).astype(np.float32)
     ids = np.stack([rng.permutation(E)[:K] for _ in range(2)])
     ws = rng.dirichlet(np.ones(K), size=2).astype(np.float32)
-    tol = 5e-3 if fp16 else TOL
+    tol = TOL
     print(f"intermediate 2048, 12 slots, routed={routed} fp16={fp16}", flush=True)
     old = hip.mqh_set_decode_path(0)
     try:
         got, s0 = run(layer, X, ids, ws, fp16=fp16)
         expect_kernels(hip)
+        assert hip.mqh_last_decode_path() == 0   # the 12-slot maximum runs on the fast kernels
         hip.mqh_set_decode_path(1)
         gen, s1 = run(layer, X, ids, ws, fp16=fp16)
+        assert hip.mqh_last_decode_path() == 1
     finally:
         hip.mqh_set_decode_path(old)
     assert s0 == 0 and s1 == 0
@@ -580,6 +582,7 @@ def test_intermediate_2048_over_slot_limit_falls_back(hip, oracle_mod):
     old = hip.mqh_set_decode_path(0)
     try:
         got, st = run(layer, X, ids, ws)
+        assert hip.mqh_last_decode_path() == 1   # the generic kernels ran, not the fast ones
     finally:
         hip.mqh_set_decode_path(old)
     assert st == 0

@@ -85,6 +85,19 @@ def test_non_finite_output_is_reported(oracle_mod):
     rc = lib.moe_delta_heads(state.ctypes.data, q.ctypes.data, k.ctypes.data, v.ctypes.data, beta.ctypes.data,
                              gate.ctypes.data, out.ctypes.data, nv, dk, dv)
     assert rc == -2
+    # the reference's side effects (moe_delta.cpp:30-66), which the oracle pins:
+    # state rows up to and including the bad one updated, outputs before it
+    # written, everything after it as the caller left it -- bit for bit
+    st0 = (rng.standard_normal((nv, dv, dk)) * 0.01).astype(np.float32)
+    st_o, out_o = st0.copy(), np.full((nv, dv), 7.0, np.float32)
+    assert oracle_mod.delta_heads(st_o, q, k, v, beta, gate, out=out_o)[0] == -2
+    st_g, out_g = st0.copy(), np.full((nv, dv), 7.0, np.float32)
+    rc = lib.moe_delta_heads(st_g.ctypes.data, q.ctypes.data, k.ctypes.data, v.ctypes.data, beta.ctypes.data,
+                             gate.ctypes.data, out_g.ctypes.data, nv, dk, dv)
+    assert rc == -2
+    np.testing.assert_array_equal(st_g, st_o)
+    np.testing.assert_array_equal(out_g, out_o)
+    np.testing.assert_array_equal(out_g.reshape(-1)[2 * dv + 5:], 7.0)
     with pytest.raises(RuntimeError, match="status -2"):
         NativeExpert().delta.forward(np.zeros((nv, dv, dk), np.float32), q, k, v, beta, gate)
     dev = DeltaState(nv, dv, dk)

@@ -88,3 +88,32 @@ def test_loader_contract(hip):
         load_native_expert("native", "/nonexistent/lib.so", "GPU", types)
     with pytest.raises(ValueError):
         load_native_expert("bogus", None, "GPU", types)
+
+
+@pytest.mark.parametrize("fp16", [0, 1])
+@pytest.mark.parametrize("down", [12, 14, 8])
+def test_non_finite_row_leaves_later_rows_untouched(hip, oracle_mod, fp16, down):
+    """moe_quant_expert through the C ABI with a down row whose scale is
+    +inf: -4, the rows before it within tolerance of the oracle's, that row
+    non-finite, and every later row as the caller left it -- the reference's
+    row-loop side effects (moe_quant_dot.cpp:207-211), which the oracle pins."""
+    from test_oracle_expert import poison_row
+
+    print(f"non-finite expert row: down={down} fp16={fp16}", flush=True)
+    rng = np.random.default_rng(40 + down + fp16)
+    kinds = (12, 12, down)
+    k = dict(zip(("gate", "up", "down"), kinds))
+    tensors = poison_row(kat_expert(rng, kinds), down, 100, 256)
+    x = (rng.standard_normal(256) * (.005 if fp16 else 1.0)).astype(np.float32)
+    want = np.full(256, 7.0, np.float32)
+    rc_o, _ = oracle_mod.moe_quant_expert(tensors, k, x, 256, 256, fp16, out=want)
+    assert rc_o == -4
+    arrs = [np.ascontiguousarray(tensors[r], dtype=np.uint8) for r in ("gate", "up", "down")]
+    got = np.full(256, 7.0, np.float32)
+    rc = hip.moe_quant_expert(kinds[0], arrs[0].ctypes.data, arrs[0].nbytes, kinds[1], arrs[1].ctypes.data,
+                              arrs[1].nbytes, kinds[2], arrs[2].ctypes.data, arrs[2].nbytes, x.ctypes.data, 256, 256,
+                              got.ctypes.data, fp16)
+    assert rc == -4
+    assert oracle_mod.max_relative_error(got[:100], want[:100]) <= TOL
+    assert not np.isfinite(got[100])
+    np.testing.assert_array_equal(got[101:], 7.0)

@@ -79,7 +79,7 @@ def setup(oracle_mod, hip):
         def route(self, x):
             return oracle_mod.route(x, W, K)
 
-    backend = HipExpertBackend({5: layer})
+    backend = HipExpertBackend({5: layer}, fp16_graph=0)   # the FP32 graph: checked against the FP32 oracle
     sh = SharedExpert.from_backend(backend)
     yield layer, host, shared, Router(), backend, sh
     backend.close()
@@ -205,8 +205,10 @@ def test_shared_expert_and_routers_from_gguf(tmp_path, oracle_mod, hip):
     for layer in range(2):
         sg, su, sd, gi, gate = want[layer]
         got = sh.forward_batch(layer, X)
+        gi16 = gi.astype(np.float16).astype(np.float32)   # SharedExpert._load's storage (shared_expert.py:173)
+        assert np.array_equal(sh.layers[layer].gate_inp.cpu().numpy(), gi16)
         for t in range(3):
-            g = oracle_mod._sigmoid(np.float32(X[t] @ gi).reshape(()))
+            g = oracle_mod._sigmoid(np.float32(X[t] @ gi16).reshape(()))
             ref = (g * oracle_mod.expert_forward({"gate": sg, "up": su, "down": sd},
                                                  {"gate": 14, "up": 14, "down": 14}, X[t], Hs, Is, 0))
             assert oracle_mod.max_relative_error(got[t], ref.astype(np.float32)) <= TOL
@@ -214,3 +216,55 @@ def test_shared_expert_and_routers_from_gguf(tmp_path, oracle_mod, hip):
         for t in range(3):
             assert routers[layer].route(X[t])[0] == ref_router.route(X[t])[0]
         assert np.array_equal(routers[layer].gate_weights, ref_router.gate_weights)
+    # an F16 shared matrix (the reference dequantizes nothing for it) is refused
+    # when the layer is loaded, with the tensor's name
+    f16 = rng.standard_normal((Is, Hs)).astype(np.float16)
+    bad = [(n.replace("blk.1.", "blk.0."), d, t, b) for n, d, t, b in tensors if n.startswith("blk.1.")]
+    bad[0] = ("blk.0.ffn_gate_shexp.weight", (Hs, Is), 1, f16.tobytes())
+    with pytest.raises(ValueError, match="ffn_gate_shexp"):
+        SharedExpert(write(tmp_path, pack_gguf([], bad), "f16_shared.gguf"), 1, Hs, Is)
+
+
+@pytest.mark.parametrize("via", ["fused", "protocol"])
+def test_backend_default_is_the_fp16_graph(oracle_mod, hip, via):
+    """HipExpertBackend defaults to the reference decode's numerics, the
+    native FP16 graph (native_expert.py:33-34): run_moe_layer through the fused
+    hook and through forward() fan-out, at the reference's FP16-graph check
+    magnitudes (d ~ 0.002, x ~ 0.05), against the oracle's FP16-graph experts
+    with the FP32-graph shared expert, at max relative error <= 5e-4, and
+    nearer to it than to the oracle's FP32 graph (the two graphs differ by
+    5-8e-4 here), so the graph is told apart."""
+    from flash_moe_hip.backend import HipExpertBackend
+    from flash_moe_hip.moe_layer import run_moe_layer
+    from flash_moe_hip.shared_expert import SharedExpert
+
+    layer, host, shared = make_layer(91, E, H, I, TYPES, shared_types={"gate": 14, "up": 14, "down": 14},
+                                     scale=0.002)
+    rng = np.random.default_rng(92)
+    W = (rng.standard_normal((H, E)) * 0.05).astype(np.float32)
+
+    class Router:
+        top_k = K
+
+        def route(self, x):
+            return oracle_mod.route(x, W, K)
+
+    backend = HipExpertBackend({5: layer})
+    try:
+        assert backend.fp16_graph == 1
+        sh = SharedExpert.from_backend(backend)
+        b = backend if via == "fused" else ProtocolOnly(backend)
+        for i in range(3):
+            x = (rng.standard_normal(H) * 0.05).astype(np.float32)
+            print(f"FP16-graph run_moe_layer via {via} token {i}", flush=True)
+            got = run_moe_layer(5, x, Router(), b, H, I, shared_expert=sh)
+            ids, ws = oracle_mod.route(x, W, K)
+            want16 = oracle_layer(oracle_mod, layer, host, shared, x, ids, ws, fp16=1)
+            want32 = oracle_layer(oracle_mod, layer, host, shared, x, ids, ws, fp16=0)
+            err = oracle_mod.max_relative_error(got, want16)
+            err32 = oracle_mod.max_relative_error(got, want32)
+            print(f"  max rel err {err:.3e} against the FP16 graph, {err32:.3e} against the FP32 graph", flush=True)
+            assert err <= 5e-4
+            assert err < err32
+    finally:
+        backend.close()

@@ -102,6 +102,12 @@ def test_route_exact_scores_match_bit_for_bit(oracle_mod):
 
 
 def test_route_ties_take_ascending_expert_ids(oracle_mod):
+    """Exactly equal scores: the device takes the lower expert id first.  The
+    reference's np.argsort(s)[-k:][::-1] (router.py:156, the default unstable
+    sort) orders exact ties as its sort implementation leaves them, which
+    depends on the NumPy build, so only the set of tied experts and the score
+    at every rank are compared with the oracle; the ascending order is this
+    kernel's own, documented rule."""
     H, E, k = 64, 32, 6
     rng = np.random.default_rng(11)
     x = rng.integers(0, 3, size=(2, H)).astype(np.float32)
@@ -114,7 +120,10 @@ def test_route_ties_take_ascending_expert_ids(oracle_mod):
         o_ids, o_w = oracle_mod.route(x[t], w, k)
         s = x[t] @ w
         np.testing.assert_array_equal(s[ids[t]], s[o_ids])          # the same scores at every rank
-        assert ids[t][:4].tolist() == [3, 9, 17, 30]                # the tied top four, ascending
+        assert set(ids[t][:4].tolist()) == set(o_ids[:4]) == {3, 9, 17, 30}   # the same tied experts
+        assert ids[t][:4].tolist() == [3, 9, 17, 30]                # this kernel's order: ascending
+        if s[o_ids[k - 1]] != np.sort(s)[::-1][k]:                  # no tie across the k-th rank
+            assert set(ids[t].tolist()) == set(o_ids)
         np.testing.assert_allclose(wts[t], o_w, rtol=0, atol=1e-7)
 
 

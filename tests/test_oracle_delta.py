@@ -110,3 +110,39 @@ def test_status_codes(oracle_mod):
     for heads, dk, dv in ((0, 4, 3), (257, 4, 3), (2, 0, 3), (2, 1025, 3), (2, 4, 0), (2, 4, 1025)):
         assert L.oracle_delta_heads(st.ctypes.data, q.ctypes.data, k.ctypes.data, v.ctypes.data, b.ctypes.data,
                                     g.ctypes.data, v.ctypes.data, heads, dk, dv) == -1
+
+
+def test_first_non_finite_row_stops_the_step(oracle_mod):
+    """A NaN value in head 2, row 5 of a 4 x 8 x 16 step: the oracle returns -2
+    with the state rows up to and including that row updated, the outputs
+    before it written, and that row's output and every later row's state and
+    output as the caller had them (moe_delta.cpp:30-66: the row loop returns
+    before the output store).  Against the reference kernel built from its
+    source as well, bit for bit, where it was built."""
+    rng = np.random.default_rng(12)
+    nv, dv, dk = 4, 8, 16
+    q, k, v, beta, gate = inputs(rng, nv, dv, dk)
+    v[2, 5] = np.nan
+    bad = 2 * dv + 5
+    st0 = (rng.standard_normal((nv, dv, dk)) * 0.01).astype(np.float32)
+    st = st0.copy()
+    out = np.full((nv, dv), 7.0, np.float32)
+    rc, _ = oracle_mod.delta_heads(st, q, k, v, beta, gate, out=out)
+    assert rc == -2
+    clean = st0.copy()
+    v_ok = v.copy()
+    v_ok[2, 5] = 0.0
+    _, out_ok = oracle_mod.delta_heads(clean, q, k, v_ok, beta, gate)
+    rows, orow = st.reshape(-1, dk), out.reshape(-1)
+    np.testing.assert_array_equal(rows[:bad], clean.reshape(-1, dk)[:bad])   # earlier rows: a normal step
+    assert not np.isfinite(rows[bad]).all()                                  # the bad row's state: updated
+    np.testing.assert_array_equal(rows[bad + 1:], st0.reshape(-1, dk)[bad + 1:])
+    np.testing.assert_array_equal(orow[:bad], out_ok.reshape(-1)[:bad])
+    np.testing.assert_array_equal(orow[bad:], 7.0)
+    if oracle_mod.reference_delta_lib() is not None:
+        st_r = st0.copy()
+        out_r = np.full((nv, dv), 7.0, np.float32)
+        rc_r, _ = oracle_mod.reference_delta_heads(st_r, q, k, v, beta, gate, out=out_r)
+        assert rc_r == -2
+        np.testing.assert_array_equal(st_r, st)
+        np.testing.assert_array_equal(out_r, out)

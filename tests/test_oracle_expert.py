@@ -179,3 +179,40 @@ def test_combine_order_and_weight_cast(oracle_mod):
     np.testing.assert_array_equal(got, want)
     ref64 = sum(np.float64(v) * y.astype(np.float64) for y, v in zip(ys, w))
     assert oracle_mod.max_relative_error(got, ref64) < 1e-6
+
+
+SCALE_OFFSET = {8: 0, 11: 108, 12: 0, 13: 0, 14: 208}   # byte offset of each block's FP16 d
+
+
+def poison_row(tensors, kind, row, cols, role="down"):
+    """A copy of ``tensors`` whose ``role`` matrix has every block of ``row``
+    scaled by FP16 +inf, so that row's output is not finite."""
+    bs, size = BLOCK[kind]
+    raw = np.array(tensors[role], dtype=np.uint8).reshape(-1, size)
+    per_row = cols // bs
+    off = SCALE_OFFSET[kind]
+    raw[row * per_row:(row + 1) * per_row, off:off + 2] = np.frombuffer(np.float16(np.inf).tobytes(), np.uint8)
+    return dict(tensors, **{role: raw.reshape(-1)})
+
+
+@pytest.mark.parametrize("fp16", [0, 1])
+@pytest.mark.parametrize("down", [12, 14, 8])
+def test_first_non_finite_row_stops_the_expert(oracle_mod, fp16, down):
+    """A down row with an infinite scale: the oracle returns -4 with the rows
+    before it as a clean run computes them, that row non-finite, and every
+    later row as the caller had it (moe_quant_dot.cpp:207-211: the row is
+    stored, then checked, then the loop returns)."""
+    rng = np.random.default_rng(40 + down + fp16)
+    kinds = (12, 12, down)
+    k = dict(zip(("gate", "up", "down"), kinds))
+    tensors = kat_expert(rng, kinds)
+    x = (rng.standard_normal(256) * (.005 if fp16 else 1.0)).astype(np.float32)
+    r0 = 100
+    rc, clean = oracle_mod.moe_quant_expert(tensors, k, x, 256, 256, fp16)
+    assert rc == 0
+    out = np.full(256, 7.0, np.float32)
+    rc, _ = oracle_mod.moe_quant_expert(poison_row(tensors, down, r0, 256), k, x, 256, 256, fp16, out=out)
+    assert rc == -4
+    np.testing.assert_array_equal(out[:r0], clean[:r0])
+    assert not np.isfinite(out[r0])
+    np.testing.assert_array_equal(out[r0 + 1:], 7.0)

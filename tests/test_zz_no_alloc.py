@@ -3,9 +3,9 @@
 Both entry points run the same kernels; the no-allocation one keeps their
 scratch in the library's static device array instead of a workspace.  Two
 calls in a row, the second with a smaller input, must equal mqh_moe_decode's
-outputs bit for bit (integer, order-fixed kernels), on the fast and on the
-generic (FP16-graph) kernels; the oracle's run_moe_layer arithmetic bounds
-both at the usual 1e-3.  A call beyond the scratch size returns -6 without
+outputs bit for bit (order-fixed kernels), in the FP32 graph and in the FP16
+graph (both on the fast kernels); the oracle's run_moe_layer arithmetic, in
+the same graph, bounds both at the north star's 1e-3.  A call beyond the scratch size returns -6 without
 launching, and fault flags land in the caller's flag words.
 """
 from __future__ import annotations
@@ -80,7 +80,7 @@ def test_noalloc_matches_workspace_decode(hip, oracle_mod, layer_q4k_q6k, layer_
         assert np.array_equal(a, b), (T, float(np.abs(a - b).max()))
         for t in (0, T - 1):
             want = oracle_layer(oracle_mod, layer, host, shared, X[t], ids[t].tolist(), wts[t].tolist(), fp16=fp16)
-            assert oracle_mod.max_relative_error(b[t], want) <= (5e-3 if fp16 else TOL)
+            assert oracle_mod.max_relative_error(b[t], want) <= TOL
 
 
 def test_noalloc_limits_and_flags(hip, layer_q4k_q6k):

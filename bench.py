@@ -604,7 +604,7 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
     frac_a = (layers[0].expert_bytes("gate") + layers[0].expert_bytes("up")) / layers[0].bytes_per_expert()
     dom = "A" if kb["A"] >= kb["B"] else "B"
     frac = frac_a if dom == "A" else 1 - frac_a
-    kname = {"prefill": {"A": "mqh::k_prefill_gate_up<11, 8, false, 2>", "B": "mqh::k_prefill_down<11, 2, 1>"},
+    kname = {"prefill": {"A": "mqh::k_prefill_gate_up<11, 11, 8, false, 2>", "B": "mqh::k_prefill_down<11, 11, 2, 1>"},
              "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32, false, 2>", "B": "mqh::k_fast_down_bal<11, 11, 8, 4>"}}[best][dom]
     out = {
         "workload": f"batched decode: {T} tokens, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
@@ -675,7 +675,7 @@ def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
     tflops = flop / (ms * 1e-3) / 1e12
     dom = "A" if kern["a_us"] >= kern["b_us"] else "B"
     dom_bytes = gu if dom == "A" else nbytes - gu
-    roof = _hbm_roofline("mqh::k_prefill_gate_up<12, 8, true, 2>" if dom == "A" else "mqh::k_prefill_down<14, 2, 1>",
+    roof = _hbm_roofline("mqh::k_prefill_gate_up<12, 12, 8, true, 2>" if dom == "A" else "mqh::k_prefill_down<14, 14, 2, 1>",
                          dom_bytes, kern["a_us"] if dom == "A" else kern["b_us"],
                          read_floor_us(int(dom_bytes)))
     log(f"prefill: {ms * 1e3:.1f} us/layer, {tflops:.1f} TFLOP/s, parity {err:.2e}; "
@@ -692,7 +692,7 @@ def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
         "mfma_ceiling": {"peak_tflops_fp16_dense": 2500.0, "frac": round(tflops / 2500.0, 5)},
         # matrix-core activity of the gate/up GEMM from the committed counter run
         # (useful FLOPs are about a quarter of those issued: ~4 of 16 token columns)
-        "mfma_counters": measured_mfma("mqh::k_prefill_gate_up<12, 8, true, 2>"),
+        "mfma_counters": measured_mfma("mqh::k_prefill_gate_up<12, 12, 8, true, 2>"),
     }
     if cpu_seconds > 0:
         L0 = layers[0]

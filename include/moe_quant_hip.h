@@ -212,16 +212,21 @@ int64_t mqh_moe_prefill_workspace_bytes(int n_tokens, int top_k, int n_experts, 
  *   y[t] = sum_s weights[t,s] * E_{ids[t,s]}(x[t]) + sigmoid(x[t].sh_gate_inp) * E_sh(x[t])
  * Same tensors and ids/weights as mqh_moe_decode; x is [n_tokens x hidden],
  * FP32 (x_bf16 = 0) or BF16 (x_bf16 = 1), 16-byte aligned; y FP32.  The shared
- * expert (optional, sh_gate == NULL: none) has the routed experts' types and
- * intermediate size.  Tokens are bucketed per expert on the device; weights are
- * multiplied as exact integer MFMA operands with FP32 accumulation.  Supported:
- * Q3_K/Q4_K/Q5_K/Q6_K with gate == up type, hidden and intermediate in
+ * expert (optional, sh_gate == NULL: none) runs in the same grouped launches:
+ * its intermediate size is the routed one (sh_intermediate == intermediate,
+ * else -1), its gate/up type the routed gate/up type or Q6_K, its down type
+ * the routed down type or Q6_K (the reference model's layers: Q6_K shared
+ * experts beside Q3_K, Q4_K or Q8_0 routed matrices).  Tokens are bucketed per
+ * expert on the device; weights are multiplied as exact integer MFMA operands
+ * with FP32 accumulation.  Supported: gate == up type in Q3_K/Q4_K/Q5_K/Q6_K,
+ * down type in Q3_K/Q4_K/Q5_K/Q6_K/Q8_0, hidden and intermediate in
  * {256, 512, 1024, 2048}, at most 1024 experts; else -2.  The workspace
  * (256-byte aligned, mqh_moe_prefill_workspace_bytes(...)) is zeroed once with
  * mqh_workspace_init.  Returns 0, -1, -2, -5 or -6; mqh_status reads -4 / -9. */
 int mqh_moe_prefill(int gate_type, const void* gate, int up_type, const void* up,
                     int down_type, const void* down, int n_experts, int hidden, int intermediate,
-                    const void* sh_gate, const void* sh_up, const void* sh_down, const float* sh_gate_inp,
+                    int sh_gate_type, const void* sh_gate, int sh_up_type, const void* sh_up,
+                    int sh_down_type, const void* sh_down, int sh_intermediate, const float* sh_gate_inp,
                     const void* x, int x_bf16, int n_tokens, const int32_t* ids, const float* weights,
                     int top_k, float* y, void* workspace, int64_t workspace_bytes, void* stream);
 

@@ -566,19 +566,22 @@ int64_t mqh_moe_prefill_workspace_bytes(int n_tokens, int top_k, int n_experts, 
 }
 
 int mqh_moe_prefill(int gate_type, const void* gate, int up_type, const void* up, int down_type, const void* down,
-                    int n_experts, int hidden, int intermediate, const void* sh_gate, const void* sh_up,
-                    const void* sh_down, const float* sh_gate_inp, const void* x, int x_bf16, int n_tokens,
-                    const int32_t* ids, const float* weights, int top_k, float* y, void* workspace,
-                    int64_t workspace_bytes, void* stream) {
+                    int n_experts, int hidden, int intermediate, int sh_gate_type, const void* sh_gate,
+                    int sh_up_type, const void* sh_up, int sh_down_type, const void* sh_down, int sh_intermediate,
+                    const float* sh_gate_inp, const void* x, int x_bf16, int n_tokens, const int32_t* ids,
+                    const float* weights, int top_k, float* y, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
     const int has_shared = sh_gate != nullptr ? 1 : 0;
     if (!x || !y || !workspace || (x_bf16 != 0 && x_bf16 != 1)) return ST_ARG;
     if (n_tokens <= 0 || top_k < 0 || top_k > 64 || (top_k == 0 && !has_shared)) return ST_ARG;
     if (n_experts <= 0 || hidden <= 0 || intermediate <= 0) return ST_ARG;
     if (top_k > 0 && (!gate || !up || !down || !ids || !weights)) return ST_ARG;
-    if (has_shared && (!sh_up || !sh_down)) return ST_ARG;
+    if (has_shared && (!sh_up || !sh_down || sh_intermediate != intermediate)) return ST_ARG;
     if (odd(gate) || odd(up) || odd(down) || odd(sh_gate) || odd(sh_up) || odd(sh_down)) return ST_ARG;
-    const int st = check_expert_types(gate_type, up_type, down_type, hidden, intermediate);
+    int st = check_expert_types(gate_type, up_type, down_type, hidden, intermediate);
     if (st) return st;
+    if (has_shared && (st = check_expert_types(sh_gate_type, sh_up_type, sh_down_type, hidden, intermediate)))
+        return st;
     // 16-byte vector loads of x rows, of the gate vector and of the packed tile records
     if (((uintptr_t)x & 15) || ((uintptr_t)sh_gate_inp & 15) || ((uintptr_t)workspace & 255)) return ST_ARG;
 
@@ -589,6 +592,8 @@ int mqh_moe_prefill(int gate_type, const void* gate, int up_type, const void* up
     p.up_eb = matrix_bytes(up_type, intermediate, hidden);
     p.down_eb = matrix_bytes(down_type, hidden, intermediate);
     p.n_experts = n_experts; p.hidden = hidden; p.inter = intermediate;
+    p.has_shared = has_shared;
+    p.sh_gate_type = sh_gate_type; p.sh_up_type = sh_up_type; p.sh_down_type = sh_down_type;
     if (!prefill_supported(p)) return ST_TYPE;
     const PrefillLayout L = prefill_layout(n_tokens, top_k, n_experts, hidden, intermediate, has_shared);
     if (workspace_bytes < L.total) return ST_WORKSPACE;

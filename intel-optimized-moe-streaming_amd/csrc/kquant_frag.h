@@ -47,11 +47,22 @@ template <> struct FragGeo<T_Q4_K> { static constexpr int NW = 12, NA = 1, HDR =
 template <> struct FragGeo<T_Q5_K> { static constexpr int NW = 16, NA = 1, HDR = 0, D_SHIFT = 0; static constexpr bool MIN = true; };
 template <> struct FragGeo<T_Q6_K> { static constexpr int NW = 21, NA = 2, HDR = 20, D_SHIFT = 0; static constexpr bool MIN = false; };
 template <> struct FragGeo<T_Q3_K> { static constexpr int NW = 12, NA = 1, HDR = 11, D_SHIFT = 16; static constexpr bool MIN = false; };
+// Q8_0 (a unit of 256 columns is 8 blocks of 34 bytes, each with its own FP16
+// d): step M is block M, its operand the 32 int8 quants as exact halves, and
+// d is applied per step (PfRows::block); words 16 and 17 hold the FP16 d of
+// blocks 2qq and 2qq + 1 of the lane's row
+template <> struct FragGeo<T_Q8_0> { static constexpr int NW = 18, NA = 1, HDR = 16, D_SHIFT = 0; static constexpr bool MIN = false; };
+
+// Bytes of one 256-column unit of a row: a K-quant super-block, or eight
+// Q8_0 blocks.
+template <int T>
+__host__ __device__ constexpr int frag_unit_bytes() { return T == T_Q8_0 ? 8 * 34 : block_bytes(T); }
 
 // First column of step M's 8 columns, before the lane's offset.
 template <int T, int M>
 __host__ __device__ constexpr int frag_col() {
-    if constexpr (T == T_Q6_K) return 128 * (M >> 2) + 64 * ((M >> 1) & 1) + 8 * (M & 1);
+    if constexpr (T == T_Q8_0) return 32 * M;
+    else if constexpr (T == T_Q6_K) return 128 * (M >> 2) + 64 * ((M >> 1) & 1) + 8 * (M & 1);
     else if constexpr (T == T_Q3_K) return 32 * (M >> 1) + 8 * (M & 1);
     else return 128 * (M >> 2) + 32 * ((M >> 1) & 1) + 8 * (M & 1);
 }
@@ -59,7 +70,8 @@ __host__ __device__ constexpr int frag_col() {
 // The lane's column offset (qq = (q + 3) & 3).
 template <int T>
 __host__ __device__ inline int frag_lane_col(int qq) {
-    if constexpr (T == T_Q6_K) return 32 * (qq >> 1) + 16 * (qq & 1);
+    if constexpr (T == T_Q8_0) return 8 * qq;
+    else if constexpr (T == T_Q6_K) return 32 * (qq >> 1) + 16 * (qq & 1);
     else if constexpr (T == T_Q3_K) return 128 * (qq >> 1) + 16 * (qq & 1);
     else return 64 * (qq >> 1) + 16 * (qq & 1);
 }
@@ -77,6 +89,17 @@ __host__ __device__ inline void frag_ld128(const uint8_t* p, uint32_t* w) {
     w[3] = v.w;
 #else
     memcpy(w, p, 16);
+#endif
+}
+
+__host__ __device__ inline void frag_ld64(const uint8_t* p, uint32_t* w) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef uint2 __attribute__((aligned(1))) u64_unaligned;
+    const uint2 v = *(const __attribute__((address_space(1))) u64_unaligned*)p;
+    w[0] = v.x;
+    w[1] = v.y;
+#else
+    memcpy(w, p, 8);
 #endif
 }
 
@@ -133,6 +156,13 @@ __host__ __device__ inline void frag_load(const uint8_t* blk, int q, uint32_t* r
         // (the four reads above end by byte 196, inside the block)
         frag_ld128(blk + 192, r + 16);                  // int8 scales[16]
         r[20] = frag_ld16(blk + 208);                   // d
+    } else if constexpr (T == T_Q8_0) {
+        // quants 8qq .. 8qq+7 of each of the unit's eight blocks (block m at
+        // byte 34m, its quants from byte 34m + 2), then the d of blocks 2qq, 2qq+1
+#pragma unroll
+        for (int m = 0; m < 8; ++m) frag_ld64(blk + 34 * m + 2 + 8 * qq, r + 2 * m);
+        r[16] = frag_ld16(blk + 68 * qq);
+        r[17] = frag_ld16(blk + 68 * qq + 34);
     } else {  // Q3_K
         frag_ld128(blk + 32 + 16 * qq, r);              // qs bytes 16qq .. +16
         frag_ld128(blk + 16 * (qq & 1), r + 4);         // hmask bytes 16(qq&1) .. +16
@@ -185,7 +215,10 @@ template <int T> struct FragPrep { h2_t s[2], c[2]; };
 template <int T>
 __host__ __device__ inline void frag_prep(const uint32_t* r, int q, FragPrep<T>& P) {
     const int qq = (q + 3) & 3;
-    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+    if constexpr (T == T_Q8_0) {
+        (void)r;   // no sub-block scales: each step's d is applied to its product
+        (void)qq;
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         // get_scale_min_k4 (cpp/dequant_k.cpp:166-175): sc0..3 = s[0..3] & 63,
         // sc4..7 = (s[8..11] & 15) | (s[0..3] >> 6) << 4, s = words r[1..3].  Step m
         // is sub-block 4(m >> 2) + 2(qq >> 1) + ((m >> 1) & 1).
@@ -233,7 +266,18 @@ template <int T, int M>
 __host__ __device__ inline void frag_step(const uint32_t* r, const FragPrep<T>& P, int q, h8_t* a) {
     const int qq = (q + 3) & 3;
     h2_t p[4];
-    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+    if constexpr (T == T_Q8_0) {
+        // block M's int8 quants 8qq .. 8qq+7: byte ^ 0x80 = q + 128, a biased
+        // half less 1152 is q, exact
+        (void)P;
+        (void)qq;
+        frag_bytes_f16(r[2 * M] ^ 0x80808080u, (_Float16)128.0f, p[0], p[1]);
+        frag_bytes_f16(r[2 * M + 1] ^ 0x80808080u, (_Float16)128.0f, p[2], p[3]);
+        for (int i = 0; i < 4; ++i) {
+            a[0][2 * i] = p[i][0];
+            a[0][2 * i + 1] = p[i][1];
+        }
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         // qs run M >> 2, bytes 8(M & 1) .. +8, nibble (M >> 1) & 1; the Q5_K fifth
         // bit is qh (same byte index) bit column / 32 = 4(M >> 2) + 2(qq >> 1) + nibble
         constexpr int QW = (T == T_Q4_K ? 4 : 8) + 4 * (M >> 2) + 2 * (M & 1), NIB = (M >> 1) & 1;

@@ -97,6 +97,7 @@ struct PrefillParams {
     const uint8_t* sh_gate;
     const uint8_t* sh_up;
     const uint8_t* sh_down;
+    int sh_gate_type, sh_up_type, sh_down_type;   // the routed types, or Q6_K
     const float* sh_gate_inp;
     int has_shared;
     const void* x;          // [n_tokens x hidden], FP32 or BF16

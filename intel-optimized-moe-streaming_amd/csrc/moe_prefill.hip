@@ -56,6 +56,13 @@ constexpr int PF_ROWS_DOWN = 128; // down rows per workgroup chunk: 8 waves x 16
 #ifndef PF_RING_DOWN
 #define PF_RING_DOWN PF_RING
 #endif
+// A shared expert of another type than the routed experts runs in the same
+// launch (its tiles take their own instance of the body), and the kernel's
+// register allocation is the larger body's: its ring is shallower, so that
+// a Q6_K shared expert does not cost the routed tiles their occupancy.
+#ifndef PF_RING_SHARED
+#define PF_RING_SHARED 2
+#endif
 constexpr int PF_PAD = 8;        // LDS row padding (halves)
 
 // Waves per SIMD that the LDS footprint of one workgroup (PF_WAVES waves)
@@ -345,7 +352,7 @@ __device__ __forceinline__ void pf_planes_store(const PfPlanes<K, SPLIT>& r, int
 // overlap.  D layout: lane l holds rows 4(l/16) + i, token column l % 16.
 template <int T, int NMAT, int NB, int CPW, int RING = PF_RING>
 struct PfRows {
-    static constexpr int NW = FragGeo<T>::NW, BB = block_bytes(T), NBT = NB * CPW;
+    static constexpr int NW = FragGeo<T>::NW, BB = frag_unit_bytes<T>(), NBT = NB * CPW;
     // R ring slots: block b lives in slot b % R; while block b is computed,
     // blocks b+1 .. b+R-1 are in flight (all of them for short rows)
     static constexpr bool UNROLLED = NBT <= RING;
@@ -368,11 +375,48 @@ struct PfRows {
         for (int b = 0; b < (NBT < R - 1 ? NBT : R - 1); ++b) load(min(b, nbt - 1), raw[b]);
     }
 
+    // one 256-column unit of eight Q8_0 blocks (unit kb of its row): step m is
+    // block m, P_m its exact integer product with the token planes, acc +=
+    // d_m * P_m.  The D layout wants the d of rows 4q .. 4q+3, held by other
+    // lanes (k-group qq of row r loaded blocks 2qq, 2qq+1), so each lane puts
+    // its two into the wave's LDS table [block][row] and reads four back per
+    // step (one wave's LDS accesses complete in order: no barrier)
+    template <bool SPLIT>
+    __device__ __forceinline__ void block_q8(const uint32_t (&cur)[NMAT][NW], int kb, const _Float16* xh,
+                                             const _Float16* xl, f32x4 (&acc)[NMAT]) {
+        static_assert(NMAT == 1, "one Q8_0 matrix a wave");
+        constexpr int KP = NB * 256 + PF_PAD;
+        __shared__ __attribute__((aligned(16))) float s_d8[PF_WAVES][8][16];
+        const int lane = threadIdx.x & 63, tok = lane & 15, qq = (q + 3) & 3;
+        const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        s_d8[wave][2 * qq][lane & 15] = frag_h2f(cur[0][16]);
+        s_d8[wave][2 * qq + 1][lane & 15] = frag_h2f(cur[0][17]);
+        const int brow = tok * KP + kb * 256 + frag_lane_col<T>(qq);
+        FragPrep<T> sp;
+        pf_unroll(std::make_integer_sequence<int, 8>{}, [&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+            const int off = brow + frag_col<T, m>();
+            const h8_t bh = *(const h8_t*)(xh + off);
+            h8_t a[2];
+            frag_step<T, m>(cur[0], sp, q, a);
+            f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], bh, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            if constexpr (SPLIT) {
+                const h8_t bl = *(const h8_t*)(xl + off);
+                P = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], bl, P, 0, 0, 0);
+            }
+            const float4 d = *(const float4*)&s_d8[wave][m][4 * q];
+            acc[0][0] = fmaf(d.x, P[0], acc[0][0]);
+            acc[0][1] = fmaf(d.y, P[1], acc[0][1]);
+            acc[0][2] = fmaf(d.z, P[2], acc[0][2]);
+            acc[0][3] = fmaf(d.w, P[3], acc[0][3]);
+        });
+    }
+
     // one super-block (block kb of its row): P = sum over its 8 steps of the exact
     // integer operands times the token planes, then acc += d * P (- dmin * min term)
     template <bool SPLIT>
-    __device__ __forceinline__ void block(const uint32_t (&cur)[NMAT][NW], int kb, const _Float16* xh,
-                                          const _Float16* xl, const _Float16* xs, f32x4 (&acc)[NMAT]) {
+    __device__ __forceinline__ void block_k(const uint32_t (&cur)[NMAT][NW], int kb, const _Float16* xh,
+                                            const _Float16* xl, const _Float16* xs, f32x4 (&acc)[NMAT]) {
         constexpr int KP = NB * 256 + PF_PAD;
         const int lane = threadIdx.x & 63, tok = lane & 15;
         const int brow = tok * KP + kb * 256 + frag_lane_col<T>((q + 3) & 3);
@@ -416,6 +460,13 @@ struct PfRows {
                 acc[mt][i] = fmaf(frag_d<T>(hdr), P[mt][i], acc[mt][i]);
                 if constexpr (FragGeo<T>::MIN) acc[mt][i] = fmaf(-frag_dmin(hdr), Mn[mt][i], acc[mt][i]);
             }
+    }
+
+    template <bool SPLIT>
+    __device__ __forceinline__ void block(const uint32_t (&cur)[NMAT][NW], int kb, const _Float16* xh,
+                                          const _Float16* xl, const _Float16* xs, f32x4 (&acc)[NMAT]) {
+        if constexpr (T == T_Q8_0) block_q8<SPLIT>(cur, kb, xh, xl, acc);
+        else block_k<SPLIT>(cur, kb, xh, xl, xs, acc);
     }
 
     // All NBT blocks; end(c, acc) runs after the last block of chunk c, with the
@@ -615,7 +666,10 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
 
 // ------------------------------------------------------------ P1
 
-template <int GT, int NBH, bool XBF16, int CPW>
+// SGT: the shared expert's gate/up type.  A tile is one expert's, so a
+// workgroup runs one type: with SGT != GT, the shared tiles (expert -1) take
+// the SGT instance of the body and the routed tiles the GT one, in one launch.
+template <int GT, int SGT, int NBH, bool XBF16, int CPW>
 __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(const int* n_tiles, const int4* tiles,
                                                                              const int* tile_tok, const void* xsrc,
                                                                              int max_tiles, int nbig, int nsmall,
@@ -652,17 +706,12 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     const int wv = __builtin_amdgcn_readfirstlane(wave);
     const int mat = wv / (PF_WAVES / 2), wsub = wv % (PF_WAVES / 2);
     const int rbase = chunk0 * PF_ROWS_GU + wsub * 16;
-    const int64_t row_bytes = (int64_t)NBH * block_bytes(GT);
 
     // (selects of wave-uniform values, no branch: each branch would load its
     // own arguments after the tile's round trip)
-    PfRows<GT, 1, NBH, CPW> g;
     const uint8_t* Ws = mat ? sh_up : sh_gate;
     const uint8_t* Wr = (mat ? up : gate) + (int64_t)max(e, 0) * (mat ? up_eb : gate_eb);
-    g.W[0] = (e < 0 ? Ws : Wr) + (int64_t)(rbase + (lane & 15)) * row_bytes;
-    g.chunk_stride = PF_ROWS_GU * row_bytes;
-    g.q = q;
-    g.nbt = NBH * nch;
+    const uint8_t* W0 = e < 0 ? Ws : Wr;
     // the wave's token columns wv and wv + 8 (a column past cnt reads token 0's
     // first words and stages nothing): their loads go out before the
     // weight prefetch, so the staging below waits for them only
@@ -675,43 +724,58 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     pf_planes_load<H, SPLIT>(xhi, xlo, xsum, xexp, t0, l0, r0);
     pf_planes_load<H, SPLIT>(xhi, xlo, xsum, xexp, t1, l1, r1);
     __builtin_amdgcn_sched_barrier(0);
-    g.prefetch();
-    // (a compiler memory barrier: the prefetched values are first used after
-    // the staging's branches, and hipcc would otherwise sink their loads there)
-    __asm__ volatile("" ::: "memory");
-    pf_planes_pin(r0);
-    pf_planes_pin(r1);
-    __builtin_amdgcn_sched_barrier(0);
-    pf_planes_store(r0, wv, l0, xh, xl, xs, s_exp);
-    pf_planes_store(r1, wv + PF_WAVES, l1, xh, xl, xs, s_exp);
-    __syncthreads();
 
-    const int col = lane & 15;
-    const float sc = col < cnt ? ldexpf(1.0f, s_exp[col]) : 0.0f;
-    f32x4 acc[1] = {{0, 0, 0, 0}};
-    g.template run<SPLIT>(xh, xl, xs, acc, [&](int c, f32x4 (&a)[1]) {
-        // the up waves hand their results to the gate waves of the same rows
-        // (same D layout, so no transposition); columns at or past cnt hold stale
-        // LDS and are never stored
-        if (mat) *(float4*)s_up[wsub][lane] = make_float4(a[0][0], a[0][1], a[0][2], a[0][3]);
+    auto body = [&](auto tc) {
+        constexpr int T = decltype(tc)::value;
+        const int64_t row_bytes = (int64_t)NBH * frag_unit_bytes<T>();
+        PfRows<T, 1, NBH, CPW, (SGT != GT && T == SGT) ? PF_RING_SHARED : PF_RING> g;
+        g.W[0] = W0 + (int64_t)(rbase + (lane & 15)) * row_bytes;
+        g.chunk_stride = PF_ROWS_GU * row_bytes;
+        g.q = q;
+        g.nbt = NBH * nch;
+        g.prefetch();
+        // (a compiler memory barrier: the prefetched values are first used after
+        // the staging's branches, and hipcc would otherwise sink their loads there)
+        __asm__ volatile("" ::: "memory");
+        pf_planes_pin(r0);
+        pf_planes_pin(r1);
+        __builtin_amdgcn_sched_barrier(0);
+        pf_planes_store(r0, wv, l0, xh, xl, xs, s_exp);
+        pf_planes_store(r1, wv + PF_WAVES, l1, xh, xl, xs, s_exp);
         __syncthreads();
-        if (!mat && col < cnt) {
-            const float4 u = *(const float4*)s_up[wsub][lane];
-            float4 o;
-            o.x = pf_silu_mul(a[0][0] * sc, u.x * sc);
-            o.y = pf_silu_mul(a[0][1] * sc, u.y * sc);
-            o.z = pf_silu_mul(a[0][2] * sc, u.z * sc);
-            o.w = pf_silu_mul(a[0][3] * sc, u.w * sc);
-            *(float4*)(p.act + (int64_t)(first + col) * p.inter + rbase + PF_ROWS_GU * c + 4 * q) = o;
-        }
-        __syncthreads();
-        a[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    });
+
+        const int col = lane & 15;
+        const float sc = col < cnt ? ldexpf(1.0f, s_exp[col]) : 0.0f;
+        f32x4 acc[1] = {{0, 0, 0, 0}};
+        g.template run<SPLIT>(xh, xl, xs, acc, [&](int c, f32x4 (&a)[1]) {
+            // the up waves hand their results to the gate waves of the same rows
+            // (same D layout, so no transposition); columns at or past cnt hold
+            // stale LDS and are never stored
+            if (mat) *(float4*)s_up[wsub][lane] = make_float4(a[0][0], a[0][1], a[0][2], a[0][3]);
+            __syncthreads();
+            if (!mat && col < cnt) {
+                const float4 u = *(const float4*)s_up[wsub][lane];
+                float4 o;
+                o.x = pf_silu_mul(a[0][0] * sc, u.x * sc);
+                o.y = pf_silu_mul(a[0][1] * sc, u.y * sc);
+                o.z = pf_silu_mul(a[0][2] * sc, u.z * sc);
+                o.w = pf_silu_mul(a[0][3] * sc, u.w * sc);
+                *(float4*)(p.act + (int64_t)(first + col) * p.inter + rbase + PF_ROWS_GU * c + 4 * q) = o;
+            }
+            __syncthreads();
+            a[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        });
+    };
+    if constexpr (SGT == GT) body(std::integral_constant<int, GT>{});
+    else if (e < 0) body(std::integral_constant<int, SGT>{});   // (uniform: the workgroup's tile)
+    else body(std::integral_constant<int, GT>{});
 }
 
 // ------------------------------------------------------------ P2
 
-template <int DT, int NBI, int CPW>
+// SDT: the shared expert's down type (its tiles take that instance of the
+// body, as in the gate/up kernel).
+template <int DT, int SDT, int NBI, int CPW>
 __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(const int* n_tiles, const int4* tiles,
                                                                            const int* tile_tok, const void* act,
                                                                            int max_tiles, int nch_log2, PrefillParams p) {
@@ -731,32 +795,39 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(cons
     const int e = td.x, first = td.y, cnt = td.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
     const int rbase = chunk * PF_ROWS_DOWN * CPW + wave * 16;
-    const int64_t row_bytes = (int64_t)NBI * block_bytes(DT);
+    const uint8_t* W0 = e < 0 ? sh_down : down + (int64_t)max(e, 0) * down_eb;
 
-    PfRows<DT, 1, NBI, CPW, PF_RING_DOWN> g;
-    g.W[0] = (e < 0 ? sh_down : down + (int64_t)max(e, 0) * down_eb) + (int64_t)(rbase + (lane & 15)) * row_bytes;
-    g.chunk_stride = PF_ROWS_DOWN * row_bytes;
-    g.q = q;
-    // (here the live activation rows follow the prefetch: issuing the tile's
-    // rows first, as the gate/up kernel does with its tokens, measured 66 ->
-    // 72 us for this kernel at the 128-token prompt)
-    g.prefetch();
-    for (int j = wave; j < cnt; j += PF_WAVES) {
-        PfStageRaw<I, false> r;
-        pf_stage_load<I, false>(act, first + j, true, r);
-        pf_stage_finish<I, false, true>(r, j, true, xh, xl, xs, s_exp);
-    }
-    __syncthreads();
+    auto body = [&](auto tc) {
+        constexpr int T = decltype(tc)::value;
+        const int64_t row_bytes = (int64_t)NBI * frag_unit_bytes<T>();
+        PfRows<T, 1, NBI, CPW, (SDT != DT && T == SDT) ? PF_RING_SHARED : PF_RING_DOWN> g;
+        g.W[0] = W0 + (int64_t)(rbase + (lane & 15)) * row_bytes;
+        g.chunk_stride = PF_ROWS_DOWN * row_bytes;
+        g.q = q;
+        // (here the live activation rows follow the prefetch: issuing the tile's
+        // rows first, as the gate/up kernel does with its tokens, measured 66 ->
+        // 72 us for this kernel at the 128-token prompt)
+        g.prefetch();
+        for (int j = wave; j < cnt; j += PF_WAVES) {
+            PfStageRaw<I, false> r;
+            pf_stage_load<I, false>(act, first + j, true, r);
+            pf_stage_finish<I, false, true>(r, j, true, xh, xl, xs, s_exp);
+        }
+        __syncthreads();
 
-    const int col = lane & 15;
-    const float sc = col < cnt ? ldexpf(1.0f, s_exp[col]) : 0.0f;
-    f32x4 acc[1] = {{0, 0, 0, 0}};
-    g.template run<true>(xh, xl, xs, acc, [&](int c, f32x4 (&a)[1]) {
-        if (col < cnt)
-            *(float4*)(p.ypair + (int64_t)(first + col) * p.hidden + rbase + PF_ROWS_DOWN * c + 4 * q) =
-                make_float4(a[0][0] * sc, a[0][1] * sc, a[0][2] * sc, a[0][3] * sc);
-        a[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    });
+        const int col = lane & 15;
+        const float sc = col < cnt ? ldexpf(1.0f, s_exp[col]) : 0.0f;
+        f32x4 acc[1] = {{0, 0, 0, 0}};
+        g.template run<true>(xh, xl, xs, acc, [&](int c, f32x4 (&a)[1]) {
+            if (col < cnt)
+                *(float4*)(p.ypair + (int64_t)(first + col) * p.hidden + rbase + PF_ROWS_DOWN * c + 4 * q) =
+                    make_float4(a[0][0] * sc, a[0][1] * sc, a[0][2] * sc, a[0][3] * sc);
+            a[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        });
+    };
+    if constexpr (SDT == DT) body(std::integral_constant<int, DT>{});
+    else if (e < 0) body(std::integral_constant<int, SDT>{});   // (uniform: the workgroup's tile)
+    else body(std::integral_constant<int, DT>{});
 }
 
 // ------------------------------------------------------------ P3
@@ -796,12 +867,21 @@ __global__ __launch_bounds__(256) void k_prefill_combine(PrefillParams p) {
 
 // ------------------------------------------------------------ host side
 
+// gate/up: the K-quants; down: the K-quants and Q8_0 (the reference model's
+// first-layer down projection)
 static bool pf_type(int t) { return t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+static bool pf_down_type(int t) { return pf_type(t) || t == T_Q8_0; }
 static bool pf_dim(int n) { return n == 256 || n == 512 || n == 1024 || n == 2048; }
 
 bool prefill_supported(const PrefillParams& p) {
     if (!pf_dim(p.hidden) || !pf_dim(p.inter) || p.n_experts < 1 || p.n_experts > PREFILL_MAX_EXPERTS) return false;
-    if (!(pf_type(p.gate_type) && p.up_type == p.gate_type && pf_type(p.down_type))) return false;
+    if (!(pf_type(p.gate_type) && p.up_type == p.gate_type && pf_down_type(p.down_type))) return false;
+    // a shared expert inside the grouped kernels: the routed types, or Q6_K
+    // (the reference model's shared experts beside Q3_K or Q4_K routed ones)
+    if (p.has_shared && ((p.sh_gate_type != p.gate_type && p.sh_gate_type != T_Q6_K) ||
+                         p.sh_up_type != p.sh_gate_type ||
+                         (p.sh_down_type != p.down_type && p.sh_down_type != T_Q6_K)))
+        return false;
     return true;
 }
 
@@ -842,7 +922,7 @@ PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden,
 // down row chunks per workgroup (CPW x 128 rows)
 constexpr int pf_cpw_down(int hidden) { return hidden / PF_ROWS_DOWN < PF_CPW_DOWN ? hidden / PF_ROWS_DOWN : PF_CPW_DOWN; }
 
-template <int GT, int NBH, bool XBF16>
+template <int GT, int SGT, int NBH, bool XBF16>
 static void launch_p1(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
     // per tile, PF_BIG_GU-chunk workgroups over all but at least PF_SMALL_GU
     // chunks, one-chunk workgroups for the rest
@@ -852,52 +932,75 @@ static void launch_p1(const PrefillParams& p, hipStream_t s, const KernelEvents&
     const dim3 grid((nbig + nsmall) * ((p.max_tiles + PF_XCDS - 1) / PF_XCDS * PF_XCDS)), block(64 * PF_WAVES);
     const unsigned mbig = pf_magic(nbig), msmall = pf_magic(nsmall);
     if (ev.armed_a())
-        hipExtLaunchKernelGGL((k_prefill_gate_up<GT, NBH, XBF16, CB>), grid, block, 0, s, ev.a_start, ev.a_stop, 0,
+        hipExtLaunchKernelGGL((k_prefill_gate_up<GT, SGT, NBH, XBF16, CB>), grid, block, 0, s, ev.a_start, ev.a_stop, 0,
                               (const int*)p.n_tiles, (const int4*)p.tiles, (const int*)p.tile_tok, (const void*)p.xhi,
                               p.max_tiles, nbig, nsmall, mbig, msmall, p);
     else
-        hipLaunchKernelGGL((k_prefill_gate_up<GT, NBH, XBF16, CB>), grid, block, 0, s, (const int*)p.n_tiles,
+        hipLaunchKernelGGL((k_prefill_gate_up<GT, SGT, NBH, XBF16, CB>), grid, block, 0, s, (const int*)p.n_tiles,
                            (const int4*)p.tiles, (const int*)p.tile_tok, (const void*)p.xhi, p.max_tiles, nbig, nsmall,
                            mbig, msmall, p);
 }
 
-template <int GT, int NBH>
+template <int GT, int SGT, int NBH>
 static void launch_p1_i(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
-    if (p.x_bf16) launch_p1<GT, NBH, true>(p, s, ev);
-    else launch_p1<GT, NBH, false>(p, s, ev);
+    if (p.x_bf16) launch_p1<GT, SGT, NBH, true>(p, s, ev);
+    else launch_p1<GT, SGT, NBH, false>(p, s, ev);
 }
 
-template <int GT>
+template <int GT, int SGT>
 static void launch_p1_h(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
     switch (p.hidden) {
-        case 256: launch_p1_i<GT, 1>(p, s, ev); break;
-        case 512: launch_p1_i<GT, 2>(p, s, ev); break;
-        case 1024: launch_p1_i<GT, 4>(p, s, ev); break;
-        default: launch_p1_i<GT, 8>(p, s, ev); break;
+        case 256: launch_p1_i<GT, SGT, 1>(p, s, ev); break;
+        case 512: launch_p1_i<GT, SGT, 2>(p, s, ev); break;
+        case 1024: launch_p1_i<GT, SGT, 4>(p, s, ev); break;
+        default: launch_p1_i<GT, SGT, 8>(p, s, ev); break;
     }
 }
 
-template <int DT, int NBI, int CPW>
+// a shared expert of another type is Q6_K (prefill_supported admits no other)
+template <int GT>
+static void launch_p1_t(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
+    if constexpr (GT != T_Q6_K) {
+        if (p.has_shared && p.sh_gate_type != GT) {
+            launch_p1_h<GT, T_Q6_K>(p, s, ev);
+            return;
+        }
+    }
+    launch_p1_h<GT, GT>(p, s, ev);
+}
+
+template <int DT, int SDT, int NBI, int CPW>
 static void launch_p2(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
     const int nch = p.hidden / (PF_ROWS_DOWN * CPW);
     const dim3 grid(pf_grid(nch, p.max_tiles));
-    PF_LAUNCH((k_prefill_down<DT, NBI, CPW>), grid, ev.armed_b(), ev.b_start, ev.b_stop, s, p.act, nch, p);
+    PF_LAUNCH((k_prefill_down<DT, SDT, NBI, CPW>), grid, ev.armed_b(), ev.b_start, ev.b_stop, s, p.act, nch, p);
 }
 
-template <int DT, int NBI>
+template <int DT, int SDT, int NBI>
 static void launch_p2_h(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
-    if (p.hidden == 256) launch_p2<DT, NBI, pf_cpw_down(256)>(p, s, ev);
-    else launch_p2<DT, NBI, PF_CPW_DOWN>(p, s, ev);
+    if (p.hidden == 256) launch_p2<DT, SDT, NBI, pf_cpw_down(256)>(p, s, ev);
+    else launch_p2<DT, SDT, NBI, PF_CPW_DOWN>(p, s, ev);
+}
+
+template <int DT, int SDT>
+static void launch_p2_i(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
+    switch (p.inter) {
+        case 256: launch_p2_h<DT, SDT, 1>(p, s, ev); break;
+        case 512: launch_p2_h<DT, SDT, 2>(p, s, ev); break;
+        case 1024: launch_p2_h<DT, SDT, 4>(p, s, ev); break;
+        default: launch_p2_h<DT, SDT, 8>(p, s, ev); break;
+    }
 }
 
 template <int DT>
-static void launch_p2_i(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
-    switch (p.inter) {
-        case 256: launch_p2_h<DT, 1>(p, s, ev); break;
-        case 512: launch_p2_h<DT, 2>(p, s, ev); break;
-        case 1024: launch_p2_h<DT, 4>(p, s, ev); break;
-        default: launch_p2_h<DT, 8>(p, s, ev); break;
+static void launch_p2_t(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
+    if constexpr (DT != T_Q6_K) {
+        if (p.has_shared && p.sh_down_type != DT) {
+            launch_p2_i<DT, T_Q6_K>(p, s, ev);
+            return;
+        }
     }
+    launch_p2_i<DT, DT>(p, s, ev);
 }
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t s, const KernelEvents& ev) {
@@ -916,17 +1019,18 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t s, const KernelEve
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     switch (p.gate_type) {
-        case T_Q4_K: launch_p1_h<T_Q4_K>(p, s, ev); break;
-        case T_Q5_K: launch_p1_h<T_Q5_K>(p, s, ev); break;
-        case T_Q6_K: launch_p1_h<T_Q6_K>(p, s, ev); break;
-        default: launch_p1_h<T_Q3_K>(p, s, ev); break;
+        case T_Q4_K: launch_p1_t<T_Q4_K>(p, s, ev); break;
+        case T_Q5_K: launch_p1_t<T_Q5_K>(p, s, ev); break;
+        case T_Q6_K: launch_p1_t<T_Q6_K>(p, s, ev); break;
+        default: launch_p1_t<T_Q3_K>(p, s, ev); break;
     }
     if ((err = hipGetLastError()) != hipSuccess) return err;
     switch (p.down_type) {
-        case T_Q4_K: launch_p2_i<T_Q4_K>(p, s, ev); break;
-        case T_Q5_K: launch_p2_i<T_Q5_K>(p, s, ev); break;
-        case T_Q6_K: launch_p2_i<T_Q6_K>(p, s, ev); break;
-        default: launch_p2_i<T_Q3_K>(p, s, ev); break;
+        case T_Q4_K: launch_p2_t<T_Q4_K>(p, s, ev); break;
+        case T_Q5_K: launch_p2_t<T_Q5_K>(p, s, ev); break;
+        case T_Q6_K: launch_p2_t<T_Q6_K>(p, s, ev); break;
+        case T_Q8_0: launch_p2_t<T_Q8_0>(p, s, ev); break;
+        default: launch_p2_t<T_Q3_K>(p, s, ev); break;
     }
     if ((err = hipGetLastError()) != hipSuccess) return err;
     hipLaunchKernelGGL(k_prefill_combine, dim3((p.hidden + 255) / 256, p.n_tokens), dim3(256), 0, s, p);

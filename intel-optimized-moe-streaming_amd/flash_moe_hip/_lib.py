@@ -113,7 +113,7 @@ def _declare(lib: C.CDLL) -> C.CDLL:
     lib.mqh_moe_prefill_workspace_bytes.restype = _I64
     lib.mqh_moe_prefill.argtypes = [
         _I, _P, _I, _P, _I, _P, _I, _I, _I,      # routed types/tensors, n_experts, hidden, inter
-        _P, _P, _P, _P,                          # shared tensors, sh_gate_inp
+        _I, _P, _I, _P, _I, _P, _I, _P,          # shared types/tensors, sh_inter, sh_gate_inp
         _P, _I, _I, _P, _P, _I,                  # x, x_bf16, n_tokens, ids, weights, top_k
         _P, _P, _I64, _P,                        # y, workspace, ws bytes, stream
     ]

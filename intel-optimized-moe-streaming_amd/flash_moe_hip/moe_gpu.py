@@ -22,10 +22,13 @@ from .layer_store import ExpertLayer
 
 _NULL = None
 
-# shapes and types the grouped prefill kernels are built for
+# shapes and types the grouped prefill kernels are built for: gate/up in the
+# K-quants, down also Q8_0 (the reference model's first-layer down projection)
 PREFILL_TYPES = (11, 12, 13, 14)
+PREFILL_DOWN_TYPES = PREFILL_TYPES + (8,)
 PREFILL_DIMS = (256, 512, 1024, 2048)
 PREFILL_MAX_EXPERTS = 1024
+Q6_K = 14
 
 
 class MoeRunner:
@@ -211,21 +214,28 @@ class MoeRunner:
     def prefill_supported(layer: ExpertLayer) -> bool:
         """Whether the grouped prefill kernels cover this layer's routed experts."""
         t = layer.types
-        return (t["gate"] == t["up"] and all(t[r] in PREFILL_TYPES for r in ("gate", "up", "down"))
+        return (t["gate"] == t["up"] and t["gate"] in PREFILL_TYPES and t["down"] in PREFILL_DOWN_TYPES
                 and layer.hidden in PREFILL_DIMS and layer.intermediate in PREFILL_DIMS
                 and layer.n_experts <= PREFILL_MAX_EXPERTS)
 
     @staticmethod
     def _shared_in_prefill(layer: ExpertLayer) -> bool:
+        """Whether the layer's shared expert runs inside the grouped kernels:
+        the routed intermediate size, gate type == up type, each role the
+        routed type or Q6_K (the reference model's Q6_K shared experts)."""
         sh = layer.shared
-        return sh is not None and sh.types == layer.types and sh.intermediate == layer.intermediate
+        if sh is None or sh.intermediate != layer.intermediate:
+            return False
+        st, t = sh.types, layer.types
+        return (st["gate"] == st["up"] and st["gate"] in (t["gate"], Q6_K) and st["down"] in (t["down"], Q6_K))
 
     def prefill(self, layer: ExpertLayer, x, ids, weights, *, y=None, use_shared: bool = True, stream=None):
         """The layer for a prompt: x [T,H] FP32 or BF16, ids [T,k] int32, weights
         [T,k] FP32 (CUDA tensors).  Same result as ``decode`` up to FP32
-        summation order inside each dot product.  A shared expert whose types or
-        size differ from the routed experts' runs through the decode kernels and
-        is added after the routed sum, as in run_moe_sequence."""
+        summation order inside each dot product.  The shared expert runs inside
+        the grouped kernels when it has the routed size and, per role, the
+        routed type or Q6_K; any other shared expert runs through the decode
+        kernels and is added after the routed sum, as in run_moe_sequence."""
         import torch
 
         if not self.prefill_supported(layer):
@@ -258,8 +268,10 @@ class MoeRunner:
         rc = self.lib.mqh_moe_prefill(
             layer.types["gate"], t["gate"].data_ptr(), layer.types["up"], t["up"].data_ptr(),
             layer.types["down"], t["down"].data_ptr(), layer.n_experts, layer.hidden, layer.intermediate,
-            sh.gate.data_ptr() if inside else _NULL, sh.up.data_ptr() if inside else _NULL,
-            sh.down.data_ptr() if inside else _NULL,
+            sh.types["gate"] if inside else 0, sh.gate.data_ptr() if inside else _NULL,
+            sh.types["up"] if inside else 0, sh.up.data_ptr() if inside else _NULL,
+            sh.types["down"] if inside else 0, sh.down.data_ptr() if inside else _NULL,
+            sh.intermediate if inside else 0,
             sh.gate_inp.data_ptr() if (inside and sh.gate_inp is not None) else _NULL,
             x.data_ptr(), int(x.dtype == torch.bfloat16), T, ids.data_ptr(), weights.data_ptr(), top_k,
             y.data_ptr(), ws.data_ptr(), ws.numel(), stream.cuda_stream)

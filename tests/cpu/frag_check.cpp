@@ -75,6 +75,45 @@ void step(const uint32_t* r, int row, int q, int b, const Tile& t, int split, st
     }
 }
 
+// Q8_0: each step is one 32-column block with its own d, applied to that
+// step's product (the lane of k-group qq holds the d of blocks 2qq and 2qq+1)
+template <int M>
+void step_q8(const uint32_t* r, int row, int q, int b, const Tile& t, int split, std::vector<double>& P) {
+    std::vector<double> Pm(16 * 16, 0.0);
+    step<T_Q8_0, M>(r, row, q, b, t, split, Pm);
+    for (int j = 0; j < t.ntok; ++j) P[(M * 16 + row) * 16 + j] += Pm[row * 16 + j];
+}
+
+void gemm_q8(const uint8_t* w, int K, const Tile& t, int split, float* out) {
+    constexpr int BB = frag_unit_bytes<T_Q8_0>();
+    const int nb = K / 256;
+    std::vector<double> acc(16 * 16, 0.0);
+    for (int b = 0; b < nb; ++b) {
+        std::vector<double> P(8 * 16 * 16, 0.0);   // [step][row][token]
+        float d[16][8];
+        for (int l = 0; l < 64; ++l) {
+            const int row = l % 16, q = l / 16, qq = (q + 3) & 3;
+            uint32_t r[FragGeo<T_Q8_0>::NW];
+            frag_load<T_Q8_0>(w + (size_t)row * nb * BB + (size_t)b * BB, q, r);
+            step_q8<0>(r, row, q, b, t, split, P);
+            step_q8<1>(r, row, q, b, t, split, P);
+            step_q8<2>(r, row, q, b, t, split, P);
+            step_q8<3>(r, row, q, b, t, split, P);
+            step_q8<4>(r, row, q, b, t, split, P);
+            step_q8<5>(r, row, q, b, t, split, P);
+            step_q8<6>(r, row, q, b, t, split, P);
+            step_q8<7>(r, row, q, b, t, split, P);
+            d[row][2 * qq] = frag_h2f(r[16]);
+            d[row][2 * qq + 1] = frag_h2f(r[17]);
+        }
+        for (int m = 0; m < 8; ++m)
+            for (int row = 0; row < 16; ++row)
+                for (int j = 0; j < t.ntok; ++j) acc[row * 16 + j] += (double)d[row][m] * P[(m * 16 + row) * 16 + j];
+    }
+    for (int j = 0; j < t.ntok; ++j)
+        for (int row = 0; row < 16; ++row) out[(size_t)j * 16 + row] = (float)ldexp(acc[row * 16 + j], t.k[j]);
+}
+
 template <int T>
 void gemm(const uint8_t* w, int K, const Tile& t, int split, float* out) {
     constexpr int BB = block_bytes(T);
@@ -129,6 +168,7 @@ extern "C" void mqh_cpu_frag_gemm(int type, const uint8_t* w, int K, const float
         case T_Q4_K: gemm<T_Q4_K>(w, K, t, split, out); break;
         case T_Q5_K: gemm<T_Q5_K>(w, K, t, split, out); break;
         case T_Q6_K: gemm<T_Q6_K>(w, K, t, split, out); break;
+        case T_Q8_0: gemm_q8(w, K, t, split, out); break;
         default: gemm<T_Q3_K>(w, K, t, split, out); break;
     }
 }
@@ -152,6 +192,7 @@ extern "C" void mqh_cpu_frag_cover(int type, int* count) {
         case T_Q4_K: cover<T_Q4_K>(count); break;
         case T_Q5_K: cover<T_Q5_K>(count); break;
         case T_Q6_K: cover<T_Q6_K>(count); break;
+        case T_Q8_0: cover<T_Q8_0>(count); break;
         default: cover<T_Q3_K>(count); break;
     }
 }

@@ -7,7 +7,8 @@ of a super-block, unpacks the 8 consecutive columns it owns in each of the 8
 steps as exact FP16 integers sc*q (Q6_K: a split pair), the token rows enter as
 power-of-two-scaled FP16 high (+ low) planes read at the same columns, the
 Q4_K/Q5_K min term goes through the sub-block sums, and d / dmin are applied
-per super-block.  Every column of a super-block must be dealt exactly once.
+per super-block (Q8_0: each step is one 32-column block, its int8 quants the
+exact operand and its own d applied to the step's product).  Every column of a super-block must be dealt exactly once.
 The result must match the FP64 product of the oracle-dequantized rows to FP32
 rounding: the decomposition itself is exact, unlike FP16-rounded weights
 (which miss the 1e-3 bar on Q4_K through cancellation of the min offsets).
@@ -62,7 +63,7 @@ def frag_gemm(chk, t, rows, K, x, split):
     return out
 
 
-@pytest.mark.parametrize("t", [11, 12, 13, 14])
+@pytest.mark.parametrize("t", [11, 12, 13, 14, 8])
 @pytest.mark.parametrize("kind", ["normal", "heavy", "sparse", "large"])
 @pytest.mark.parametrize("split", [1, 0], ids=["fp32-x", "bf16-x"])
 def test_frag_gemm_matches_oracle(chk, oracle_mod, t, kind, split):
@@ -105,7 +106,7 @@ def test_all_zero_rows(chk):
     assert np.all(out == 0.0)
 
 
-@pytest.mark.parametrize("t", [11, 12, 13, 14])
+@pytest.mark.parametrize("t", [11, 12, 13, 14, 8])
 def test_lanes_cover_each_column_once(chk, t):
     count = np.zeros(256, np.int32)
     chk.mqh_cpu_frag_cover(t, count.ctypes.data)

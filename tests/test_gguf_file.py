@@ -321,7 +321,10 @@ def test_device_routes_a_file_layer_as_the_reference_router(tmp_path, oracle_mod
     for t in range(3):
         r_ids, r_w = router.route(X[t])
         assert ids[t].tolist() == r_ids, f"token {t}: device {ids[t].tolist()} reference {r_ids}"
-        np.testing.assert_allclose(wts[t], r_w, rtol=0, atol=2e-6)
+        # the scores here reach ~40 (one FP32 ulp = 3.8e-6): the device's
+        # summation order moves them by a few ulps against NumPy's, and the
+        # softmax weights by ~1e-5 of their value
+        np.testing.assert_allclose(wts[t], r_w, rtol=5e-5, atol=2e-6)
         ref = oracle_layer(oracle_mod, layer, host, shared, X[t], r_ids, r_w)
         err = oracle_mod.max_relative_error(y[t], ref)
         print(f"  token {t}: ids {r_ids} max rel err {err:.3e}", flush=True)

@@ -231,15 +231,14 @@ def test_backend_default_is_the_fp16_graph(oracle_mod, hip, via):
     native FP16 graph (native_expert.py:33-34): run_moe_layer through the fused
     hook and through forward() fan-out, at the reference's FP16-graph check
     magnitudes (d ~ 0.002, x ~ 0.05), against the oracle's FP16-graph experts
-    with the FP32-graph shared expert, at max relative error <= 5e-4, and
-    nearer to it than to the oracle's FP32 graph (the two graphs differ by
-    5-8e-4 here), so the graph is told apart."""
+    at max relative error <= 5e-4, and nearer to them than to the oracle's FP32
+    graph (the two graphs differ by 5-8e-4 here), so the graph is told apart.
+    No shared expert: it runs the FP32 graph in both, and its output would
+    dominate the maximum and hide the routed experts' graph."""
     from flash_moe_hip.backend import HipExpertBackend
     from flash_moe_hip.moe_layer import run_moe_layer
-    from flash_moe_hip.shared_expert import SharedExpert
 
-    layer, host, shared = make_layer(91, E, H, I, TYPES, shared_types={"gate": 14, "up": 14, "down": 14},
-                                     scale=0.002)
+    layer, host, shared = make_layer(91, E, H, I, TYPES, scale=0.002)
     rng = np.random.default_rng(92)
     W = (rng.standard_normal((H, E)) * 0.05).astype(np.float32)
 
@@ -252,12 +251,11 @@ def test_backend_default_is_the_fp16_graph(oracle_mod, hip, via):
     backend = HipExpertBackend({5: layer})
     try:
         assert backend.fp16_graph == 1
-        sh = SharedExpert.from_backend(backend)
         b = backend if via == "fused" else ProtocolOnly(backend)
         for i in range(3):
             x = (rng.standard_normal(H) * 0.05).astype(np.float32)
             print(f"FP16-graph run_moe_layer via {via} token {i}", flush=True)
-            got = run_moe_layer(5, x, Router(), b, H, I, shared_expert=sh)
+            got = run_moe_layer(5, x, Router(), b, H, I)
             ids, ws = oracle_mod.route(x, W, K)
             want16 = oracle_layer(oracle_mod, layer, host, shared, x, ids, ws, fp16=1)
             want32 = oracle_layer(oracle_mod, layer, host, shared, x, ids, ws, fp16=0)

@@ -330,7 +330,8 @@ DEQ_TYPES = (11, 12, 14, 8)
 class StepRunner:
     """Runs n steps of a sweep over `layers` layers (step i = layer i % layers)
     as replays of one captured graph of the whole sweep plus, for n % layers,
-    a graph of the first n % layers steps (captured on first use)."""
+    a graph of the first n % layers steps (captured on first use).
+    sweep(n, start=0) runs layers start .. start + n - 1."""
 
     def __init__(self, sweep, layers: int, dev, eager: bool = False):
         self.sweep, self.layers, self.dev, self.eager = sweep, layers, dev, eager
@@ -362,6 +363,11 @@ class StepRunner:
             self._replay(self.layers)
         if rem:
             self._replay(rem)
+        if not full:
+            # capturing the partial graph ran layers 0 .. rem - 1 last: run the
+            # other layers after them, so the timed layers are the least
+            # recently touched (the resident layers are ~3x the Infinity Cache)
+            self.sweep(self.layers - rem, rem)
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda._sleep(2_000_000)
@@ -630,17 +636,22 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
     return out
 
 
-def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
-    """128-token BF16 prompt through one layer (gate/up Q4_K, down Q6_K, top-8 of
-    N(0,1) logits + shared), n_layers seeded layers rotated."""
+def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float, types=None, shared_types=None,
+                  what: str = "gate/up Q4_K, down Q6_K, shared expert the same") -> dict:
+    """128-token BF16 prompt through one layer (default: gate/up Q4_K, down Q6_K,
+    top-8 of N(0,1) logits + a shared expert of the routed types), n_layers
+    seeded layers rotated."""
     import torch
 
     from flash_moe_hip.layer_store import ExpertLayer
     from flash_moe_hip.moe_gpu import MoeRunner
 
+    types = dict(types or TYPES)
+    shared_types = dict(shared_types or types)
     T = 128
-    layers = [ExpertLayer.synthetic(TYPES, E, H, I, seed=9000 + 1000 * l, shared_types=TYPES,
+    layers = [ExpertLayer.synthetic(types, E, H, I, seed=9000 + 1000 * l, shared_types=shared_types,
                                     shared_intermediate=I, gate_inp=True, device=dev) for l in range(n_layers)]
+    assert MoeRunner.prefill_supported(layers[0]) and MoeRunner._shared_in_prefill(layers[0])
     rng = np.random.default_rng(5)
     gen = torch.Generator().manual_seed(5)
     Xh, IDh, WSh = [], [], []
@@ -662,7 +673,7 @@ def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
     import oracle
 
     xf = Xh[0].float().numpy()
-    want = _oracle_tokens(layers[0], TYPES, xf, IDh[0], WSh[0], [0, 64, 127])
+    want = _oracle_tokens(layers[0], types, xf, IDh[0], WSh[0], [0, 64, 127])
     got = Y.cpu().numpy()
     err = max(oracle.max_relative_error(got[t], want[t]) for t in want)
     replay = _graph(lambda: [call(l) for l in range(n_layers)], dev)
@@ -670,19 +681,22 @@ def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
     kern = _kernel_pair_times([lambda l=l: call(l) for l in range(n_layers)], 3)
     U = [len(np.unique(v)) for v in IDh]
     flop = 2.0 * T * (K + 1) * 3 * H * I
-    nbytes = float(np.mean([(u + 1) * layers[0].bytes_per_expert() for u in U]))
-    gu = float(np.mean([(u + 1) * (layers[0].expert_bytes("gate") + layers[0].expert_bytes("up")) for u in U]))
+    L0 = layers[0]
+    sh_gu = L0.shared.gate.numel() + L0.shared.up.numel()
+    nbytes = float(np.mean([u * L0.bytes_per_expert() + L0.shared_bytes() for u in U]))
+    gu = float(np.mean([u * (L0.expert_bytes("gate") + L0.expert_bytes("up")) + sh_gu for u in U]))
     tflops = flop / (ms * 1e-3) / 1e12
     dom = "A" if kern["a_us"] >= kern["b_us"] else "B"
     dom_bytes = gu if dom == "A" else nbytes - gu
-    roof = _hbm_roofline("mqh::k_prefill_gate_up<12, 12, 8, true, 2>" if dom == "A" else "mqh::k_prefill_down<14, 14, 2, 1>",
-                         dom_bytes, kern["a_us"] if dom == "A" else kern["b_us"],
+    gt, dt, sgt, sdt = types["gate"], types["down"], shared_types["gate"], shared_types["down"]
+    name_a, name_b = f"mqh::k_prefill_gate_up<{gt}, {sgt}, 8, true, 2>", f"mqh::k_prefill_down<{dt}, {sdt}, 2, 1>"
+    roof = _hbm_roofline(name_a if dom == "A" else name_b, dom_bytes, kern["a_us"] if dom == "A" else kern["b_us"],
                          read_floor_us(int(dom_bytes)))
-    log(f"prefill: {ms * 1e3:.1f} us/layer, {tflops:.1f} TFLOP/s, parity {err:.2e}; "
+    log(f"prefill ({what}): {ms * 1e3:.1f} us/layer, {tflops:.1f} TFLOP/s, parity {err:.2e}; "
         f"gate/up {kern['a_us']:.1f} us, down {kern['b_us']:.1f} us")
     out = {
         "workload": f"prefill: {T}-token BF16 prompt, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
-                    f"logits + shared, gate/up Q4_K, down Q6_K, {n_layers} resident layers rotated",
+                    f"logits + shared, {what}, {n_layers} resident layers rotated",
         "metric": "prefill TFLOP/s (useful FLOPs: 1152 pairs x 6,291,456)", "value": round(tflops, 2),
         "unit": "TFLOP/s", "us_per_layer": round(ms * 1e3, 2), "flop_per_layer": int(flop),
         "weight_bytes_per_layer": int(nbytes), "weight_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
@@ -692,11 +706,10 @@ def bench_prefill(dev, n_layers: int, reps: int, cpu_seconds: float) -> dict:
         "mfma_ceiling": {"peak_tflops_fp16_dense": 2500.0, "frac": round(tflops / 2500.0, 5)},
         # matrix-core activity of the gate/up GEMM from the committed counter run
         # (useful FLOPs are about a quarter of those issued: ~4 of 16 token columns)
-        "mfma_counters": measured_mfma("mqh::k_prefill_gate_up<12, 12, 8, true, 2>"),
+        "mfma_counters": measured_mfma(name_a),
     }
     if cpu_seconds > 0:
-        L0 = layers[0]
-        jobs = [(TYPES, L0.host_expert(int(e)), xf[t]) for t in range(0, T, 8) for e in IDh[0][t]]
+        jobs = [(types, L0.host_expert(int(e)), xf[t]) for t in range(0, T, 8) for e in IDh[0][t]]
         calls, dt = _cpu_pairs(jobs, cpu_seconds, CPU_THREADS)
         per_layer = dt / calls * T * (K + 1)
         out["cpu_baseline"] = {"value": round(flop / per_layer / 1e12, 5), "unit": "TFLOP/s",
@@ -928,6 +941,92 @@ def bench_single_expert(dev, reps: int, cpu_seconds: float) -> dict:
     return out
 
 
+def bench_reference_callers(dev, reps: int) -> dict:
+    """The paths a caller of the reference's Python API takes without edits,
+    timed on the host clock (each call stages host buffers over PCIe and
+    synchronises): NativeExpert.forward (native_expert.py:23-37; the config-1
+    Q4_K expert's 1.77 MB of host bytes staged per call, FP32 graph since the
+    FP16 graph overflows on those scales), and run_moe_layer
+    (moe_layer.py:39-107) over HipExpertBackend with resident weights, through
+    the backend's fused hook and through forward() fanned out on its 4-worker
+    executor, on the headline layer shape in the reference decode's FP16 graph
+    (scales of the reference's FP16-graph check, d ~ 0.002, x ~ 0.05).  These
+    are PCIe- and host-inclusive latencies, not kernel throughput."""
+    import torch
+
+    import oracle
+    from flash_moe_hip.backend import HipExpertBackend
+    from flash_moe_hip.layer_store import ExpertLayer
+    from flash_moe_hip.moe_layer import run_moe_layer
+    from flash_moe_hip.native_expert import NativeExpert
+    from flash_moe_hip.shared_expert import SharedExpert
+    from flash_moe_hip.synthetic import config1_expert
+
+    def per_call_us(fn, n):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        return round((time.perf_counter() - t0) / n * 1e6, 1)
+
+    tensors, kinds, x = config1_expert(0)
+    native = NativeExpert()
+    native.fp16_graph = 0
+    err_native = oracle.max_relative_error(native.forward(tensors, kinds, x, H, I),
+                                           oracle.expert_forward(tensors, kinds, x, H, I, 0))
+    us_native = per_call_us(lambda: native.forward(tensors, kinds, x, H, I), reps)
+
+    layer = ExpertLayer.synthetic(TYPES, E, H, I, seed=31, shared_types=TYPES, shared_intermediate=I,
+                                  gate_inp=True, scale=0.002, device=dev)
+    rng = np.random.default_rng(31)
+    W = (rng.standard_normal((H, E)) * 0.02).astype(np.float32)
+    xs = [(rng.standard_normal(H) * 0.05).astype(np.float32) for _ in range(8)]
+
+    class Router:
+        top_k = K
+
+        def route(self, v):
+            return oracle.route(v, W, K)
+
+    class ProtocolOnly:   # the attributes a reference backend has (no fused hook)
+        def __init__(self, b):
+            self._b, self.store, self._moe_executor = b, b.store, b._moe_executor
+
+        def forward(self, *a):
+            return self._b.forward(*a)
+
+    backend = HipExpertBackend({0: layer})
+    try:
+        sh = SharedExpert.from_backend(backend)
+        router = Router()
+        res = {}
+        for name, b in (("fused_hook", backend), ("forward_fan_out", ProtocolOnly(backend))):
+            i = [0]
+
+            def one(b=b):
+                i[0] += 1
+                return run_moe_layer(0, xs[i[0] % len(xs)], router, b, H, I, shared_expert=sh)
+
+            res[name] = per_call_us(one, max(4, reps // 4))
+        torch.cuda.synchronize()
+    finally:
+        backend.close()
+    log(f"reference callers: NativeExpert.forward {us_native} us, run_moe_layer fused {res['fused_hook']} us, "
+        f"forward fan-out {res['forward_fan_out']} us")
+    del layer
+    torch.cuda.empty_cache()
+    return {
+        "workload": "the reference's Python entry points unchanged: NativeExpert.forward on one Q4_K expert "
+                    "(host bytes, staged per call) and run_moe_layer over HipExpertBackend (resident weights, "
+                    "host x, host routing) on the headline layer shape in the FP16 graph",
+        "metric": "us per call, host clock (PCIe- and synchronisation-inclusive)",
+        "higher_is_better": False,
+        "native_expert_forward_us": us_native, "native_expert_parity_max_rel_err": float(f"{err_native:.3e}"),
+        "run_moe_layer_fused_hook_us": res["fused_hook"],
+        "run_moe_layer_forward_fan_out_us": res["forward_fan_out"],
+    }
+
+
 def bench_deltanet(dev, reps: int, cpu_seconds: float) -> dict:
     """The DeltaNet decode recurrence (moe_delta_heads) of the reference model's
     recurrent layers: 30 layers, each a [32 heads x 128 x 128] FP32 state
@@ -1010,7 +1109,8 @@ def main() -> int:
     ap.add_argument("--only-decode", action="store_true", help="skip the batched-decode, prefill and dequant lines")
     # single_expert (one Q4_K expert, one token) runs the headline's gate/up kernel
     # instance: a profile of the headline kernels leaves it out (--workloads)
-    ap.add_argument("--workloads", default="single_expert,fp16_graph_decode,batched_decode,prefill,dequant,deltanet",
+    ap.add_argument("--workloads", default="single_expert,fp16_graph_decode,batched_decode,prefill,"
+                                           "prefill_q3k_q6k_shared,dequant,deltanet,reference_callers",
                     help="comma-separated workloads run after the headline decode")
     ap.add_argument("--extra-cpu-seconds", type=float, default=4.0)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
@@ -1038,8 +1138,9 @@ def main() -> int:
     Y = torch.empty((args.layers, H), dtype=torch.float32, device=dev)
     runner = MoeRunner(dev)
 
-    def sweep(n=args.layers):
-        for l in range(n):
+    def sweep(n=args.layers, start=0):
+        for l in range(start, start + n):
+            l %= args.layers
             runner.decode(layers[l], X[l:l + 1], IDS[l:l + 1], WS[l:l + 1], y=Y[l:l + 1])
 
     # eager warm-up (allocates the workspace), parity spot check on four layers
@@ -1132,8 +1233,14 @@ def main() -> int:
             "fp16_graph_decode": lambda: bench_fp16_graph_decode(dev, args.layers, 20, cpu_s),
             "batched_decode": lambda: bench_batched_decode(dev, args.layers, 25 * args.layers, cpu_s),
             "prefill": lambda: bench_prefill(dev, 8, 20, cpu_s),
+            # the reference model's layers 5-34 (docs/PHASE0_FINDINGS.md:60-69)
+            "prefill_q3k_q6k_shared": lambda: bench_prefill(
+                dev, 8, 20, cpu_s, types={"gate": 11, "up": 11, "down": 11},
+                shared_types={"gate": 14, "up": 14, "down": 14},
+                what="every routed matrix Q3_K, the shared expert Q6_K (the reference model's layers 5-34)"),
             "dequant": lambda: bench_dequant(dev, 10, cpu_s),
             "deltanet": lambda: bench_deltanet(dev, 50, cpu_s),
+            "reference_callers": lambda: bench_reference_callers(dev, 40),
         }
         result["workloads"] = {name: run() for name, run in runs.items() if name in wanted}
     print(json.dumps(result), flush=True)

@@ -202,3 +202,48 @@ def test_prefill_full_scale(oracle_mod, hip):
     assert max(errs) <= PREFILL_TOL, (int(np.argmax(errs)), max(errs))
     del layer
     torch.cuda.empty_cache()
+
+
+# The reference model's MoE layers (docs/PHASE0_FINDINGS.md:60-69): a Q6_K
+# shared expert in every layer, beside Q3_K routed matrices (layers 5-34),
+# Q4_K gate/up with a Q6_K down (layers 1-4, 35-39) or a Q8_0 down (layer 0).
+REAL_MIXES = {
+    "L5-34": {"gate": 11, "up": 11, "down": 11},
+    "L1-4": {"gate": 12, "up": 12, "down": 14},
+    "L0": {"gate": 12, "up": 12, "down": 8},
+}
+
+
+@pytest.mark.parametrize("mix", list(REAL_MIXES))
+def test_prefill_real_model_mix_full_scale(oracle_mod, hip, mix):
+    """A 128-token BF16 prompt through one layer of the reference model's type
+    mix at full size (256 experts, hidden 2048, intermediate 512, top-8 + the
+    Q6_K shared expert): the shared expert runs inside the grouped kernels
+    (no decode-kernel fallback), every token within 1e-4 of the oracle's
+    run_moe_sequence arithmetic (moe_layer.py:110-195, shared_expert.py:200-219)."""
+    import torch
+
+    from flash_moe_hip.layer_store import ExpertLayer
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    types = REAL_MIXES[mix]
+    q6 = {"gate": 14, "up": 14, "down": 14}
+    layer = ExpertLayer.synthetic(types, E, H, I, seed=9100 + len(mix), shared_types=q6, shared_intermediate=I,
+                                  gate_inp=True, device="cuda")
+    assert MoeRunner.prefill_supported(layer) and MoeRunner._shared_in_prefill(layer)
+    host, shared, gi = _host_layer(layer)
+    rng = np.random.default_rng(6 + len(mix))
+    T = 128
+    xb = torch.randn((T, H), generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    X = xb.float().numpy()
+    ids, ws = _topk(rng, T)
+    print(f"prefill {mix} {types} + Q6_K shared: {len(np.unique(ids))} distinct experts", flush=True)
+    want = _oracle_tokens(oracle_mod, layer, host, shared, gi, X, ids, ws)
+    runner = MoeRunner()
+    got, rc = runner.fetch(runner.prefill(layer, xb.cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(ws).cuda()))
+    assert rc == 0
+    errs = [oracle_mod.max_relative_error(got[t], want[t]) for t in range(T)]
+    print(f"  prefill {mix} max rel err over {T} tokens: {max(errs):.3e}", flush=True)
+    assert max(errs) <= PREFILL_TOL, (int(np.argmax(errs)), max(errs))
+    del layer
+    torch.cuda.empty_cache()

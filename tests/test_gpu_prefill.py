@@ -248,3 +248,49 @@ def test_prefill_sweep(oracle_mod, hip, seed):
     got, st_ = run_prefill(layer, X, ids, ws, x_bf16=xb)
     assert st_ == 0
     check(oracle_mod, layer, host, shared, X, ids, ws, got, f"sweep {seed}")
+
+
+@pytest.mark.parametrize("routed", [(11, 11), (12, 8), (13, 14), (12, 11), (11, 8)])
+@pytest.mark.parametrize("shape", [(256, 256), (512, 1024), (1024, 2048), (2048, 512)])
+def test_prefill_q6k_shared_beside_other_routed_types(oracle_mod, hip, routed, shape):
+    """A Q6_K shared expert in the grouped launches beside routed experts of
+    other types (its tiles run their own instance of the GEMM body), and Q8_0
+    down projections (per-block scales applied per MFMA step): every token
+    against the oracle, BF16 tokens for even intermediate sizes (the high
+    plane only) and FP32 tokens for the others (both planes)."""
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    gt, dt = routed
+    H, I = shape
+    kinds = {"gate": gt, "up": gt, "down": dt}
+    q6 = {"gate": 14, "up": 14, "down": 14}
+    layer, host, shared = make_layer(700 + gt + dt + H // 256 + I, 12, H, I, kinds, shared_types=q6)
+    assert MoeRunner._shared_in_prefill(layer)
+    rng = np.random.default_rng(gt * 31 + dt + H + I)
+    T = 37
+    x_bf16 = (I // 256) % 2 == 0
+    X = rng.standard_normal((T, H)).astype(np.float32)
+    if x_bf16:
+        X = bf16(X)
+    ids, ws = routing(rng, T, 12, 4)
+    print(f"prefill routed={routed} + Q6_K shared H={H} I={I} T={T} bf16={x_bf16}", flush=True)
+    got, st = run_prefill(layer, X, ids, ws, x_bf16=x_bf16)
+    assert st == 0
+    check(oracle_mod, layer, host, shared, X, ids, ws, got, f"routed {routed} shape {shape}")
+
+
+@pytest.mark.parametrize("shape", [(512, 256), (2048, 1024)])
+def test_prefill_q8_0_down_without_shared(oracle_mod, hip, shape):
+    """Q8_0 down projections with no shared expert, and the shared expert
+    switched off on a layer that has one (use_shared=False)."""
+    H, I = shape
+    kinds = {"gate": 12, "up": 12, "down": 8}
+    layer, host, shared = make_layer(750 + H + I, 6, H, I, kinds, shared_types={"gate": 14, "up": 14, "down": 14})
+    rng = np.random.default_rng(H + I)
+    T = 23
+    X = rng.standard_normal((T, H)).astype(np.float32)
+    ids, ws = routing(rng, T, 6, 3)
+    print(f"prefill Q8_0 down, no shared, H={H} I={I}", flush=True)
+    got, st = run_prefill(layer, X, ids, ws, use_shared=False)
+    assert st == 0
+    check(oracle_mod, layer, host, None, X, ids, ws, got, f"Q8_0 down {shape}")

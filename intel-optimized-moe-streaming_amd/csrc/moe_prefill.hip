@@ -61,7 +61,7 @@ constexpr int PF_ROWS_DOWN = 128; // down rows per workgroup chunk: 8 waves x 16
 // register allocation is the larger body's: its ring is shallower, so that
 // a Q6_K shared expert does not cost the routed tiles their occupancy.
 #ifndef PF_RING_SHARED
-#define PF_RING_SHARED 2
+#define PF_RING_SHARED 3
 #endif
 constexpr int PF_PAD = 8;        // LDS row padding (halves)
 
@@ -629,7 +629,11 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
         if (w < wave) { bc += wsum[w][0]; bt += wsum[w][1]; }
         tott += wsum[w][1];
     }
-    const int first = bc + ic - c, tfirst = bt + it - tc;
+    // the shared expert's tiles come first (tile j: tokens 16 j .. 16 j + 15):
+    // they are the fullest tiles and, with a shared expert of another type, the
+    // slowest, so they start in the launch's first round rather than its tail
+    const int nsh = p.has_shared ? (T + PREFILL_TILE - 1) / PREFILL_TILE : 0;
+    const int first = bc + ic - c, tfirst = nsh + bt + it - tc;
     if (e < E) {
         off[e] = first;
         toff[e] = tfirst;
@@ -637,12 +641,9 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
             ((int4*)p.tiles)[tfirst + j] =
                 make_int4(e, first + PREFILL_TILE * j, min(PREFILL_TILE, c - PREFILL_TILE * j), 0);
     }
-    if (threadIdx.x == 0) {
-        int nt = tott;
-        if (p.has_shared)
-            for (int j = 0; j < T; j += PREFILL_TILE) ((int4*)p.tiles)[nt++] = make_int4(-1, TK + j, min(PREFILL_TILE, T - j), 0);
-        *p.n_tiles = nt;
-    }
+    for (int j = threadIdx.x; j < nsh; j += PF_ROUTE_THREADS)
+        ((int4*)p.tiles)[j] = make_int4(-1, TK + PREFILL_TILE * j, min(PREFILL_TILE, T - PREFILL_TILE * j), 0);
+    if (threadIdx.x == 0) *p.n_tiles = nsh + tott;
     __syncthreads();
     // pair order inside an expert follows the atomics; a pair's result does not
     // depend on its column in the tile, so outputs do not depend on it
@@ -659,8 +660,8 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
     }
     if (p.has_shared) {
         for (int t = threadIdx.x; t < T; t += PF_ROUTE_THREADS) p.pos[t * p.S + K] = TK + t;
-        // the shared tiles follow the routed ones: column c of shared tile j is token 16 j + c
-        for (int t = threadIdx.x; t < T; t += PF_ROUTE_THREADS) p.tile_tok[tott * PREFILL_TILE + t] = t;
+        // column c of shared tile j is token 16 j + c
+        for (int t = threadIdx.x; t < T; t += PF_ROUTE_THREADS) p.tile_tok[t] = t;
     }
 }
 

@@ -26,11 +26,12 @@ prefill kernels' exact FP16 products with FP32 accumulation stay within 1e-4
 of the FP32 graph.
 
 All arithmetic runs in the HIP kernels; results come back as NumPy FP32 like
-the reference backend's.  Each call stages its inputs through one pinned host
-buffer (one host-to-device copy) and returns after one synchronisation, which
-also reads the kernels' fault flags.  The calls are thread-safe: the reference
-runs ``forward`` for a token's experts on the backend's ``_moe_executor``
-(``moe_layer.py:74-94``), and every worker thread has a workspace of its own.
+the reference backend's.  Each call stages its inputs through the calling
+thread's pinned host buffer (one host-to-device copy, no allocation) and
+returns after one synchronisation, which also reads the kernels' fault
+flags.  The calls are thread-safe: the reference runs ``forward`` for a
+token's experts on the backend's ``_moe_executor`` (``moe_layer.py:74-94``),
+and every worker thread has a workspace and pinned buffers of its own.
 """
 from __future__ import annotations
 
@@ -93,19 +94,13 @@ class HipExpertBackend:
         x = np.asarray(activations, dtype=np.float32).reshape(-1, hidden)
         T = x.shape[0]
         k = 0 if ids is None else int(np.asarray(ids).reshape(T, -1).shape[1])
-        host = torch.empty(T * hidden + 2 * T * k, dtype=torch.float32, pin_memory=True)
-        h = host.numpy()
-        h[:T * hidden] = x.reshape(-1)
-        if k:
-            h[T * hidden:T * (hidden + k)].view(np.int32)[:] = np.asarray(ids, dtype=np.int64).reshape(-1)
-            h[T * (hidden + k):] = np.asarray(weights, dtype=np.float32).reshape(-1)
-        dev = host.to(self.device, non_blocking=True)
-        xd = dev[:T * hidden].view(T, hidden)
         if not k:
-            return xd, None, None
-        idd = dev[T * hidden:T * (hidden + k)].view(torch.int32).view(T, k)
-        wd = dev[T * (hidden + k):].view(T, k)
-        return xd, idd, wd
+            (xd,) = self.runner.upload([x])
+            return xd.view(torch.float32).view(T, hidden), None, None
+        xd, idd, wd = self.runner.upload([x, np.asarray(ids, dtype=np.int64).reshape(T, k).astype(np.int32),
+                                          np.asarray(weights, dtype=np.float32).reshape(T, k)])
+        return (xd.view(torch.float32).view(T, hidden), idd.view(torch.int32).view(T, k),
+                wd.view(torch.float32).view(T, k))
 
     def _finish(self, y, what: str) -> np.ndarray:
         out, rc = self.runner.fetch(y)

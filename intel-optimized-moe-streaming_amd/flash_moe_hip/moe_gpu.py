@@ -17,6 +17,8 @@ from __future__ import annotations
 
 import threading
 
+import numpy as np
+
 from . import _lib
 from .layer_store import ExpertLayer
 
@@ -44,6 +46,50 @@ class MoeRunner:
     @property
     def _ws(self):
         return getattr(self._local, "ws", None)
+
+    def pinned(self, slot: str, nbytes: int):
+        """The calling thread's pinned host buffer `slot` (uint8, at least
+        `nbytes`, grown on demand and kept): host-staged calls reuse it
+        instead of allocating pinned memory per call, which costs hundreds of
+        microseconds each time.  The caller must have finished with the
+        previous contents (every host-staged call synchronizes before
+        returning)."""
+        import torch
+
+        buf = getattr(self._local, "pin_" + slot, None)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(int(nbytes), 1 << 16), dtype=torch.uint8, pin_memory=True)
+            setattr(self._local, "pin_" + slot, buf)
+        return buf[:nbytes]
+
+    def upload(self, arrays, slot: str = "stage", stream=None):
+        """Copy host arrays to the device through the calling thread's pinned
+        buffer `slot`: one host-to-device copy, enqueued on `stream`; returns
+        the device views (uint8 flat, in order).  Waits first for this slot's
+        previous copy, so a call that raised before synchronizing cannot have
+        its buffer overwritten under a copy in flight."""
+        import torch
+
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        prev = getattr(self._local, "ev_" + slot, None)
+        if prev is not None:
+            prev.synchronize()
+        raws = [np.ascontiguousarray(a).reshape(-1).view(np.uint8) for a in arrays]
+        offs, n = [], 0
+        for r in raws:
+            offs.append(n)
+            n += (r.size + 15) & ~15
+        host = self.pinned(slot, n)
+        h = host.numpy()
+        for r, o in zip(raws, offs):
+            h[o:o + r.size] = r
+        with torch.cuda.stream(stream):
+            dev = host.to(self.device, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(stream)
+        setattr(self._local, "ev_" + slot, ev)
+        return [dev[o:o + r.size] for r, o in zip(raws, offs)]
 
     def _workspace(self, n_tokens: int, top_k: int, inter: int, sh_inter: int, stream):
         need = int(self.lib.mqh_moe_workspace_bytes(n_tokens, top_k, inter, sh_inter))
@@ -301,15 +347,17 @@ class MoeRunner:
         if stream is None:
             stream = torch.cuda.current_stream(self.device)
         ws = self._ws
+        nbytes = y.numel() * y.element_size()
+        host = self.pinned("fetch", nbytes + 8)
         with torch.cuda.stream(stream):
-            out = torch.empty(y.shape, dtype=y.dtype, pin_memory=True)
+            out = host[:nbytes].view(y.dtype).view(y.shape)
             out.copy_(y, non_blocking=True)
             flags = None
             if ws is not None:
-                flags = torch.empty(2, dtype=torch.int32, pin_memory=True)
+                flags = host[nbytes:nbytes + 8].view(torch.int32)
                 flags.copy_(ws[:8].view(torch.int32), non_blocking=True)
         stream.synchronize()
         rc = 0
         if flags is not None and bool(flags.any()):
             rc = int(self.lib.mqh_status(ws.data_ptr(), stream.cuda_stream))
-        return out.numpy(), rc
+        return out.numpy().copy(), rc

@@ -133,7 +133,9 @@ class SharedExpert:
         import torch
 
         sh = self.layers[layer]
-        xd = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(self.runner.device)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        (xd,) = self.runner.upload([x], slot="shared")
+        xd = xd.view(torch.float32).view(x.shape)
         y = self.runner.decode_shared(sh, self.hidden_size, xd)
         out, rc = self.runner.fetch(y)
         if rc:

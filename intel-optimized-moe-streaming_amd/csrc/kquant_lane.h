@@ -419,6 +419,12 @@ __host__ __device__ inline float sub_rn(float a, float b) {
 #endif
 }
 
+// the FP16 value of the low / high half of v, in FP32 (exact, subnormals included)
+__host__ __device__ inline float half_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)v); }
+__host__ __device__ inline float half_hi(uint32_t v) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+}
+
 // w[j] = f(byte j of the 4 dwords at q) for 16 bytes, packed as FP16 pairs into out[0..7]
 template <class F>
 __host__ __device__ inline void pack16_bytes(const uint32_t* q, uint32_t* out, F&& f) {
@@ -469,17 +475,44 @@ __host__ __device__ inline void lane_w16_piece(const uint32_t* raw, int k, uint3
         k4_scale_min_pair(raw, k, sc2, mn2);
         const float d1 = detail::mul_rn(d, (float)((sc2 >> (8 * r)) & 0xFFu));
         const float m1 = detail::mul_rn(dmin, (float)((mn2 >> (8 * r)) & 0xFFu));
-        uint32_t q[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            q[i] = (raw[QS + 4 * p + i] >> (4 * r)) & 0x0F0F0F0Fu;
-            if constexpr (T == T_Q5_K) q[i] |= ((raw[4 + 4 * p + i] >> (2 * k + r)) & 0x01010101u) << 4;
-        }
         // RN(RN(d1 q) - m1) as one fused multiply-add: d1 = d sc has at most 17
         // significant bits (FP16 d, 6-bit sc), so d1 q (q < 32) has at most 22 and
         // RN(d1 q) = d1 q; the fused form rounds d1 q - m1 once, as the
-        // reference's subtraction does (one instruction a weight instead of two)
-        detail::pack16_bytes(q, out, [&](float b) { return fmaf(d1, b, -m1); });
+        // reference's subtraction does.  The quants enter the multiply-add as
+        // FP16 subnormals: a 16-bit half holding the integer v is v 2^-24
+        // exactly, so the masked halves of a quant dword (bytes 0 and 2, then 1
+        // and 3) times d1 2^24 (exact: a power of two) give d1 q.  gfx950 reads
+        // an FP16 operand from either half of a register in v_fma_mix_f32, so a
+        // weight is one instruction, with no byte extraction or conversion.  A
+        // Q4_K high nibble stays in place (16 q in the half) with d1 2^20.
+        uint32_t e[4], o[4];
+        float ds;
+        if constexpr (T == T_Q4_K) {
+            constexpr uint32_t M = r == 0 ? 0x000F000Fu : 0x00F000F0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t w = raw[QS + 4 * p + i];
+                e[i] = w & M;
+                o[i] = (w >> 8) & M;
+            }
+            ds = d1 * (r == 0 ? 16777216.0f : 1048576.0f);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t q = ((raw[QS + 4 * p + i] >> (4 * r)) & 0x0F0F0F0Fu) |
+                                   (((raw[4 + 4 * p + i] >> (2 * k + r)) & 0x01010101u) << 4);
+                e[i] = q & 0x00FF00FFu;
+                o[i] = (q >> 8) & 0x00FF00FFu;
+            }
+            ds = d1 * 16777216.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float w0 = fmaf(ds, detail::half_lo(e[i]), -m1), w1 = fmaf(ds, detail::half_lo(o[i]), -m1);
+            const float w2 = fmaf(ds, detail::half_hi(e[i]), -m1), w3 = fmaf(ds, detail::half_hi(o[i]), -m1);
+            out[2 * i] = pack_rn16(w0, w1);
+            out[2 * i + 1] = pack_rn16(w2, w3);
+        }
     } else if constexpr (T == T_Q6_K) {
         // q - 32 for the 6-bit u: its two's complement is u ^ 32 in bits 2..7 of a
         // byte (low nibble rotated to bits 2..5, the two high bits to 6..7, the

@@ -305,7 +305,16 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     const int per_slot = h.a_inter / RPI;
     const int n_items = h.S * per_slot, wg_items = h.a_waves * IPW;
     if (xg * wg_items >= n_items) return;   // padding of the last group of eight (no division on this path)
-    const int item = uniform((xg * h.a_waves + wave) * IPW);
+    // Items are dealt in order (a workgroup's waves take consecutive items,
+    // mostly of one slot), or, with one wave per slot and one item a wave
+    // (then per_slot workgroups), by slot: wave s takes slot s's row group xg.
+    // A CU's nine waves are then eight routed items and the shared expert's,
+    // and the SIMD that holds three of them holds the shared one, which in
+    // the FP16 graph runs the cheaper integer-digit path.  (The routed
+    // prologue needs consecutive slots per workgroup: it ranks only as many
+    // experts as its workgroup uses.)
+    const bool by_slot = !ROUTED && IPW == 1 && h.a_waves == h.S;
+    const int item = uniform(by_slot ? wave * per_slot + xg : (xg * h.a_waves + wave) * IPW);
     const bool live = item < h.S * per_slot;
     const int s = live ? item >> __builtin_ctz(per_slot) : 0;
     const int row0 = live ? (item & (per_slot - 1)) * RPI : 0;

@@ -606,7 +606,7 @@ int mqh_moe_prefill(int gate_type, const void* gate, int up_type, const void* up
     p.y = y;
     p.flags = (int*)(WS + L.flags_off); p.sh_scale = (float*)(WS + L.scale_off);
     p.tiles = (int*)(WS + L.tiles_off); p.n_tiles = (int*)(WS + L.ntiles_off);
-    p.tile_tok = (int*)(WS + L.tok_off); p.pos = (int*)(WS + L.pos_off);
+    p.tile_tok = (int*)(WS + L.tok_off); p.tile_dst = (int*)(WS + L.dst_off);
     p.act = (float*)(WS + L.act_off); p.ypair = (float*)(WS + L.ypair_off);
     p.xhi = (uint16_t*)(WS + L.xhi_off); p.xlo = (uint16_t*)(WS + L.xlo_off);
     p.xsum = (uint32_t*)(WS + L.xsum_off); p.xexp = (int*)(WS + L.xexp_off);

@@ -83,8 +83,13 @@ inline WorkspaceLayout decode_workspace_layout(int n_tokens, int top_k, int inte
 
 // Grouped prefill (moe_prefill.hip).  Token/slot pairs are bucketed by expert
 // on the device; a tile is up to PREFILL_TILE tokens of one expert (or of the
-// shared expert, expert id -1).
-constexpr int PREFILL_TILE = 16;
+// shared expert, expert id -1): 8 or 16 (the MFMA's 16 token columns; with 8,
+// columns 8..15 repeat 0..7 and their results are dropped).
+#ifndef MQH_PREFILL_TILE
+#define MQH_PREFILL_TILE 16
+#endif
+constexpr int PREFILL_TILE = MQH_PREFILL_TILE;
+static_assert(PREFILL_TILE == 8 || PREFILL_TILE == 16, "prefill tiles of 8 or 16 tokens");
 constexpr int PREFILL_MAX_EXPERTS = 1024;
 
 struct PrefillParams {
@@ -113,10 +118,10 @@ struct PrefillParams {
     float* sh_scale;        // [n_tokens]
     int* tiles;             // [max_tiles x 4]: expert, first pair, token count, 0
     int* n_tiles;           // [1]
-    int* tile_tok;          // [max_tiles x 16]: token of column c of tile i (stale past the tile's count)
-    int* pos;               // [n_tokens x S]: sorted pair index of (token, slot)
-    float* act;             // [P x inter] SwiGLU activations
-    float* ypair;           // [P x hidden] expert outputs per pair
+    int* tile_tok;          // [max_tiles x PREFILL_TILE]: token of column c of tile i (stale past the tile's count)
+    int* tile_dst;          // [max_tiles x PREFILL_TILE]: its output row t S + s (token t, slot s)
+    float* act;             // [P x inter] SwiGLU activations, in sorted pair order
+    float* ypair;           // [P x hidden] expert outputs, row t S + s
     // the tokens as the gate/up kernel's B operand, made once per token by the
     // route pass: FP16 high and low planes [n_tokens x hidden] at scale 2^-k,
     // the 32-column sub-block sums [n_tokens x hidden / 32] as (high, low)
@@ -129,7 +134,7 @@ struct PrefillParams {
 };
 
 struct PrefillLayout {
-    int64_t flags_off, scale_off, tiles_off, ntiles_off, tok_off, pos_off, act_off, ypair_off;
+    int64_t flags_off, scale_off, tiles_off, ntiles_off, tok_off, dst_off, act_off, ypair_off;
     int64_t xhi_off, xlo_off, xsum_off, xexp_off, total;
     int max_tiles;
 };

@@ -47,19 +47,25 @@ constexpr int PF_ROWS_DOWN = 128; // down rows per workgroup chunk: 8 waves x 16
 #ifndef PF_SMALL_GU
 #define PF_SMALL_GU 2
 #endif
+// Down row chunks per workgroup: one (two: 63 -> 88 us, four: 93 us for the
+// 128-token prompt's Q6_K down projections -- fewer workgroups in flight).
 #ifndef PF_CPW_DOWN
-#define PF_CPW_DOWN 1            // down row chunks per workgroup
+#define PF_CPW_DOWN 1
 #endif
+// Register ring of super-blocks per lane (R - 1 in flight).  Three: the
+// mixed-type gate/up kernel (Q3_K routed, Q6_K shared) holds 126 VGPRs and
+// two workgroups a CU (155 and one a CU with four: 107 -> 94 us at the
+// 128-token prompt), Q4_K gate/up 77 -> 75 us; six measured slower.
 #ifndef PF_RING
-#define PF_RING 4                // register ring of super-blocks per lane (R - 1 in flight)
+#define PF_RING 3
 #endif
 #ifndef PF_RING_DOWN
 #define PF_RING_DOWN PF_RING
 #endif
 // A shared expert of another type than the routed experts runs in the same
 // launch (its tiles take their own instance of the body), and the kernel's
-// register allocation is the larger body's: its ring is shallower, so that
-// a Q6_K shared expert does not cost the routed tiles their occupancy.
+// register allocation is the larger body's: its ring may be set shallower, so
+// that a Q6_K shared expert does not cost the routed tiles their occupancy.
 #ifndef PF_RING_SHARED
 #define PF_RING_SHARED 3
 #endif
@@ -387,7 +393,7 @@ struct PfRows {
         static_assert(NMAT == 1, "one Q8_0 matrix a wave");
         constexpr int KP = NB * 256 + PF_PAD;
         __shared__ __attribute__((aligned(16))) float s_d8[PF_WAVES][8][16];
-        const int lane = threadIdx.x & 63, tok = lane & 15, qq = (q + 3) & 3;
+        const int lane = threadIdx.x & 63, tok = lane & (PREFILL_TILE - 1), qq = (q + 3) & 3;
         const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
         s_d8[wave][2 * qq][lane & 15] = frag_h2f(cur[0][16]);
         s_d8[wave][2 * qq + 1][lane & 15] = frag_h2f(cur[0][17]);
@@ -418,7 +424,8 @@ struct PfRows {
     __device__ __forceinline__ void block_k(const uint32_t (&cur)[NMAT][NW], int kb, const _Float16* xh,
                                             const _Float16* xl, const _Float16* xs, f32x4 (&acc)[NMAT]) {
         constexpr int KP = NB * 256 + PF_PAD;
-        const int lane = threadIdx.x & 63, tok = lane & 15;
+        // B column lane % 16 reads LDS token column lane % PREFILL_TILE
+        const int lane = threadIdx.x & 63, tok = lane & (PREFILL_TILE - 1);
         const int brow = tok * KP + kb * 256 + frag_lane_col<T>((q + 3) & 3);
         f32x4 P[NMAT];
         FragPrep<T> sp[NMAT];
@@ -646,22 +653,25 @@ __global__ __launch_bounds__(PF_ROUTE_THREADS) void k_prefill_route(PrefillParam
     if (threadIdx.x == 0) *p.n_tiles = nsh + tott;
     __syncthreads();
     // pair order inside an expert follows the atomics; a pair's result does not
-    // depend on its column in the tile, so outputs do not depend on it
+    // depend on its column in the tile, so outputs do not depend on it.  Each
+    // column also gets the output row of its (token, slot), where the down
+    // kernel writes it and the combine reads it.
     for (int i = threadIdx.x; i < TK; i += PF_ROUTE_THREADS) {
         const int j = (i - threadIdx.x) / PF_ROUTE_THREADS;
         const int id = j < PF_ROUTE_IDS ? idr[j < PF_ROUTE_IDS ? j : 0] : p.ids[i];
-        int pp = -1;
         if (id >= 0 && id < E) {
             const int k = atomicAdd(&fill[id], 1);
-            pp = off[id] + k;
-            p.tile_tok[(toff[id] + k / PREFILL_TILE) * PREFILL_TILE + k % PREFILL_TILE] = i / K;
+            const int c = (toff[id] + k / PREFILL_TILE) * PREFILL_TILE + k % PREFILL_TILE;
+            p.tile_tok[c] = i / K;
+            p.tile_dst[c] = (i / K) * p.S + i % K;
         }
-        p.pos[(i / K) * p.S + (i % K)] = pp;
     }
     if (p.has_shared) {
-        for (int t = threadIdx.x; t < T; t += PF_ROUTE_THREADS) p.pos[t * p.S + K] = TK + t;
-        // column c of shared tile j is token 16 j + c
-        for (int t = threadIdx.x; t < T; t += PF_ROUTE_THREADS) p.tile_tok[t] = t;
+        // column c of shared tile j is token PREFILL_TILE j + c
+        for (int t = threadIdx.x; t < T; t += PF_ROUTE_THREADS) {
+            p.tile_tok[t] = t;
+            p.tile_dst[t] = t * p.S + K;
+        }
     }
 }
 
@@ -713,17 +723,18 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     const uint8_t* Ws = mat ? sh_up : sh_gate;
     const uint8_t* Wr = (mat ? up : gate) + (int64_t)max(e, 0) * (mat ? up_eb : gate_eb);
     const uint8_t* W0 = e < 0 ? Ws : Wr;
-    // the wave's token columns wv and wv + 8 (a column past cnt reads token 0's
-    // first words and stages nothing): their loads go out before the
-    // weight prefetch, so the staging below waits for them only
-    static_assert(PREFILL_TILE == 2 * PF_WAVES, "two token columns per wave");
-    const bool l0 = wv < cnt, l1 = wv + PF_WAVES < cnt;
+    // the wave's token column wv (and wv + 8 in 16-token tiles; a column past
+    // cnt reads token 0's first words and stages nothing): their loads go out
+    // before the weight prefetch, so the staging below waits for them only
+    constexpr bool TWO = PREFILL_TILE == 2 * PF_WAVES;
+    static_assert(PREFILL_TILE == PF_WAVES || TWO, "one or two token columns per wave");
+    const bool l0 = wv < cnt, l1 = TWO && wv + PF_WAVES < cnt;
     // (columns at or past cnt hold stale words: token 0 stands in)
     const int t0 = l0 ? __builtin_amdgcn_readlane(pt, wv) : 0;
-    const int t1 = l1 ? __builtin_amdgcn_readlane(pt, wv + PF_WAVES) : 0;
+    const int t1 = l1 ? __builtin_amdgcn_readlane(pt, (wv + PF_WAVES) & (PREFILL_TILE - 1)) : 0;
     PfPlanes<H, SPLIT> r0, r1;
     pf_planes_load<H, SPLIT>(xhi, xlo, xsum, xexp, t0, l0, r0);
-    pf_planes_load<H, SPLIT>(xhi, xlo, xsum, xexp, t1, l1, r1);
+    if constexpr (TWO) pf_planes_load<H, SPLIT>(xhi, xlo, xsum, xexp, t1, l1, r1);
     __builtin_amdgcn_sched_barrier(0);
 
     auto body = [&](auto tc) {
@@ -739,10 +750,10 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
         // the staging's branches, and hipcc would otherwise sink their loads there)
         __asm__ volatile("" ::: "memory");
         pf_planes_pin(r0);
-        pf_planes_pin(r1);
+        if constexpr (TWO) pf_planes_pin(r1);
         __builtin_amdgcn_sched_barrier(0);
         pf_planes_store(r0, wv, l0, xh, xl, xs, s_exp);
-        pf_planes_store(r1, wv + PF_WAVES, l1, xh, xl, xs, s_exp);
+        if constexpr (TWO) pf_planes_store(r1, wv + PF_WAVES, l1, xh, xl, xs, s_exp);
         __syncthreads();
 
         const int col = lane & 15;
@@ -778,7 +789,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
 // body, as in the gate/up kernel).
 template <int DT, int SDT, int NBI, int CPW>
 __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(const int* n_tiles, const int4* tiles,
-                                                                           const int* tile_tok, const void* act,
+                                                                           const int* tile_dst, const void* act,
                                                                            int max_tiles, int nch_log2, PrefillParams p) {
     constexpr int I = NBI * 256, KP = I + PF_PAD;
     __shared__ __attribute__((aligned(16))) _Float16 xh[PREFILL_TILE * KP];
@@ -787,6 +798,9 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(cons
     __shared__ int s_exp[PREFILL_TILE];
     int tile, chunk;
     pf_wg(nch_log2, tile, chunk);
+    // the output row of the lane's token column (stale past the tile's count,
+    // never used there), loaded with the tile's descriptor
+    const int dst = tile_dst[min(tile, max_tiles - 1) * PREFILL_TILE + (threadIdx.x & (PREFILL_TILE - 1))];
     int4 td;
     const bool live = pf_live_tile(n_tiles, tiles, max_tiles, tile, td);
     const uint8_t *down = p.down, *sh_down = p.sh_down;
@@ -821,7 +835,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(cons
         f32x4 acc[1] = {{0, 0, 0, 0}};
         g.template run<true>(xh, xl, xs, acc, [&](int c, f32x4 (&a)[1]) {
             if (col < cnt)
-                *(float4*)(p.ypair + (int64_t)(first + col) * p.hidden + rbase + PF_ROWS_DOWN * c + 4 * q) =
+                *(float4*)(p.ypair + (int64_t)dst * p.hidden + rbase + PF_ROWS_DOWN * c + 4 * q) =
                     make_float4(a[0][0] * sc, a[0][1] * sc, a[0][2] * sc, a[0][3] * sc);
             a[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         });
@@ -833,33 +847,33 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(cons
 
 // ------------------------------------------------------------ P3
 
-// Eight slots at a time: their pair indexes and weights (scalar loads), then
-// their eight expert outputs, then the sum in top-k order; the shared
-// expert's output is loaded with the first eight and added last.
+// Eight slots at a time: their expert ids and weights (scalar loads) and
+// their eight expert outputs (rows t S + s, written there by the down
+// kernel) together, then the sum in top-k order; the shared expert's output
+// (row t S + top_k) is loaded with the first eight and added last.
 constexpr int PF_COMBINE_SLOTS = 8;
 __global__ __launch_bounds__(256) void k_prefill_combine(PrefillParams p) {
     const int t = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
     if (h >= p.hidden) return;
-    const int* pos = p.pos + t * p.S;
+    const float* yt = p.ypair + (int64_t)t * p.S * p.hidden + h;
+    const int32_t* it = p.ids + t * p.top_k;
     const float* wt = p.weights + t * p.top_k;
-    const int psh = p.has_shared ? pos[p.top_k] : 0;
     const float ssh = p.has_shared ? p.sh_scale[t] : 0.0f;
-    const float ysh = p.ypair[(int64_t)psh * p.hidden + h];
+    const float ysh = p.has_shared ? yt[(int64_t)p.top_k * p.hidden] : 0.0f;
     float acc = 0.0f;
     for (int s0 = 0; s0 < p.top_k; s0 += PF_COMBINE_SLOTS) {
-        int pp[PF_COMBINE_SLOTS];
+        int id[PF_COMBINE_SLOTS];
         float w[PF_COMBINE_SLOTS], y[PF_COMBINE_SLOTS];
 #pragma unroll
         for (int j = 0; j < PF_COMBINE_SLOTS; ++j) {
             const int s = min(s0 + j, p.top_k - 1);
-            pp[j] = pos[s];
+            id[j] = it[s];
             w[j] = wt[s];
+            y[j] = yt[(int64_t)s * p.hidden];
         }
 #pragma unroll
-        for (int j = 0; j < PF_COMBINE_SLOTS; ++j) y[j] = p.ypair[(int64_t)max(pp[j], 0) * p.hidden + h];
-#pragma unroll
-        for (int j = 0; j < PF_COMBINE_SLOTS; ++j)   // (pp < 0: an expert id out of range, flagged by the route pass)
-            if (s0 + j < p.top_k && pp[j] >= 0) acc = __fadd_rn(acc, __fmul_rn(w[j], y[j]));
+        for (int j = 0; j < PF_COMBINE_SLOTS; ++j)   // (an expert id out of range: no row, flagged by the route pass)
+            if (s0 + j < p.top_k && id[j] >= 0 && id[j] < p.n_experts) acc = __fadd_rn(acc, __fmul_rn(w[j], y[j]));
     }
     if (p.has_shared) acc = __fadd_rn(acc, __fmul_rn(ssh, ysh));
     p.y[(int64_t)t * p.hidden + h] = acc;
@@ -898,8 +912,8 @@ PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden,
     L.tiles_off = align256(L.scale_off + (int64_t)n_tokens * 4);
     L.ntiles_off = align256(L.tiles_off + (int64_t)std::max(L.max_tiles, 1) * 16);
     L.tok_off = align256(L.ntiles_off + 4);
-    L.pos_off = align256(L.tok_off + (int64_t)std::max(L.max_tiles, 1) * PREFILL_TILE * 4);
-    L.act_off = align256(L.pos_off + P * 4);
+    L.dst_off = align256(L.tok_off + (int64_t)std::max(L.max_tiles, 1) * PREFILL_TILE * 4);
+    L.act_off = align256(L.dst_off + (int64_t)std::max(L.max_tiles, 1) * PREFILL_TILE * 4);
     L.ypair_off = align256(L.act_off + P * inter * 4);
     L.xhi_off = align256(L.ypair_off + P * hidden * 4);
     L.xlo_off = align256(L.xhi_off + (int64_t)n_tokens * hidden * 2);
@@ -914,10 +928,10 @@ PrefillLayout prefill_layout(int n_tokens, int top_k, int n_experts, int hidden,
     do {                                                                                                      \
         if (armed)                                                                                            \
             hipExtLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, e0, e1, 0, (const int*)p.n_tiles,   \
-                                  (const int4*)p.tiles, (const int*)p.tile_tok, (const void*)(src), p.max_tiles, __builtin_ctz(nch), p); \
+                                  (const int4*)p.tiles, (const int*)p.tile_dst, (const void*)(src), p.max_tiles, __builtin_ctz(nch), p); \
         else                                                                                                  \
             hipLaunchKernelGGL(kernel, grid, dim3(64 * PF_WAVES), 0, s, (const int*)p.n_tiles,                 \
-                               (const int4*)p.tiles, (const int*)p.tile_tok, (const void*)(src), p.max_tiles, __builtin_ctz(nch), p); \
+                               (const int4*)p.tiles, (const int*)p.tile_dst, (const void*)(src), p.max_tiles, __builtin_ctz(nch), p); \
     } while (0)
 
 // down row chunks per workgroup (CPW x 128 rows)

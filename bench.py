@@ -1192,6 +1192,16 @@ def main() -> int:
     kernels_us = {"k_fast_gate_up": round(kern["a_us"], 3), "k_fast_down": round(kern["b_us"], 3),
                   "launches_each": kern["launches"], "statistic": "median over launches",
                   "mean": {"k_fast_gate_up": round(kern["a_mean_us"], 3), "k_fast_down": round(kern["b_mean_us"], 3)}}
+    # each kernel against a plain streaming read of its own byte count
+    a_bytes = (K + 1) * (layers[0].expert_bytes("gate") + layers[0].expert_bytes("up"))
+    b_bytes = (K + 1) * layers[0].expert_bytes("down")
+    floors = {}
+    for kname, nb, kus in (("k_fast_gate_up", a_bytes, kern["a_us"]), ("k_fast_down", b_bytes, kern["b_us"])):
+        f_us = read_floor_us(nb)
+        floors[kname] = {"algorithmic_bytes": nb, "kernel_us": round(kus, 3), "read_floor_us": round(f_us, 3),
+                         "frac_of_read_floor": round(f_us / kus, 4)}
+    log("read floors: " + ", ".join(f"{k} {v['read_floor_us']:.3f} us ({v['frac_of_read_floor']:.2f})"
+                                    for k, v in floors.items()))
 
     result = {
         "metric": METRIC,
@@ -1217,6 +1227,7 @@ def main() -> int:
         "us_per_layer": round(ms_step * 1e3, 3),
         "parity_max_rel_err": float(f"{max(err, err_graph):.3e}"),
         "kernels_us": kernels_us,
+        "kernels_read_floor": floors,
         "roofline": roofline(kern, layers[0], floor=read_floor_us),
     }
     result["routed_decode"] = bench_routed_decode(runner, layers, X, ids, ws, 20, dev)

@@ -69,6 +69,18 @@ constexpr int PF_ROWS_DOWN = 128; // down rows per workgroup chunk: 8 waves x 16
 #ifndef PF_RING_SHARED
 #define PF_RING_SHARED 3
 #endif
+// In the down kernel a Q6_K shared expert beside routed experts of another
+// type takes a two-slot ring, and the kernel asks for six waves a SIMD (80
+// VGPRs, three workgroups a CU instead of two) when the intermediate size is
+// at most 512 and the routed type is a K-quant (a Q8_0 body would spill): the
+// Q3_K-routed down projections 47.4 -> 44.7 us at the 128-token prompt.  (A
+// two-slot ring for Q6_K throughout measured 65.3 -> 66.8 us.)
+#ifndef PF_RING_SHARED_DOWN
+#define PF_RING_SHARED_DOWN 2
+#endif
+#ifndef PF_MIXED_WAVES_DOWN
+#define PF_MIXED_WAVES_DOWN 6
+#endif
 constexpr int PF_PAD = 8;        // LDS row padding (halves)
 
 // Waves per SIMD that the LDS footprint of one workgroup (PF_WAVES waves)
@@ -362,7 +374,8 @@ struct PfRows {
     // R ring slots: block b lives in slot b % R; while block b is computed,
     // blocks b+1 .. b+R-1 are in flight (all of them for short rows)
     static constexpr bool UNROLLED = NBT <= RING;
-    static constexpr int R = UNROLLED ? NBT + 1 : RING;
+    static constexpr int R = UNROLLED && NBT + 1 < RING ? NBT + 1 : RING;
+    static_assert(R >= 2, "a ring of at least two slots");
     uint32_t raw[R][NMAT][NW];
     const uint8_t* W[NMAT];
     int64_t chunk_stride;
@@ -788,7 +801,8 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
 // SDT: the shared expert's down type (its tiles take that instance of the
 // body, as in the gate/up kernel).
 template <int DT, int SDT, int NBI, int CPW>
-__global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(const int* n_tiles, const int4* tiles,
+__global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN
+__attribute__((amdgpu_waves_per_eu(SDT != DT && DT != T_Q8_0 && NBI <= 2 ? PF_MIXED_WAVES_DOWN : 1))) void k_prefill_down(const int* n_tiles, const int4* tiles,
                                                                            const int* tile_dst, const void* act,
                                                                            int max_tiles, int nch_log2, PrefillParams p) {
     constexpr int I = NBI * 256, KP = I + PF_PAD;
@@ -815,7 +829,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_DOWN void k_prefill_down(cons
     auto body = [&](auto tc) {
         constexpr int T = decltype(tc)::value;
         const int64_t row_bytes = (int64_t)NBI * frag_unit_bytes<T>();
-        PfRows<T, 1, NBI, CPW, (SDT != DT && T == SDT) ? PF_RING_SHARED : PF_RING_DOWN> g;
+        PfRows<T, 1, NBI, CPW, (SDT != DT && T == SDT) ? PF_RING_SHARED_DOWN : PF_RING_DOWN> g;
         g.W[0] = W0 + (int64_t)(rbase + (lane & 15)) * row_bytes;
         g.chunk_stride = PF_ROWS_DOWN * row_bytes;
         g.q = q;

@@ -315,7 +315,6 @@ def kernel_times(runner, layers, X, IDS, WS, Y, reps: int, fp16_graph: int = 0) 
     b = [ms(ev[4 * i + 2], ev[4 * i + 3]) * 1e3 for i in range(n)]
     for h in ev:
         rt.hipEventDestroy(h)
-    # 1: one kernel did both halves (its duration is a_us, b_us is empty)
     return {"a_us": float(np.median(a)), "b_us": float(np.median(b)), "launches": n,
             "a_mean_us": float(np.mean(a)), "b_mean_us": float(np.mean(b)),
             "kernels": int(lib.mqh_last_decode_kernels())}

@@ -96,6 +96,19 @@ __host__ __device__ inline float f16_bits_to_f32(uint32_t h) {
 
 constexpr int LANES_PER_BLOCK = 4;
 
+// A block's scale word, read where a dot product needs it: on the device the
+// word passes through an empty asm statement, so the compiler cannot move its
+// conversion up to the load (with a wait for the load at that point).  Used
+// for Q3_K, where that happened; for the other types the plain read measured
+// the same or faster.
+__host__ __device__ inline uint32_t scale_word(const uint32_t* raw, int i) {
+    uint32_t w = raw[i];
+#if defined(__HIP_DEVICE_COMPILE__)
+    __asm__ volatile("" : "+v"(w));
+#endif
+    return w;
+}
+
 // NR runs of RL columns per lane; NRAW dwords of raw block bytes per lane.
 template <int T> struct LaneGeo;
 template <> struct LaneGeo<T_Q4_K> { static constexpr int NR = 2, RL = 32, NRAW = 12; };
@@ -169,7 +182,13 @@ __host__ __device__ inline void put2(uint32_t* w, const uint8_t* p) { __builtin_
 
 // Raw bytes lane k needs from the block (Q8_0: the 256-column unit) at blk,
 // into raw[0 .. NRAW).
-template <int T>
+// DW: Q6_K's d as the high half of the block's last dword (bytes 206..209,
+// read through scale_word), else as a 16-bit load.  The gate/up kernel takes
+// the dword form: with the 16-bit load, the shared expert's Q6_K instance held
+// its first barrier for its weight loads (FP16-graph layers with a Q6_K shared
+// expert 12.4-12.6 -> 11.7-11.9 us).  The down kernel keeps the 16-bit load
+// (9.52 against 9.57 us for the benchmark layer).
+template <int T, bool DW = false>
 __host__ __device__ inline void lane_load(const uint8_t* blk, int k, uint32_t* raw) {
     if constexpr (T == T_Q8_0) {
         const uint8_t* b = blk + 68 * k;         // blocks 2k, 2k+1: d0 qs0[32] d1 qs1[32]
@@ -195,17 +214,23 @@ __host__ __device__ inline void lane_load(const uint8_t* blk, int k, uint32_t* r
         put4(raw + 8, blk + 128 + 32 * h);               // qh
         put4(raw + 12, blk + 128 + 32 * h + 16);
         put2(raw + 16, blk + 192 + 8 * h);               // int8 scales 8h .. 8h+7
-        uint16_t d;
-        __builtin_memcpy(&d, blk + 208, 2);
-        raw[18] = d;
+        if constexpr (DW) {
+            __builtin_memcpy(raw + 18, blk + 206, 4);
+        } else {
+            uint16_t d;
+            __builtin_memcpy(&d, blk + 208, 2);
+            raw[18] = d;
+        }
     } else {  // Q3_K
         const int h = k >> 1, l0 = 16 * (k & 1);
         put4(raw, blk + l0);                     // hmask
         put4(raw + 4, blk + 32 + 32 * h + l0);   // qs
         __builtin_memcpy(raw + 8, blk + 96, 12); // scales
-        uint16_t d;
-        __builtin_memcpy(&d, blk + 108, 2);
-        raw[11] = d;
+        // d in the high half of the block's last dword (bytes 106..109): a
+        // 16-bit load's zero extension was placed, with a wait for the load,
+        // ahead of the kernel's first barrier, so that barrier waited for every
+        // weight load of the wave
+        __builtin_memcpy(raw + 11, blk + 106, 4);
     }
 }
 
@@ -267,7 +292,14 @@ __host__ __device__ inline int k3_scale_run(const uint32_t* sc, int sh, int s) {
 // ---------------------------------------------------------------- lane dots
 
 // Dot product of lane k's 64 weights (raw bytes from lane_load) with x.
-template <int T>
+// Q6_K's d from raw as lane_load<T_Q6_K, DW> left it
+template <bool DW>
+__host__ __device__ inline float q6_d(const uint32_t* raw) {
+    if constexpr (DW) return f16_bits_to_f32(scale_word(raw, 18) >> 16);
+    else return f16_bits_to_f32(raw[18] & 0xFFFFu);
+}
+
+template <int T, bool DW = false>
 __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const LaneX& x) {
     if constexpr (T == T_Q8_0) {
         // block 0: d at bytes 0-1, quants at bytes 2..33 (dwords shifted by two
@@ -285,7 +317,8 @@ __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const Lane
         return fmaf(d0, run0, d1 * run1);
     } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         constexpr int QS = T == T_Q4_K ? 4 : 12;
-        const float d = f16_bits_to_f32(raw[0] & 0xFFFFu), dmin = f16_bits_to_f32(raw[0] >> 16);
+        const uint32_t dw = raw[0];
+        const float d = f16_bits_to_f32(dw & 0xFFFFu), dmin = f16_bits_to_f32(dw >> 16);
         uint32_t sc2, mn2;
         k4_scale_min_pair(raw, k, sc2, mn2);
         float acc = 0.0f, off = 0.0f;
@@ -307,7 +340,7 @@ __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const Lane
         }
         return fmaf(d, acc, -dmin * off);
     } else if constexpr (T == T_Q6_K) {
-        const float d = f16_bits_to_f32(raw[18] & 0xFFFFu);
+        const float d = q6_d<DW>(raw);
         const int j = k & 1;
         float acc = 0.0f;
 #pragma unroll
@@ -331,7 +364,7 @@ __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const Lane
         }
         return d * acc;
     } else {  // Q3_K
-        const float d = f16_bits_to_f32(raw[11] & 0xFFFFu);
+        const float d = f16_bits_to_f32(scale_word(raw, 11) >> 16);
         const int h = k >> 1, odd = k & 1, sh = 8 * odd + 4 * h;
         float acc = 0.0f;
 #pragma unroll
@@ -453,7 +486,7 @@ __host__ __device__ inline void pack16_sbytes(const uint32_t* w, float s, uint32
 // Piece P (0..3, 16 weights) of lane k's 64 weights as FP16 pairs, in run
 // order: out[0..7] are the pairs 8P .. 8P+7 of lane_w16 (raw bytes from
 // lane_load).
-template <int T, int P>
+template <int T, int P, bool DW = false>
 __host__ __device__ inline void lane_w16_piece(const uint32_t* raw, int k, uint32_t* out) {
     if constexpr (T == T_Q8_0) {
         // pieces 0, 1: block 2k (d at bytes 0-1, quants at bytes 2..33); 2, 3: block 2k+1
@@ -470,7 +503,8 @@ __host__ __device__ inline void lane_w16_piece(const uint32_t* raw, int k, uint3
         }
     } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         constexpr int QS = T == T_Q4_K ? 4 : 12, r = P / 2, p = P % 2;
-        const float d = f16_bits_to_f32(raw[0] & 0xFFFFu), dmin = f16_bits_to_f32(raw[0] >> 16);
+        const uint32_t dw = raw[0];
+        const float d = f16_bits_to_f32(dw & 0xFFFFu), dmin = f16_bits_to_f32(dw >> 16);
         uint32_t sc2, mn2;
         k4_scale_min_pair(raw, k, sc2, mn2);
         const float d1 = detail::mul_rn(d, (float)((sc2 >> (8 * r)) & 0xFFu));
@@ -519,7 +553,7 @@ __host__ __device__ inline void lane_w16_piece(const uint32_t* raw, int k, uint3
         // top bit flipped), i.e. the int8 4 (u - 32); times RN(d sc) / 4 (exact)
         // that is RN(d sc (u - 32)), the reference decoder's product
         constexpr int r = P / 2, p = P % 2;
-        const float d = f16_bits_to_f32(raw[18] & 0xFFFFu);
+        const float d = q6_d<DW>(raw);
         const int s = (k & 1) + 2 * r, ra = (4 * r + 30) & 31, rb = (2 * s + 26) & 31;
         uint32_t w[4];
 #pragma unroll
@@ -532,7 +566,7 @@ __host__ __device__ inline void lane_w16_piece(const uint32_t* raw, int k, uint3
         // q - 4 = low2 - 4 (1 - hbit): the two low bits rotated to bits 5..6 and
         // the inverted mask bit to bit 7 make the int8 32 (q - 4); times
         // RN(d sc) / 32 (exact) that is RN(d sc (q - 4))
-        const float d = f16_bits_to_f32(raw[11] & 0xFFFFu);
+        const float d = f16_bits_to_f32(scale_word(raw, 11) >> 16);
         const int h = k >> 1, odd = k & 1, sh = 8 * odd + 4 * h;
         const int ra = (2 * P + 27) & 31, rb = (4 * h + P + 25) & 31;
         uint32_t w[4];
@@ -543,19 +577,19 @@ __host__ __device__ inline void lane_w16_piece(const uint32_t* raw, int k, uint3
 }
 
 // Lane k's 64 weights as FP16 pairs in run order.
-template <int T>
+template <int T, bool DW = false>
 __host__ __device__ inline void lane_w16(const uint32_t* raw, int k, uint32_t (&w)[32]) {
-    lane_w16_piece<T, 0>(raw, k, w);
-    lane_w16_piece<T, 1>(raw, k, w + 8);
-    lane_w16_piece<T, 2>(raw, k, w + 16);
-    lane_w16_piece<T, 3>(raw, k, w + 24);
+    lane_w16_piece<T, 0, DW>(raw, k, w);
+    lane_w16_piece<T, 1, DW>(raw, k, w + 8);
+    lane_w16_piece<T, 2, DW>(raw, k, w + 16);
+    lane_w16_piece<T, 3, DW>(raw, k, w + 24);
 }
 
 namespace detail {
-template <int T, int P>
+template <int T, int P, bool DW>
 __host__ __device__ inline float dot16_piece(const uint32_t* raw, int k, const LaneH& x, float acc) {
     uint32_t w[8];
-    lane_w16_piece<T, P>(raw, k, w);
+    lane_w16_piece<T, P, DW>(raw, k, w);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -574,12 +608,12 @@ __host__ __device__ inline float dot16_piece(const uint32_t* raw, int k, const L
 // FP16-graph dot product of lane k's 64 weights with x: FP16 products summed
 // in FP32, two columns per v_dot2_f32_f16 (the host build sums the exact
 // products in FP32 in the same order), decoded one 16-weight piece at a time.
-template <int T>
+template <int T, bool DW = false>
 __host__ __device__ inline float lane_dot_f16(const uint32_t* raw, int k, const LaneH& x) {
-    float acc = detail::dot16_piece<T, 0>(raw, k, x, 0.0f);
-    acc = detail::dot16_piece<T, 1>(raw, k, x, acc);
-    acc = detail::dot16_piece<T, 2>(raw, k, x, acc);
-    return detail::dot16_piece<T, 3>(raw, k, x, acc);
+    float acc = detail::dot16_piece<T, 0, DW>(raw, k, x, 0.0f);
+    acc = detail::dot16_piece<T, 1, DW>(raw, k, x, acc);
+    acc = detail::dot16_piece<T, 2, DW>(raw, k, x, acc);
+    return detail::dot16_piece<T, 3, DW>(raw, k, x, acc);
 }
 
 }  // namespace mqh

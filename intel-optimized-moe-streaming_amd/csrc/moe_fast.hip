@@ -279,8 +279,8 @@ __device__ __forceinline__ void item_loads(const uint8_t* Gm, const uint8_t* Um,
                                            uint32_t* rg, uint32_t* ru) {
     constexpr int64_t ROW_BYTES = (int64_t)(H / 256) * unit_bytes(T);
     const int64_t off = (int64_t)row * ROW_BYTES + blk * unit_bytes(T);
-    lane_load<T>(Gm + off, k, rg);
-    lane_load<T>(Um + off, k, ru);
+    lane_load<T, true>(Gm + off, k, rg);
+    lane_load<T, true>(Um + off, k, ru);
 }
 
 // SGT: the shared expert's gate/up type (its waves take that code path).
@@ -445,8 +445,8 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
             __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
             // 3. gate and up dot products
-            g[0] = lane_dot_f16<GT>(rg[0], k, XH);
-            u[0] = lane_dot_f16<GT>(ru[0], k, XH);
+            g[0] = lane_dot_f16<GT, true>(rg[0], k, XH);
+            u[0] = lane_dot_f16<GT, true>(ru[0], k, XH);
         }
     } else {
         DigitsRef xd;
@@ -460,11 +460,11 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
 #pragma unroll
         for (int i = 0; i < IPW; ++i) {
             if (sw) {
-                g[i] = lane_dot<SGT>(rg[i], k, X);
-                u[i] = lane_dot<SGT>(ru[i], k, X);
+                g[i] = lane_dot<SGT, true>(rg[i], k, X);
+                u[i] = lane_dot<SGT, true>(ru[i], k, X);
             } else {
-                g[i] = lane_dot<GT>(rg[i], k, X);
-                u[i] = lane_dot<GT>(ru[i], k, X);
+                g[i] = lane_dot<GT, true>(rg[i], k, X);
+                u[i] = lane_dot<GT, true>(ru[i], k, X);
             }
         }
     }
@@ -513,13 +513,45 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     }
 }
 
+// Whether the calling wave's item is the shared expert's: the item and slot
+// as gate_up_items computes them (wave-uniform).
+template <int LPR, bool ROUTED, int IPW>
+__device__ __forceinline__ bool wave_is_shared(const DecodeHot& h) {
+    constexpr int RPI = 64 / LPR;
+    const int xg = (int)blockIdx.y * 8 + (int)blockIdx.x, wave = threadIdx.x >> 6;
+    const int per_slot = h.a_inter / RPI;
+    const bool by_slot = !ROUTED && IPW == 1 && h.a_waves == h.S;
+    const int item = uniform(by_slot ? wave * per_slot + xg : (xg * h.a_waves + wave) * IPW);
+    return (h.has_shared != 0) & (item < h.S * per_slot) & ((item >> __builtin_ctz(per_slot)) == h.top_k);
+}
+
+// A shared expert of another type than the routed ones: the shared expert's
+// waves run their own instance of the item code, chosen once at the start by a
+// scalar branch.  With both types in one body, the weight loads of the two
+// types sat in two branches whose join made the wait-count pass hold the
+// shared expert's header loads for the token's load, and the compiler
+// converted the Q6_K scale right after its load (a round trip ahead of the
+// main weight loads): Q3_K beside a Q6_K shared expert took 11.0 us for this
+// kernel against 6.2 us with a Q3_K shared expert.  Each wave executes the
+// same barriers whichever instance it runs.
+template <int GT, int SGT, int LPR, bool ROUTED, bool F16G, int IPW>
+__device__ __forceinline__ void gate_up_waves(const DecodeHot& h, const DecodeParams& p, SharedX<64 * LPR, F16G>& sh) {
+    if constexpr (SGT != GT) {
+        if (wave_is_shared<LPR, ROUTED, IPW>(h)) {
+            gate_up_items<SGT, SGT, LPR, ROUTED, F16G, IPW>(h, p, sh);
+            return;
+        }
+    }
+    gate_up_items<GT, GT, LPR, ROUTED, F16G, IPW>(h, p, sh);
+}
+
 template <int GT, int SGT, int LPR, bool F16G, int IPW = 1>
 __global__ __launch_bounds__(1024) void k_fast_gate_up(const float* x, const int32_t* ids, float* act, const float* sh_gate_inp, int top_k,
                                                   int S, int has_shared, int n_experts, int a_inter, int a_waves,
                                                   DecodeParams p) {
     __shared__ SharedX<64 * LPR, F16G> sh;
     const DecodeHot h{x, ids, act, nullptr, sh_gate_inp, top_k, S, has_shared, n_experts, a_inter, a_waves};
-    gate_up_items<GT, SGT, LPR, false, F16G, IPW>(h, p, sh);
+    gate_up_waves<GT, SGT, LPR, false, F16G, IPW>(h, p, sh);
 }
 
 // Kernel A with the router's select step in its prologue: the same work as
@@ -530,7 +562,7 @@ __global__ __launch_bounds__(1024) void k_fast_gate_up_routed(const float* x, co
                                                   DecodeParams p) {
     __shared__ SharedX<64 * LPR, F16G> sh;
     const DecodeHot h{x, ids, act, nullptr, sh_gate_inp, top_k, S, has_shared, n_experts, a_inter, a_waves};
-    gate_up_items<GT, SGT, LPR, true, F16G>(h, p, sh);
+    gate_up_waves<GT, SGT, LPR, true, F16G, 1>(h, p, sh);
 }
 
 // ---------------------------------------------------------------- kernel B

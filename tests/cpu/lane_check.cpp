@@ -42,19 +42,23 @@ struct HostDigits {
     }
 };
 
+// (both forms of the loaded scale words, lane_load<T, DW>, must give the same
+// bits; a difference returns NaN)
 template <int T>
 static float row_dot(const uint8_t* row, int ncols, const HostDigits& hd) {
-    float acc = 0.0f;
+    float acc = 0.0f, acc_dw = 0.0f;
     for (int b = 0; b < ncols / 256; ++b) {
         for (int k = 0; k < LANES_PER_BLOCK; ++k) {
-            uint32_t raw[LaneGeo<T>::NRAW];
+            uint32_t raw[LaneGeo<T>::NRAW], raw_dw[LaneGeo<T>::NRAW];
             LaneX x;
             lane_x<T>(hd.ref(), b, k, x);
             lane_load<T>(row + (int64_t)b * unit_bytes(T), k, raw);
+            lane_load<T, true>(row + (int64_t)b * unit_bytes(T), k, raw_dw);
             acc += lane_dot<T>(raw, k, x);
+            acc_dw += lane_dot<T, true>(raw_dw, k, x);
         }
     }
-    return acc;
+    return __builtin_memcmp(&acc, &acc_dw, 4) == 0 ? acc : __builtin_nanf("");
 }
 
 extern "C" float mqh_cpu_row_dot(int type, const uint8_t* row, int ncols, const float* x) {
@@ -101,10 +105,13 @@ extern "C" void mqh_cpu_lane_cover(int type, int* count) {
 template <int T>
 static void w16_unit(const uint8_t* unit, uint16_t* bits, int* cols) {
     for (int k = 0; k < LANES_PER_BLOCK; ++k) {
-        uint32_t raw[LaneGeo<T>::NRAW];
-        uint32_t w[32];
+        uint32_t raw[LaneGeo<T>::NRAW], raw_dw[LaneGeo<T>::NRAW];
+        uint32_t w[32], w_dw[32];
         lane_load<T>(unit, k, raw);
         lane_w16<T>(raw, k, w);
+        lane_load<T, true>(unit, k, raw_dw);
+        lane_w16<T, true>(raw_dw, k, w_dw);
+        if (__builtin_memcmp(w, w_dw, sizeof(w)) != 0) w[0] = 0xFFFFFFFFu;   // (flagged by the caller's check)
         for (int i = 0; i < 64; ++i) {
             const int r = i / LaneGeo<T>::RL;
             bits[64 * k + i] = (uint16_t)(w[i / 2] >> (16 * (i & 1)));

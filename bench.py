@@ -884,6 +884,72 @@ def bench_fp16_graph_decode(dev, n_layers: int, reps: int, cpu_seconds: float) -
     return out
 
 
+# The reference model's expert type mixes (every layer has a Q6_K shared
+# expert): routed Q3_K throughout in layers 5-34, Q4_K gate/up with Q6_K down in
+# layers 1-4 and 35-39, Q4_K gate/up with Q8_0 down in layer 0.
+REF_MIXES = (("layers 5-34", {"gate": 11, "up": 11, "down": 11}),
+             ("layers 1-4, 35-39", {"gate": 12, "up": 12, "down": 14}),
+             ("layer 0", {"gate": 12, "up": 12, "down": 8}))
+Q6_SHARED = {"gate": 14, "up": 14, "down": 14}
+
+
+def bench_decode_mixes(dev, n_layers: int, reps: int) -> dict:
+    """The decode step (one token, top-8 + the Q6_K shared expert, hidden 2048,
+    256 experts x intermediate 512) in the reference model's type mixes, in both
+    graphs: n_layers resident layers rotated in one graph, as the headline.
+    The FP16 graph uses the reference's FP16-graph check scales (super-block
+    scales |N| * 0.002, x ~ N(0,1) * 0.05).  Parity on layer 0 of each against
+    the oracle's experts, combine and FP32-graph shared expert."""
+    import torch
+
+    import oracle
+    from flash_moe_hip.layer_store import ExpertLayer
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    runner = MoeRunner(dev)
+    out = {"workload": f"decode MoE layer, 1 token, top-8 + Q6_K shared expert, hidden {H}, {E} experts x "
+                       f"intermediate {I}, the reference model's type mixes; {n_layers} resident layers rotated",
+           "metric": "us per layer step", "unit": "us", "higher_is_better": False, "mixes": {}}
+    for name, types in REF_MIXES:
+        row = {}
+        for fp16 in (0, 1):
+            kw = {"scale": 0.002} if fp16 else {}
+            layers = [ExpertLayer.synthetic(types, E, H, I, seed=1000 * l + 7, shared_types=Q6_SHARED,
+                                            shared_intermediate=I, gate_inp=True, device=dev, **kw)
+                      for l in range(n_layers)]
+            xs, ids, ws = route_layers(n_layers, seed=31, layers=layers)
+            if fp16:
+                xs = (xs * 0.05).astype(np.float32)
+            X, IDS, WS = (torch.from_numpy(a).to(dev) for a in (xs, ids, ws))
+            Y = torch.empty((n_layers, H), dtype=torch.float32, device=dev)
+
+            def sweep(n=n_layers):
+                for l in range(n):
+                    runner.decode(layers[l], X[l:l + 1], IDS[l:l + 1], WS[l:l + 1], y=Y[l:l + 1], fp16_graph=fp16)
+
+            sweep()
+            torch.cuda.synchronize()
+            assert runner.status() == 0
+            L0 = layers[0]
+            outs = [oracle.expert_forward(L0.host_expert(int(e)), types, xs[0], H, I, fp16) for e in ids[0]]
+            gate = oracle._sigmoid(np.float32(xs[0] @ L0.shared.gate_inp.cpu().numpy()).reshape(()))
+            sh = (gate * oracle.expert_forward(L0.host_shared(), Q6_SHARED, xs[0], H, I, 0)).astype(np.float32)
+            err = oracle.max_relative_error(Y[0].cpu().numpy(), oracle.combine(outs, [float(v) for v in ws[0]], sh))
+            ms = _time(_graph(sweep, dev), reps) / n_layers
+            kern = kernel_times(runner, layers, X, IDS, WS, Y, reps=4, fp16_graph=fp16)
+            nbytes = K * L0.bytes_per_expert() + L0.shared_bytes()
+            row["fp16_graph" if fp16 else "fp32_graph"] = {
+                "us_per_layer": round(ms * 1e3, 3), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "kernels_us": {"A": round(kern["a_us"], 3), "B": round(kern["b_us"], 3)},
+                "parity_max_rel_err": float(f"{err:.3e}")}
+            log(f"decode, {name} ({'FP16' if fp16 else 'FP32'} graph): {ms * 1e3:.2f} us/layer, parity {err:.2e}; "
+                f"kernels {kern['a_us']:.2f} / {kern['b_us']:.2f} us")
+            del layers
+            torch.cuda.empty_cache()
+        out["mixes"][name] = {"types": types, "shared_types": Q6_SHARED, **row}
+    return out
+
+
 def bench_single_expert(dev, reps: int, cpu_seconds: float) -> dict:
     """One Q4_K expert (gate/up [512x2048], down [2048x512]), one token, x ~ N(0,1),
     seed 0 (the reference's single-expert decode): 40 such experts resident and
@@ -1108,8 +1174,8 @@ def main() -> int:
     ap.add_argument("--only-decode", action="store_true", help="skip the batched-decode, prefill and dequant lines")
     # single_expert (one Q4_K expert, one token) runs the headline's gate/up kernel
     # instance: a profile of the headline kernels leaves it out (--workloads)
-    ap.add_argument("--workloads", default="single_expert,fp16_graph_decode,batched_decode,prefill,"
-                                           "prefill_q3k_q6k_shared,dequant,deltanet,reference_callers",
+    ap.add_argument("--workloads", default="single_expert,fp16_graph_decode,decode_reference_mixes,batched_decode,"
+                                           "prefill,prefill_q3k_q6k_shared,dequant,deltanet,reference_callers",
                     help="comma-separated workloads run after the headline decode")
     ap.add_argument("--extra-cpu-seconds", type=float, default=4.0)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
@@ -1241,6 +1307,7 @@ def main() -> int:
         runs = {
             "single_expert": lambda: bench_single_expert(dev, 50, cpu_s),
             "fp16_graph_decode": lambda: bench_fp16_graph_decode(dev, args.layers, 20, cpu_s),
+            "decode_reference_mixes": lambda: bench_decode_mixes(dev, args.layers, 20),
             "batched_decode": lambda: bench_batched_decode(dev, args.layers, 25 * args.layers, cpu_s),
             "prefill": lambda: bench_prefill(dev, 8, 20, cpu_s),
             # the reference model's layers 5-34 (docs/PHASE0_FINDINGS.md:60-69)

@@ -271,7 +271,35 @@ struct SharedX {
     float sum16[H / RUN];
     float s_gate[16];
     __attribute__((aligned(16))) uint16_t x16[F16G ? H : 8];   // the FP16 graph's token (FP16 bits)
+    float half_dot[2][64 / (H / 64)];   // a split shared item: its gate and up row dots
+    int half_done;                      // and how many of its two waves have written theirs
 };
+
+// The shared expert's scale: sigmoid(x . g_inp) (shared_expert.py:221-251)
+// or 1, once per token, by every wave of the token's last workgroup
+// (scale_wg); the first NX threads hold 4 products each.
+template <int NX, int H, bool F16G>
+__device__ __forceinline__ void shared_scale(const DecodeParams& p, SharedX<H, F16G>& sh, bool scale_wg, bool gate_wg,
+                                             float4 xv, float4 gi) {
+    if (!scale_wg) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (gate_wg && wave < NX / 64) {
+        float acc = fmaf(xv.x, gi.x, xv.y * gi.y) + fmaf(xv.z, gi.z, xv.w * gi.w);
+        acc = lane_group_sum<64>(acc);
+        if (lane == 0) sh.s_gate[wave] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float scale = 1.0f;
+        if (gate_wg) {
+            float dsum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NX / 64; ++w) dsum += sh.s_gate[w];
+            scale = sigmoid_stable(dsum);
+        }
+        p.sh_scale[blockIdx.z] = scale;
+    }
+}
 
 // every weight load of one item's lane (type T)
 template <int T, int H>
@@ -287,8 +315,10 @@ __device__ __forceinline__ void item_loads(const uint8_t* Gm, const uint8_t* Um,
 // ROUTED: the router's select step first (p.route_scores set, at most
 // ROUTE_PROLOGUE_MAX_EXPERTS experts).  IPW: consecutive items per wave (the
 // same slot: items per slot are a multiple of it), loaded together and
-// sharing the wave's token operand.
-template <int GT, int SGT, int LPR, bool ROUTED, bool F16G, int IPW = 1>
+// sharing the wave's token operand.  SPLIT: the routed waves of a workgroup of
+// top_k + 2 waves whose last two split the shared expert's item
+// (gate_up_shared_half); the routed waves are dealt by slot.
+template <int GT, int SGT, int LPR, bool ROUTED, bool F16G, int IPW = 1, bool SPLIT = false>
 __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodeParams& p, SharedX<64 * LPR, F16G>& sh) {
     constexpr int H = 64 * LPR, RPI = 64 / LPR, NX = H / 4;   // NX threads hold the token, four values each
     constexpr int NA = LaneGeo<GT>::NRAW > LaneGeo<SGT>::NRAW ? LaneGeo<GT>::NRAW : LaneGeo<SGT>::NRAW;
@@ -304,7 +334,8 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     // vector load and a full wait); items per slot are a power of two
     const int per_slot = h.a_inter / RPI;
     const int n_items = h.S * per_slot, wg_items = h.a_waves * IPW;
-    if (xg * wg_items >= n_items) return;   // padding of the last group of eight (no division on this path)
+    // padding of the last group of eight (no division on this path)
+    if (SPLIT ? xg >= per_slot : xg * wg_items >= n_items) return;
     // Items are dealt in order (a workgroup's waves take consecutive items,
     // mostly of one slot), or, with one wave per slot and one item a wave
     // (then per_slot workgroups), by slot: wave s takes slot s's row group xg.
@@ -313,14 +344,15 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     // the FP16 graph runs the cheaper integer-digit path.  (The routed
     // prologue needs consecutive slots per workgroup: it ranks only as many
     // experts as its workgroup uses.)
-    const bool by_slot = !ROUTED && IPW == 1 && h.a_waves == h.S;
+    const bool by_slot = SPLIT || (!ROUTED && IPW == 1 && h.a_waves == h.S);
     const int item = uniform(by_slot ? wave * per_slot + xg : (xg * h.a_waves + wave) * IPW);
     const bool live = item < h.S * per_slot;
     const int s = live ? item >> __builtin_ctz(per_slot) : 0;
     const int row0 = live ? (item & (per_slot - 1)) * RPI : 0;
     // (bitwise: a short-circuit would branch on its first kernel argument)
     const bool shared = live & (h.has_shared != 0) & (s == h.top_k);
-    const bool scale_wg = (h.has_shared != 0) & ((xg + 1) * wg_items >= n_items);   // the token's last workgroup
+    // the token's last workgroup
+    const bool scale_wg = (h.has_shared != 0) & (SPLIT ? xg + 1 >= per_slot : (xg + 1) * wg_items >= n_items);
     const bool gate_wg = scale_wg & (h.sh_gate_inp != nullptr);
 
     // 1. the token's values and the expert id, together and before any branch
@@ -491,30 +523,70 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
         if (bad && lane == 0 && row0 == 0) atomicOr(&p.flags[FLAG_BAD_ID], 1);
     }
 
-    // the shared expert's scale: sigmoid(x . g_inp) (shared_expert.py:221-251)
-    // or 1, once per token; the first NX threads hold 4 products each
-    if (scale_wg) {
-        if (gate_wg && wave < NX / 64) {
-            float acc = fmaf(xv.x, gi.x, xv.y * gi.y) + fmaf(xv.z, gi.z, xv.w * gi.w);
-            acc = lane_group_sum<64>(acc);
-            if (lane == 0) sh.s_gate[wave] = acc;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            float scale = 1.0f;
-            if (gate_wg) {
-                float dsum = 0.0f;
-#pragma unroll
-                for (int w = 0; w < NX / 64; ++w) dsum += sh.s_gate[w];
-                scale = sigmoid_stable(dsum);
-            }
-            p.sh_scale[t] = scale;
-        }
-    }
+    shared_scale<NX>(p, sh, scale_wg, gate_wg, xv, gi);
 }
 
 // Whether the calling wave's item is the shared expert's: the item and slot
 // as gate_up_items computes them (wave-uniform).
+// The shared expert's item split over two waves, one token, one row group xg
+// a workgroup beside the top_k routed waves of that row group (SPLIT): wave
+// top_k takes the gate rows, wave top_k + 1 the same up rows, each loading and
+// dotting one matrix, so neither is the workgroup's longest wave.  Each hands
+// its row dots to the other through LDS; the second to finish (an LDS counter
+// decides, no barrier) applies SwiGLU.  The shared expert runs the FP32 graph
+// in either graph, as in the whole-item path.
+template <int T, int LPR, bool F16G>
+__device__ __forceinline__ void gate_up_shared_half(const DecodeHot& h, const DecodeParams& p,
+                                                    SharedX<64 * LPR, F16G>& sh) {
+    constexpr int H = 64 * LPR, RPI = 64 / LPR, NX = H / 4;
+    const int t = blockIdx.z, xg = (int)blockIdx.y * 8 + (int)blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int per_slot = h.a_inter / RPI;
+    if (xg >= per_slot) return;
+    const bool upw = uniform(wave) != h.top_k;
+    const bool scale_wg = xg + 1 >= per_slot;
+    const bool gate_wg = scale_wg & (h.sh_gate_inp != nullptr);
+    const float* xt = h.x + (int64_t)t * H;
+    const int xi = min((int)threadIdx.x, NX - 1) * 4;
+    const float4 xv = *(const float4*)(xt + xi);
+    const float4 gi = *(const float4*)((gate_wg ? h.sh_gate_inp : xt) + xi);
+    const uint8_t* M = upw ? p.sh_up : p.sh_gate;
+    __asm__ volatile("" ::"s"(M));
+    __builtin_amdgcn_sched_barrier(0);
+    const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
+    const int row = xg * RPI + rr;
+    constexpr int64_t ROW_BYTES = (int64_t)(H / 256) * unit_bytes(T);
+    uint32_t rw[LaneGeo<T>::NRAW];
+    lane_load<T, true>(M + (int64_t)row * ROW_BYTES + blk * unit_bytes(T), k, rw);
+    __builtin_amdgcn_sched_barrier(0);
+    if (threadIdx.x < NX) {
+        x_digits<H, NX>(xv, sh.planes, sh.xs16, sh.sum16);
+        if constexpr (F16G)
+            *(uint2*)(sh.x16 + 4 * threadIdx.x) = make_uint2(pack_rn16(xv.x, xv.y), pack_rn16(xv.z, xv.w));
+    }
+    if (!upw && lane == 0) sh.half_done = 0;   // (read only after the barrier)
+    __syncthreads();
+    DigitsRef xd;
+    xd.planes = sh.planes; xd.xs16 = sh.xs16; xd.sum16 = sh.sum16; xd.n = H;
+    LaneX X;
+    lane_x<T>(xd, blk, k, X);
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const float v = lane_group_sum<LPR>(lane_dot<T, true>(rw, k, X));
+    if (li == 0) sh.half_dot[upw][rr] = v;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    int before = 0;
+    if (lane == 0) before = __hip_atomic_fetch_add(&sh.half_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (uniform(before) == 1) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        if (li == 0) {
+            const float o = sh.half_dot[!upw][rr];
+            h.act[((int64_t)t * h.S + h.top_k) * h.a_inter + row] = upw ? silu_mul(o, v) : silu_mul(v, o);
+        }
+    }
+    shared_scale<NX>(p, sh, scale_wg, gate_wg, xv, gi);
+}
+
 template <int LPR, bool ROUTED, int IPW>
 __device__ __forceinline__ bool wave_is_shared(const DecodeHot& h) {
     constexpr int RPI = 64 / LPR;
@@ -534,8 +606,14 @@ __device__ __forceinline__ bool wave_is_shared(const DecodeHot& h) {
 // main weight loads): Q3_K beside a Q6_K shared expert took 11.0 us for this
 // kernel against 6.2 us with a Q3_K shared expert.  Each wave executes the
 // same barriers whichever instance it runs.
-template <int GT, int SGT, int LPR, bool ROUTED, bool F16G, int IPW>
+template <int GT, int SGT, int LPR, bool ROUTED, bool F16G, int IPW, bool SPLIT = false>
 __device__ __forceinline__ void gate_up_waves(const DecodeHot& h, const DecodeParams& p, SharedX<64 * LPR, F16G>& sh) {
+    if constexpr (SPLIT) {
+        static_assert(!ROUTED && IPW == 1, "the split shared item is dealt by slot");
+        if (uniform(threadIdx.x >> 6) >= h.top_k) gate_up_shared_half<SGT, LPR, F16G>(h, p, sh);
+        else gate_up_items<GT, GT, LPR, false, F16G, 1, true>(h, p, sh);
+        return;
+    }
     if constexpr (SGT != GT) {
         if (wave_is_shared<LPR, ROUTED, IPW>(h)) {
             gate_up_items<SGT, SGT, LPR, ROUTED, F16G, IPW>(h, p, sh);
@@ -545,13 +623,13 @@ __device__ __forceinline__ void gate_up_waves(const DecodeHot& h, const DecodePa
     gate_up_items<GT, GT, LPR, ROUTED, F16G, IPW>(h, p, sh);
 }
 
-template <int GT, int SGT, int LPR, bool F16G, int IPW = 1>
+template <int GT, int SGT, int LPR, bool F16G, int IPW = 1, bool SPLIT = false>
 __global__ __launch_bounds__(1024) void k_fast_gate_up(const float* x, const int32_t* ids, float* act, const float* sh_gate_inp, int top_k,
                                                   int S, int has_shared, int n_experts, int a_inter, int a_waves,
                                                   DecodeParams p) {
     __shared__ SharedX<64 * LPR, F16G> sh;
     const DecodeHot h{x, ids, act, nullptr, sh_gate_inp, top_k, S, has_shared, n_experts, a_inter, a_waves};
-    gate_up_waves<GT, SGT, LPR, false, F16G, IPW>(h, p, sh);
+    gate_up_waves<GT, SGT, LPR, false, F16G, IPW, SPLIT>(h, p, sh);
 }
 
 // Kernel A with the router's select step in its prologue: the same work as
@@ -832,6 +910,10 @@ static dim3 fast_grid(int n, int tokens) {
     return tokens == 1 ? dim3(8, (n + 7) / 8, 1) : dim3(n, 1, tokens);
 }
 
+#ifndef FAST_A_SPLIT_SHARED
+#define FAST_A_SPLIT_SHARED 1   // one token, one wave a slot: two waves for the shared expert's item
+#endif
+
 #ifndef FAST_A_PAIR_TOKENS
 #define FAST_A_PAIR_TOKENS 4   // tokens from which kernel A gives each wave two items
 #endif
@@ -864,6 +946,18 @@ static void launch_a(const DecodeParams& p, hipStream_t stream, const KernelEven
     }
     const int items = p.S * (p.inter / (64 / LPR));
     const int w = gate_up_waves(items, p.n_tokens, 64 * LPR, device_cus());
+    if (FAST_A_SPLIT_SHARED && p.route_scores == nullptr && p.n_tokens == 1 && p.has_shared && p.top_k > 0 &&
+        w == p.S && p.S + 1 <= 16) {
+        // one wave a slot (dealt by slot): the shared expert's item goes to two
+        // waves, gate and up
+        const int per_slot = p.inter / (64 / LPR);
+        const dim3 grid = fast_grid(per_slot, 1), block(64 * (p.S + 1));
+        if (ev.armed_a())
+            hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, 1, true>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, p.S + 1, p);
+        else
+            hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, 1, true>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, p.S + 1, p);
+        return;
+    }
     const dim3 grid = fast_grid((items + w - 1) / w, p.n_tokens), block(64 * w);
     if (p.route_scores != nullptr) {
         if (ev.armed_a())

@@ -532,6 +532,43 @@ def test_batched_uniform_types(hip, oracle_mod, gt):
 
 
 @pytest.mark.parametrize("fp16", [0, 1])
+@pytest.mark.parametrize("routed,shared_t", [((12, 14), (12, 14)), ((12, 14), (14, 14)), ((11, 11), (14, 14)),
+                                              ((12, 8), (14, 14))])
+def test_one_token_shared_item_on_two_waves(hip, oracle_mod, routed, shared_t, fp16):
+    """One token at hidden 2048 / intermediate 512 with top-8 + shared: kernel A
+    deals one wave a slot and gives the shared expert's item to two waves (gate
+    rows, up rows) whose second to finish applies SwiGLU.  The headline types
+    and the reference model's three mixes with a Q6_K shared expert, both
+    graphs, against the oracle and the generic kernels; a second call checks
+    that the hand-over counter starts from zero in every launch."""
+    gu, dn = routed
+    t = {"gate": gu, "up": gu, "down": dn}
+    sh = {"gate": shared_t[0], "up": shared_t[0], "down": shared_t[1]}
+    H, I, E, K = 2048, 512, 24, 8
+    layer, host, shared = make_layer(500 + gu + dn + 3 * shared_t[0] + fp16, E, H, I, t, shared_types=sh,
+                                     scale=0.002 if fp16 else 0.01)
+    rng = np.random.default_rng(gu + 5 * dn + shared_t[0] + fp16)
+    for call in range(2):
+        X = (rng.standard_normal((1, H)) * (0.05 if fp16 else 1.0)).astype(np.float32)
+        ids = rng.permutation(E)[:K][None]
+        ws = rng.dirichlet(np.ones(K), size=1).astype(np.float32)
+        print(f"one token, routed={routed} shared={shared_t} fp16={fp16} call={call}", flush=True)
+        old = hip.mqh_set_decode_path(0)
+        try:
+            got, s0 = run(layer, X, ids, ws, fp16=fp16)
+            assert hip.mqh_last_decode_path() == 0
+            expect_kernels(hip)
+            hip.mqh_set_decode_path(1)
+            gen, s1 = run(layer, X, ids, ws, fp16=fp16)
+        finally:
+            hip.mqh_set_decode_path(old)
+        assert s0 == 0 and s1 == 0
+        want = oracle_layer(oracle_mod, layer, host, shared, X[0], ids[0].tolist(), ws[0].tolist(), fp16=fp16)
+        assert oracle_mod.max_relative_error(got[0], want) <= TOL, (routed, shared_t, fp16, call)
+        assert oracle_mod.max_relative_error(got[0], gen[0]) <= TOL, (routed, shared_t, fp16, call)
+
+
+@pytest.mark.parametrize("fp16", [0, 1])
 @pytest.mark.parametrize("routed", [(12, 12), (11, 11), (12, 14), (8, 8)])
 def test_intermediate_2048_twelve_slots(hip, oracle_mod, routed, fp16):
     """Intermediate 2048 with the most slots kernel B's digit LDS admits there:

@@ -197,7 +197,7 @@ def roofline(kern: dict, layer, floor=None) -> dict:
     a_bytes = (K + 1) * (layer.expert_bytes("gate") + layer.expert_bytes("up"))
     b_bytes = (K + 1) * layer.expert_bytes("down")
     if kern["a_us"] >= kern["b_us"]:
-        name, nbytes, us = "mqh::k_fast_gate_up<12, 12, 32, false, 1>", a_bytes, kern["a_us"]
+        name, nbytes, us = "mqh::k_fast_gate_up<12, 12, 32, false, 1, true>", a_bytes, kern["a_us"]
     else:
         name, nbytes, us = "mqh::k_fast_down<14, 14, 8, 1, false>", b_bytes, kern["b_us"]
     return _hbm_roofline(name, nbytes, us, floor(nbytes) if floor else None)
@@ -610,7 +610,7 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
     dom = "A" if kb["A"] >= kb["B"] else "B"
     frac = frac_a if dom == "A" else 1 - frac_a
     kname = {"prefill": {"A": "mqh::k_prefill_gate_up<11, 11, 8, false, 2>", "B": "mqh::k_prefill_down<11, 11, 2, 1>"},
-             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32, false, 2>", "B": "mqh::k_fast_down_bal<11, 11, 8, 4>"}}[best][dom]
+             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32, false, 2, false>", "B": "mqh::k_fast_down_bal<11, 11, 8, 4>"}}[best][dom]
     out = {
         "workload": f"batched decode: {T} tokens, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
                     f"logits + shared, all Q3_K, {n_layers} resident layers rotated",
@@ -861,7 +861,7 @@ def bench_fp16_graph_decode(dev, n_layers: int, reps: int, cpu_seconds: float) -
         "metric": "quant-weight GB/s per layer-step", "value": round(step_bytes(L0) / (ms * 1e-3) / 1e9, 1),
         "unit": "GB/s", "us_per_layer": round(ms * 1e3, 3), "parity_max_rel_err": float(f"{err:.3e}"),
         "kernels_us": {"A": round(kern["a_us"], 3), "B": round(kern["b_us"], 3)},
-        "roofline": _hbm_roofline("mqh::k_fast_gate_up<12, 12, 32, true, 1>" if dom == "A" else
+        "roofline": _hbm_roofline("mqh::k_fast_gate_up<12, 12, 32, true, 1, true>" if dom == "A" else
                                   "mqh::k_fast_down<14, 14, 8, 1, true>",
                                   a_bytes if dom == "A" else step_bytes(L0) - a_bytes,
                                   kern["a_us"] if dom == "A" else kern["b_us"]),

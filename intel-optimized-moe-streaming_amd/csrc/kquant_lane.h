@@ -47,6 +47,19 @@ __host__ __device__ inline int32_t sdot4(uint32_t a, uint32_t b, int32_t c) {
 #endif
 }
 
+// sdot4(a, b, 0).  On the device the three-operand form with an inline zero
+// accumulator: the compiler selects the two-operand v_dot4c for the builtin,
+// whose accumulator must first be zeroed by a v_mov of its own.
+__host__ __device__ inline int32_t sdot4_0(uint32_t a, uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    int32_t r;
+    __asm__("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+#else
+    return sdot4(a, b, 0);
+#endif
+}
+
 // Reciprocal scale 127 / amax of a run (0 for an all-zero run); the run scale
 // stored beside the digits is amax / (127 * 254).  The device uses the hardware
 // reciprocal (1 ulp): a scale off by 1e-7 changes the reconstruction by 1e-7 of
@@ -165,10 +178,20 @@ __host__ __device__ inline void lane_x(const DigitsRef& v, int blk, int k, LaneX
 }
 
 // Exact integer dot of 16-column piece p (quant dwords q[0..3]) with both planes: 254*I0 + I1.
+// Z: the chains start with sdot4_0 (no zeroing v_mov); without it the builtin
+// form throughout, which the register allocator handles with less pressure.
+template <bool Z = true>
 __host__ __device__ inline int32_t piece_dot(const uint32_t* q, const LaneX& x, int p) {
-    int32_t i0 = 0, i1 = 0;
+    int32_t i0, i1;
+    if constexpr (Z) {
+        i0 = sdot4_0(q[0], x.d0[4 * p]);
+        i1 = sdot4_0(q[0], x.d1[4 * p]);
+    } else {
+        i0 = sdot4(q[0], x.d0[4 * p], 0);
+        i1 = sdot4(q[0], x.d1[4 * p], 0);
+    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 1; i < 4; ++i) {
         i0 = sdot4(q[i], x.d0[4 * p + i], i0);
         i1 = sdot4(q[i], x.d1[4 * p + i], i1);
     }
@@ -299,7 +322,8 @@ __host__ __device__ inline float q6_d(const uint32_t* raw) {
     else return f16_bits_to_f32(raw[18] & 0xFFFFu);
 }
 
-template <int T, bool DW = false>
+// Z: piece_dot's form (see there).
+template <int T, bool DW = false, bool Z = true>
 __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const LaneX& x) {
     if constexpr (T == T_Q8_0) {
         // block 0: d at bytes 0-1, quants at bytes 2..33 (dwords shifted by two
@@ -311,8 +335,8 @@ __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const Lane
             uint32_t q[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) q[i] = rotr_pair(raw[4 * p + i + 1], raw[4 * p + i], 16);
-            run0 = fmaf(x.xs[p], (float)piece_dot(q, x, p), run0);
-            run1 = fmaf(x.xs[2 + p], (float)piece_dot(raw + 9 + 4 * p, x, 2 + p), run1);
+            run0 = fmaf(x.xs[p], (float)piece_dot<Z>(q, x, p), run0);
+            run1 = fmaf(x.xs[2 + p], (float)piece_dot<Z>(raw + 9 + 4 * p, x, 2 + p), run1);
         }
         return fmaf(d0, run0, d1 * run1);
     } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
@@ -333,7 +357,7 @@ __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const Lane
                     q[i] = (raw[QS + 4 * p + i] >> (4 * r)) & 0x0F0F0F0Fu;
                     if constexpr (T == T_Q5_K) q[i] |= ((raw[4 + 4 * p + i] >> (2 * k + r)) & 0x01010101u) << 4;
                 }
-                run = fmaf(x.xs[2 * r + p], (float)piece_dot(q, x, 2 * r + p), run);
+                run = fmaf(x.xs[2 * r + p], (float)piece_dot<Z>(q, x, 2 * r + p), run);
             }
             acc = fmaf((float)((sc2 >> (8 * r)) & 0xFFu), run, acc);
             off = fmaf((float)((mn2 >> (8 * r)) & 0xFFu), x.sum[2 * r] + x.sum[2 * r + 1], off);
@@ -359,7 +383,7 @@ __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const Lane
                 const int sb = 2 * s + p;
                 const int sc = (int)(int8_t)(uint8_t)((sb < 4 ? raw[16] >> (8 * sb) : raw[17] >> (8 * (sb - 4))) & 0xFFu);
                 const int pc = 2 * r + p;
-                acc = fmaf((float)sc, fmaf(x.xs[pc], (float)piece_dot(q, x, pc), -32.0f * x.sum[pc]), acc);
+                acc = fmaf((float)sc, fmaf(x.xs[pc], (float)piece_dot<Z>(q, x, pc), -32.0f * x.sum[pc]), acc);
             }
         }
         return d * acc;
@@ -369,16 +393,24 @@ __host__ __device__ inline float lane_dot(const uint32_t* raw, int k, const Lane
         float acc = 0.0f;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            // hmask bit 4h + s of every byte moved to bit 2 by one rotation
-            // (rotating right by 4h + s - 2 mod 32 takes byte k's bit 4h + s to
-            // bit 8k + 2 without crossing the word's top)
-            const int r = (4 * h + s - 2) & 31;
+            // Runs 1 and 2 keep their two quant bits in place (bits 2s, 2s + 1 of
+            // every byte: the byte is 4^s q <= 112, still an int8, and the piece's
+            // integer dot 4^s times the run's, taken back exactly by the run
+            // scale); runs 0 and 3 shift them to bits 0, 1.  The mask bit 4h + s
+            // goes to the bit above them, sp + 2, by one rotation (right by
+            // 4h + s - 2 - sp mod 32, which takes byte k's bit 4h + s to bit
+            // 8k + sp + 2 without crossing the word's top).
+            const int sp = (s == 1 || s == 2) ? 2 * s : 0;
+            const int r = (4 * h + s - 2 - sp) & 31;
             uint32_t q[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                q[i] = ((raw[4 + i] >> (2 * s)) & 0x03030303u) | (rotr(raw[i], r) & 0x04040404u);
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo = sp ? raw[4 + i] & (0x03030303u << sp) : (raw[4 + i] >> (2 * s)) & 0x03030303u;
+                q[i] = lo | (rotr(raw[i], r) & (0x04040404u << sp));
+            }
+            const float xs = sp ? x.xs[s] * (sp == 2 ? 0.25f : 0.0625f) : x.xs[s];
             const int sc = k3_scale_run(raw + 8, sh, s);
-            acc = fmaf((float)sc, fmaf(x.xs[s], (float)piece_dot(q, x, s), -4.0f * x.sum[s]), acc);
+            acc = fmaf((float)sc, fmaf(xs, (float)piece_dot<Z>(q, x, s), -4.0f * x.sum[s]), acc);
         }
         return d * acc;
     }

@@ -532,6 +532,41 @@ def test_batched_uniform_types(hip, oracle_mod, gt):
 
 
 @pytest.mark.parametrize("fp16", [0, 1])
+@pytest.mark.parametrize("shape", [(1024, 1024, 4), (512, 2048, 2)], ids=["h1024-i1024-k4", "h512-i2048-k2"])
+@pytest.mark.parametrize("routed,shared_t", [((12, 14), (12, 14)), ((11, 11), (14, 14))])
+def test_one_token_shared_item_on_two_waves_narrow(hip, oracle_mod, routed, shared_t, shape, fp16):
+    """The two-wave shared item at 16 and 8 lanes per row: one token at hidden
+    1024 / intermediate 1024 with top-4 and hidden 512 / intermediate 2048 with
+    top-2, where kernel A also deals one wave a slot (top_k + 1 slots, one row
+    group of every slot a workgroup); against the oracle and the generic
+    kernels, both graphs."""
+    gu, dn = routed
+    t = {"gate": gu, "up": gu, "down": dn}
+    sh = {"gate": shared_t[0], "up": shared_t[0], "down": shared_t[1]}
+    H, I, K = shape
+    E = 12
+    layer, host, shared = make_layer(600 + H + K + gu + shared_t[0] + fp16, E, H, I, t, shared_types=sh,
+                                     scale=0.002 if fp16 else 0.01)
+    rng = np.random.default_rng(H + I + gu + fp16)
+    X = (rng.standard_normal((1, H)) * (0.05 if fp16 else 1.0)).astype(np.float32)
+    ids = rng.permutation(E)[:K][None]
+    ws = rng.dirichlet(np.ones(K), size=1).astype(np.float32)
+    print(f"one token, H={H} I={I} K={K} routed={routed} shared={shared_t} fp16={fp16}", flush=True)
+    old = hip.mqh_set_decode_path(0)
+    try:
+        got, s0 = run(layer, X, ids, ws, fp16=fp16)
+        assert hip.mqh_last_decode_path() == 0
+        hip.mqh_set_decode_path(1)
+        gen, s1 = run(layer, X, ids, ws, fp16=fp16)
+    finally:
+        hip.mqh_set_decode_path(old)
+    assert s0 == 0 and s1 == 0
+    want = oracle_layer(oracle_mod, layer, host, shared, X[0], ids[0].tolist(), ws[0].tolist(), fp16=fp16)
+    assert oracle_mod.max_relative_error(got[0], want) <= TOL, (shape, routed, shared_t, fp16)
+    assert oracle_mod.max_relative_error(got[0], gen[0]) <= TOL, (shape, routed, shared_t, fp16)
+
+
+@pytest.mark.parametrize("fp16", [0, 1])
 @pytest.mark.parametrize("routed,shared_t", [((12, 14), (12, 14)), ((12, 14), (14, 14)), ((11, 11), (14, 14)),
                                               ((12, 8), (14, 14))])
 def test_one_token_shared_item_on_two_waves(hip, oracle_mod, routed, shared_t, fp16):

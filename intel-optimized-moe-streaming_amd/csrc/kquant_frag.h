@@ -192,6 +192,15 @@ __host__ __device__ inline void frag_biased(uint32_t w, h2_t& lo, h2_t& hi) {
     hi = frag_bits_h2(frag_perm(0x64646464u, w, 0x04030402u));
 }
 
+// x rotated right by r (0..31) (v_alignbit_b32 on the device)
+__host__ __device__ inline uint32_t frag_rotr(uint32_t x, int r) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_alignbit(x, x, (uint32_t)r);
+#else
+    return r ? (x >> r) | (x << (32 - r)) : x;
+#endif
+}
+
 __host__ __device__ inline h2_t frag_splat(_Float16 v) {
     h2_t h;
     h[0] = v;
@@ -212,7 +221,9 @@ __host__ __device__ inline void frag_bytes_f16(uint32_t w, _Float16 bias, h2_t& 
 // s[m >> 2][(m >> 1) & 1].
 template <int T> struct FragPrep { h2_t s[2], c[2]; };
 
-template <int T>
+// IP: the Q3_K operand with its quant bits in place (frag_step); the other
+// types ignore it.
+template <int T, bool IP = true>
 __host__ __device__ inline void frag_prep(const uint32_t* r, int q, FragPrep<T>& P) {
     const int qq = (q + 3) & 3;
     if constexpr (T == T_Q8_0) {
@@ -252,6 +263,16 @@ __host__ __device__ inline void frag_prep(const uint32_t* r, int q, FragPrep<T>&
         const uint32_t hb = frag_perm(r[11], r[10], lo ? 0x05030503u : 0x04020402u);
         const uint32_t top = ((hb >> (4 * H)) & 0x00000303u) | ((hb >> (4 * H + 2)) & 0x03030000u);
         frag_bytes_f16(nib | (top << 4), (_Float16)32.0f, P.s[0], P.s[1]);
+        if constexpr (!IP) return;
+        // run S's operand bytes are F q with F = 1, 4, 16, 16 (frag_step): its
+        // scale is taken as sc / F (exact)
+        h2_t f0, f1;
+        f0[0] = (_Float16)1.0f;
+        f0[1] = (_Float16)0.25f;
+        f1[0] = (_Float16)0.0625f;
+        f1[1] = (_Float16)0.0625f;
+        P.s[0] = P.s[0] * f0;
+        P.s[1] = P.s[1] * f1;
     }
 }
 
@@ -262,7 +283,7 @@ __host__ __device__ inline _Float16 frag_pick(const h2_t* v) { return v[M >> 2][
 // the scaled quants.  The operand against a low-order B plane is a[0] (for
 // Q6_K a[0] is sc*q rounded to FP16: its error on a term that is itself 2^-12
 // of the result is below FP32 rounding).
-template <int T, int M>
+template <int T, int M, bool IP = true>
 __host__ __device__ inline void frag_step(const uint32_t* r, const FragPrep<T>& P, int q, h8_t* a) {
     const int qq = (q + 3) & 3;
     h2_t p[4];
@@ -317,12 +338,26 @@ __host__ __device__ inline void frag_step(const uint32_t* r, const FragPrep<T>& 
             a[1][2 * i + 1] = lo[1];
         }
     } else {  // Q3_K: qs bytes 8(M & 1) .. +8, bits 2(M >> 1); hmask same bytes, bit 4(qq >> 1) + (M >> 1)
-        constexpr int W = 2 * (M & 1), S = M >> 1;
-        const int sh = 4 * (qq >> 1) + S;
-        const uint32_t q0 = ((r[W] >> (2 * S)) & 0x03030303u) | (((r[4 + W] >> sh) & 0x01010101u) << 2);
-        const uint32_t q1 = ((r[W + 1] >> (2 * S)) & 0x03030303u) | (((r[5 + W] >> sh) & 0x01010101u) << 2);
-        frag_bytes_f16(q0, (_Float16)4.0f, p[0], p[1]);     // q - 4, exact
-        frag_bytes_f16(q1, (_Float16)4.0f, p[2], p[3]);
+        // IP: run S's two quant bits stay at bits 2S, 2S + 1 of every byte (run
+        // 3's move down to bits 4, 5) and the mask bit goes to the bit above them
+        // by one rotation (right by sh - QS - 2 mod 32 takes byte k's bit sh to
+        // bit 8k + QS + 2): the byte is F q with F = 2^QS (<= 112), and frag_prep
+        // holds the run's scale as sc / F.  Otherwise q itself, at bits 0..2.
+        constexpr int W = 2 * (M & 1), S = M >> 1, QS = IP ? (S == 3 ? 4 : 2 * S) : 0;
+        constexpr float F = (float)(1 << QS);
+        const int sh = 4 * (qq >> 1) + S, rr = (sh - QS - 2) & 31;
+        uint32_t q0, q1;
+        if constexpr (IP) {
+            const uint32_t l0 = S == 3 ? (r[W] >> 2) & 0x30303030u : r[W] & (0x03030303u << QS);
+            const uint32_t l1 = S == 3 ? (r[W + 1] >> 2) & 0x30303030u : r[W + 1] & (0x03030303u << QS);
+            q0 = l0 | (frag_rotr(r[4 + W], rr) & (0x04040404u << QS));
+            q1 = l1 | (frag_rotr(r[5 + W], rr) & (0x04040404u << QS));
+        } else {
+            q0 = ((r[W] >> (2 * S)) & 0x03030303u) | (((r[4 + W] >> sh) & 0x01010101u) << 2);
+            q1 = ((r[W + 1] >> (2 * S)) & 0x03030303u) | (((r[5 + W] >> sh) & 0x01010101u) << 2);
+        }
+        frag_bytes_f16(q0, (_Float16)(4.0f * F), p[0], p[1]);     // F (q - 4), exact
+        frag_bytes_f16(q1, (_Float16)(4.0f * F), p[2], p[3]);
         const h2_t s = frag_splat(frag_pick<M>(P.s));
         for (int i = 0; i < 4; ++i) {
             const h2_t v = p[i] * s;

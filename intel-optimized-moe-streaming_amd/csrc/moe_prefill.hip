@@ -368,7 +368,11 @@ __device__ __forceinline__ void pf_planes_store(const PfPlanes<K, SPLIT>& r, int
 // so the loads of the next chunk are in flight while one ends.  prefetch()
 // loads the first blocks before the caller stages the tokens, so that the two
 // overlap.  D layout: lane l holds rows 4(l/16) + i, token column l % 16.
-template <int T, int NMAT, int NB, int CPW, int RING = PF_RING>
+// IP: the Q3_K operand form (frag_step): the down kernel takes the in-place
+// one (the Q3_K-routed, Q6_K-shared down projections 44.3/44.7 -> 43.1/42.8 us
+// at the 128-token prompt), the gate/up kernel the other (its mixed instance
+// measured 94.2/94.8 -> 97.2/96.7 us with the in-place form, at 128 VGPRs).
+template <int T, int NMAT, int NB, int CPW, int RING = PF_RING, bool IP = true>
 struct PfRows {
     static constexpr int NW = FragGeo<T>::NW, BB = frag_unit_bytes<T>(), NBT = NB * CPW;
     // R ring slots: block b lives in slot b % R; while block b is computed,
@@ -417,7 +421,7 @@ struct PfRows {
             const int off = brow + frag_col<T, m>();
             const h8_t bh = *(const h8_t*)(xh + off);
             h8_t a[2];
-            frag_step<T, m>(cur[0], sp, q, a);
+            frag_step<T, m, IP>(cur[0], sp, q, a);
             f32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], bh, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             if constexpr (SPLIT) {
                 const h8_t bl = *(const h8_t*)(xl + off);
@@ -445,7 +449,7 @@ struct PfRows {
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt) {
             P[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            frag_prep<T>(cur[mt], q, sp[mt]);
+            frag_prep<T, IP>(cur[mt], q, sp[mt]);
         }
         pf_unroll(std::make_integer_sequence<int, 8>{}, [&](auto mc) {
             constexpr int m = decltype(mc)::value;
@@ -456,7 +460,7 @@ struct PfRows {
 #pragma unroll
             for (int mt = 0; mt < NMAT; ++mt) {
                 h8_t a[2];
-                frag_step<T, m>(cur[mt], sp[mt], q, a);
+                frag_step<T, m, IP>(cur[mt], sp[mt], q, a);
                 P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], bh, P[mt], 0, 0, 0);
                 if constexpr (FragGeo<T>::NA == 2) P[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], bh, P[mt], 0, 0, 0);
                 if constexpr (SPLIT)
@@ -753,7 +757,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) PF_OCC_GU void k_prefill_gate_up(con
     auto body = [&](auto tc) {
         constexpr int T = decltype(tc)::value;
         const int64_t row_bytes = (int64_t)NBH * frag_unit_bytes<T>();
-        PfRows<T, 1, NBH, CPW, (SGT != GT && T == SGT) ? PF_RING_SHARED : PF_RING> g;
+        PfRows<T, 1, NBH, CPW, (SGT != GT && T == SGT) ? PF_RING_SHARED : PF_RING, false> g;
         g.W[0] = W0 + (int64_t)(rbase + (lane & 15)) * row_bytes;
         g.chunk_stride = PF_ROWS_GU * row_bytes;
         g.q = q;

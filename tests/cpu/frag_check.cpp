@@ -56,12 +56,12 @@ Tile stage(const float* x, int ntok, int K, int split) {
     return t;
 }
 
-template <int T, int M>
+template <int T, int M, bool IP = true>
 void step(const uint32_t* r, int row, int q, int b, const Tile& t, int split, std::vector<double>& P) {
     h8_t a[2];
     FragPrep<T> sp;
-    frag_prep<T>(r, q, sp);
-    frag_step<T, M>(r, sp, q, a);
+    frag_prep<T, IP>(r, q, sp);
+    frag_step<T, M, IP>(r, sp, q, a);
     const h8_t alo = frag_lo_operand<T>(a);
     const int col = frag_col<T, M>() + frag_lane_col<T>((q + 3) & 3);
     for (int j = 0; j < t.ntok; ++j) {
@@ -114,7 +114,7 @@ void gemm_q8(const uint8_t* w, int K, const Tile& t, int split, float* out) {
         for (int row = 0; row < 16; ++row) out[(size_t)j * 16 + row] = (float)ldexp(acc[row * 16 + j], t.k[j]);
 }
 
-template <int T>
+template <int T, bool IP = true>
 void gemm(const uint8_t* w, int K, const Tile& t, int split, float* out) {
     constexpr int BB = block_bytes(T);
     const int nb = K / 256;
@@ -126,14 +126,14 @@ void gemm(const uint8_t* w, int K, const Tile& t, int split, float* out) {
             const int row = l % 16, q = l / 16;
             uint32_t r[FragGeo<T>::NW];
             frag_load<T>(w + (size_t)row * nb * BB + (size_t)b * BB, q, r);
-            step<T, 0>(r, row, q, b, t, split, P);
-            step<T, 1>(r, row, q, b, t, split, P);
-            step<T, 2>(r, row, q, b, t, split, P);
-            step<T, 3>(r, row, q, b, t, split, P);
-            step<T, 4>(r, row, q, b, t, split, P);
-            step<T, 5>(r, row, q, b, t, split, P);
-            step<T, 6>(r, row, q, b, t, split, P);
-            step<T, 7>(r, row, q, b, t, split, P);
+            step<T, 0, IP>(r, row, q, b, t, split, P);
+            step<T, 1, IP>(r, row, q, b, t, split, P);
+            step<T, 2, IP>(r, row, q, b, t, split, P);
+            step<T, 3, IP>(r, row, q, b, t, split, P);
+            step<T, 4, IP>(r, row, q, b, t, split, P);
+            step<T, 5, IP>(r, row, q, b, t, split, P);
+            step<T, 6, IP>(r, row, q, b, t, split, P);
+            step<T, 7, IP>(r, row, q, b, t, split, P);
             const uint32_t hdr = r[FragGeo<T>::HDR];
             d[row] = frag_d<T>(hdr);
             dmin[row] = frag_dmin(hdr);
@@ -161,7 +161,9 @@ void gemm(const uint8_t* w, int K, const Tile& t, int split, float* out) {
 
 // out[tok][row] = sum_c W[row][c] x[tok][c] for 16 quantized rows (K columns)
 // and ntok <= 16 FP32 token rows, computed from the kernel's operands.  split:
-// 1 = high and low FP16 planes of x, 0 = high plane only (BF16 inputs).
+// 1 = high and low FP16 planes of x, 0 = high plane only (BF16 inputs).  Type
+// 11 takes the in-place Q3_K operand (the down kernel's), -11 the other (the
+// gate/up kernel's).
 extern "C" void mqh_cpu_frag_gemm(int type, const uint8_t* w, int K, const float* x, int ntok, int split, float* out) {
     const Tile t = stage(x, ntok, K, split);
     switch (type) {
@@ -169,6 +171,7 @@ extern "C" void mqh_cpu_frag_gemm(int type, const uint8_t* w, int K, const float
         case T_Q5_K: gemm<T_Q5_K>(w, K, t, split, out); break;
         case T_Q6_K: gemm<T_Q6_K>(w, K, t, split, out); break;
         case T_Q8_0: gemm_q8(w, K, t, split, out); break;
+        case -T_Q3_K: gemm<T_Q3_K, false>(w, K, t, split, out); break;
         default: gemm<T_Q3_K>(w, K, t, split, out); break;
     }
 }

@@ -63,16 +63,17 @@ def frag_gemm(chk, t, rows, K, x, split):
     return out
 
 
-@pytest.mark.parametrize("t", [11, 12, 13, 14, 8])
+# -11: Q3_K with the gate/up kernel's operand form (11: the down kernel's, quant bits in place)
+@pytest.mark.parametrize("t", [11, -11, 12, 13, 14, 8])
 @pytest.mark.parametrize("kind", ["normal", "heavy", "sparse", "large"])
 @pytest.mark.parametrize("split", [1, 0], ids=["fp32-x", "bf16-x"])
 def test_frag_gemm_matches_oracle(chk, oracle_mod, t, kind, split):
     from flash_moe_hip.synthetic import random_tensor
 
-    rng = np.random.default_rng(1000 * t + 10 * len(kind) + split)
+    rng = np.random.default_rng(1000 * abs(t) + 10 * len(kind) + split)
     for K in (256, 512, 2048):
-        rows = random_tensor(rng, t, 16, K)
-        w = oracle_mod.dequant(t, rows).reshape(16, K).astype(np.float64)
+        rows = random_tensor(rng, abs(t), 16, K)
+        w = oracle_mod.dequant(abs(t), rows).reshape(16, K).astype(np.float64)
         x = tokens(rng, 16, K, kind)
         if not split:
             x = bf16(x)

@@ -529,8 +529,6 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     shared_scale<NX>(p, sh, scale_wg, gate_wg, xv, gi);
 }
 
-// Whether the calling wave's item is the shared expert's: the item and slot
-// as gate_up_items computes them (wave-uniform).
 // The shared expert's item split over two waves, one token, one row group xg
 // a workgroup beside the top_k routed waves of that row group (SPLIT): wave
 // top_k takes the gate rows, wave top_k + 1 the same up rows, each loading and
@@ -590,6 +588,8 @@ __device__ __forceinline__ void gate_up_shared_half(const DecodeHot& h, const De
     shared_scale<NX>(p, sh, scale_wg, gate_wg, xv, gi);
 }
 
+// Whether the calling wave's item is the shared expert's: the item and slot
+// as gate_up_items computes them (wave-uniform).
 template <int LPR, bool ROUTED, int IPW>
 __device__ __forceinline__ bool wave_is_shared(const DecodeHot& h) {
     constexpr int RPI = 64 / LPR;

@@ -7,6 +7,9 @@
 * Batched decode: 16 tokens in one call, every matrix Q3_K, top-8 of N(0,1)
   logits (experts overlap across tokens); the decode kernels and the grouped
   prefill kernels.
+* Decode in the reference model's type mixes (Q3_K; Q4_K/Q6_K; Q4_K/Q8_0 with
+  the Q6_K shared expert): single tokens and 16-token calls, FP32 and FP16
+  graphs, and the generic kernels beside the integer-digit ones.
 * Prefill: a 128-token BF16 prompt, Q4_K/Q6_K, top-8 of N(0,1) logits over 256
   experts (~252 distinct experts, ~4 tokens each, ~262 partly filled tiles).
 
@@ -245,5 +248,79 @@ def test_prefill_real_model_mix_full_scale(oracle_mod, hip, mix):
     errs = [oracle_mod.max_relative_error(got[t], want[t]) for t in range(T)]
     print(f"  prefill {mix} max rel err over {T} tokens: {max(errs):.3e}", flush=True)
     assert max(errs) <= PREFILL_TOL, (int(np.argmax(errs)), max(errs))
+    del layer
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("fp16", [0, 1], ids=["fp32-graph", "fp16-graph"])
+@pytest.mark.parametrize("mix", list(REAL_MIXES))
+def test_decode_real_model_mix_full_scale(oracle_mod, hip, mix, fp16):
+    """The decode layer in the reference model's type mixes at full size (256
+    experts, hidden 2048, intermediate 512, top-8 + the Q6_K shared expert):
+    four tokens each as its own call (kernel A with the shared item on two
+    waves and the shared expert's own item code) and 16 tokens in one call
+    (two items a wave), both graphs (the FP16 graph at its check scales, d ~
+    0.002, x ~ 0.05), every token against the oracle: routed experts in the
+    call's graph, the shared expert in the FP32 graph as the reference runs it."""
+    import torch
+
+    from flash_moe_hip.layer_store import ExpertLayer
+    from flash_moe_hip.moe_gpu import MoeRunner
+
+    types = REAL_MIXES[mix]
+    q6 = {"gate": 14, "up": 14, "down": 14}
+    kw = {"scale": 0.002} if fp16 else {}
+    layer = ExpertLayer.synthetic(types, E, H, I, seed=9200 + len(mix) + 10 * fp16, shared_types=q6,
+                                  shared_intermediate=I, gate_inp=True, device="cuda", **kw)
+    host, shared, gi = _host_layer(layer)
+    rng = np.random.default_rng(60 + len(mix) + fp16)
+    X = (rng.standard_normal((20, H)) * (0.05 if fp16 else 1.0)).astype(np.float32)
+    ids, ws = _topk(rng, 20)
+
+    def expert(e):
+        return {r: host[r][e * layer.expert_bytes(r):(e + 1) * layer.expert_bytes(r)] for r in host}
+
+    def want(t):
+        outs = [oracle_mod.expert_forward(expert(int(e)), types, X[t], H, I, fp16) for e in ids[t]]
+        gate = oracle_mod._sigmoid(np.float32(X[t] @ gi).reshape(()))
+        sh = (gate * oracle_mod.expert_forward(shared, q6, X[t], H, I, 0)).astype(np.float32)
+        return oracle_mod.combine(outs, [float(v) for v in ws[t]], sh)
+
+    with ThreadPoolExecutor(8) as pool:
+        wants = list(pool.map(want, range(20)))
+    runner = MoeRunner()
+    # the digit error of a 16-column run (<= 1.6e-5 of its max per value), in the
+    # hidden vector and again in the SwiGLU product, reaches ~1.2e-4 of the output
+    # on the Q4_K/Q6_K mix's tokens here (the same bound the 32-expert tests hold)
+    tol = TOL if fp16 else 2 * DIGIT_TOL
+    worst = 0.0
+    for t in range(4):
+        print(f"full-scale decode {mix} fp16={fp16} token {t}", flush=True)
+        got, rc = runner.fetch(runner.decode(layer, torch.from_numpy(X[t:t + 1]).cuda(),
+                                             torch.from_numpy(ids[t:t + 1]).cuda(),
+                                             torch.from_numpy(ws[t:t + 1]).cuda(), fp16_graph=fp16))
+        assert rc == 0
+        worst = max(worst, oracle_mod.max_relative_error(got[0], wants[t]))
+    print(f"full-scale decode {mix} fp16={fp16}: 16 tokens in one call", flush=True)
+    got, rc = runner.fetch(runner.decode(layer, torch.from_numpy(X[4:]).cuda(), torch.from_numpy(ids[4:]).cuda(),
+                                         torch.from_numpy(ws[4:]).cuda(), fp16_graph=fp16))
+    assert rc == 0
+    for t in range(16):
+        worst = max(worst, oracle_mod.max_relative_error(got[t], wants[4 + t]))
+    print(f"  decode {mix} fp16={fp16} max rel err over 20 tokens: {worst:.3e}", flush=True)
+    assert worst <= tol
+    if not fp16:
+        # the generic kernels (FP32 activations, no digits) on the same 16 tokens:
+        # the FP32 reference arithmetic up to summation order
+        old = hip.mqh_set_decode_path(1)
+        try:
+            gen, rc = runner.fetch(runner.decode(layer, torch.from_numpy(X[4:]).cuda(),
+                                                 torch.from_numpy(ids[4:]).cuda(), torch.from_numpy(ws[4:]).cuda()))
+        finally:
+            hip.mqh_set_decode_path(old)
+        assert rc == 0
+        gen_err = max(oracle_mod.max_relative_error(gen[t], wants[4 + t]) for t in range(16))
+        print(f"  generic kernels {mix}: max rel err {gen_err:.3e}", flush=True)
+        assert gen_err <= 1e-5
     del layer
     torch.cuda.empty_cache()

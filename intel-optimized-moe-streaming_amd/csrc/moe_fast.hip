@@ -476,8 +476,13 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
             lane_xh<GT>(sh.x16, blk, k, XH);
             __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
-            // 3. gate and up dot products
+            // 3. gate and up dot products, a scheduling barrier between them:
+            // every gate dot product then issues ahead of the wait for the up
+            // loads (without it the last one waited behind it: 10.53 -> 10.50 us
+            // per FP16-graph layer; the same barrier in the digit path changed
+            // nothing)
             g[0] = lane_dot_f16<GT, true>(rg[0], k, XH);
+            __builtin_amdgcn_sched_barrier(0);
             u[0] = lane_dot_f16<GT, true>(ru[0], k, XH);
         }
     } else {

@@ -59,6 +59,9 @@ struct DecodeHot {
     const float* weights;
     const float* sh_gate_inp;
     int top_k, S, has_shared, n_experts, a_inter, a_waves;
+    // kernel B: the shared expert's gate (from kernel A) and down weights
+    const float* sh_scale;
+    const uint8_t* sh_down;
 };
 
 // silu(g) * u with the hardware exp2 and reciprocal (a few ulp; the FP32 graph
@@ -678,8 +681,10 @@ struct SharedB {
 // go to waves 0 .. NPB-1, one each, after their own slot.  With eight routed
 // slots and four row groups, waves w and w + 4 (one SIMD) then hold nine row
 // groups between them on every SIMD, where nine waves (one per slot) put three
-// on one SIMD.  SDT is the shared expert's down type.
-template <int DT, int LPR, int NPB_, bool F16G, int SDT = DT, bool BAL = false>
+// on one SIMD.  SDT is the shared expert's down type.  ARGD: the shared
+// expert's down weights from the kernel's preloaded argument (h.sh_down), else
+// from the argument block.
+template <int DT, int LPR, int NPB_, bool F16G, int SDT = DT, bool BAL = false, bool ARGD = true>
 __device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams& p, int bx, int t,
                                           SharedB<GeoB<LPR, NPB_>::RB>& sh) {
     constexpr int N = LaneGeo<DT>::NRAW, NS = LaneGeo<SDT>::NRAW;
@@ -700,7 +705,7 @@ __device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams
     act_load<I>(h.act + ((int64_t)t * h.S + s) * I, lane, A);
     __builtin_amdgcn_sched_barrier(0);
 
-    const uint8_t* D = p.sh_down;
+    const uint8_t* D = BAL || !ARGD ? p.sh_down : h.sh_down;
     bool bad = false;
     float w = 0.0f;
     if (!shared) {
@@ -724,6 +729,14 @@ __device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams
             D = down + (int64_t)e * down_eb;
             w = bad ? 0.0f : w_raw;
         }
+    } else if constexpr (!BAL) {
+        // the shared expert's gate (kernel A's sigmoid), issued here, ahead of
+        // the weights, from a preloaded argument: loaded where lane 0 stores
+        // it, after the dot products, it was two round trips (the argument
+        // block, then the value) in the shared wave's tail ahead of the combine
+        // (config 3 9.33 -> 9.22 us per layer, FP16 graph 10.47 -> 10.33, four
+        // tokens 24.57 -> 24.29)
+        w = h.sh_scale[t];
     }
 
     // then every weight load, with no branch around them (a conditional load
@@ -770,7 +783,7 @@ __device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams
 #pragma unroll
     for (int q = 0; q < NPB; ++q)
         if (li == 0) sh.s_y[s][q * RPI + rr] = bad ? 0.0f : v[q];
-    if (lane == 0) sh.s_w[s] = shared ? p.sh_scale[t] : w;
+    if (lane == 0) sh.s_w[s] = w;
     if constexpr (BAL) {
         if (s < NPB) {   // wave-uniform: the shared slot's row group s, from its own copy of the shared digits
             // (loaded only now: held from the start, these registers keep the
@@ -820,15 +833,20 @@ __device__ __forceinline__ void down_combine(const DecodeHot& h, const DecodePar
 // 128 VGPRs and they spill)
 template <int DT, int SDT, int LPR, int NPB, bool F16G>
 __global__ __launch_bounds__(LPR == 32 ? 768 : 1024) void k_fast_down(const int32_t* ids, float* act, const float* weights, int top_k,
-                                                   int S, int has_shared, int n_experts, int nbx, DecodeParams p) {
+                                                   int S, int has_shared, int n_experts, int nbx,
+                                                   const float* sh_scale, const uint8_t* sh_down, DecodeParams p) {
     __shared__ SharedB<GeoB<LPR, NPB>::RB> sh;
     const int bx = (int)blockIdx.y * 8 + (int)blockIdx.x;
     if (bx >= nbx) return;   // padding of the last group of eight
-    const DecodeHot h{nullptr, ids, act, weights, nullptr, top_k, S, has_shared, n_experts, 0, 0};
+    const DecodeHot h{nullptr, ids, act, weights, nullptr, top_k, S, has_shared, n_experts, 0, 0, sh_scale, sh_down};
     if constexpr (SDT != DT) {
+        // (the shared expert's down weights from the argument block: with the
+        // preloaded argument this two-type kernel measured slower, the Q3_K
+        // layer with a Q6_K shared expert 9.62 -> 9.77 us, where one-type
+        // kernels gained 0.1 us)
         const int s = uniform(threadIdx.x >> 6);
-        if (has_shared && s == top_k) down_slot<SDT, LPR, NPB, F16G>(h, p, bx, blockIdx.z, sh);
-        else down_slot<DT, LPR, NPB, F16G>(h, p, bx, blockIdx.z, sh);
+        if (has_shared && s == top_k) down_slot<SDT, LPR, NPB, F16G, SDT, false, false>(h, p, bx, blockIdx.z, sh);
+        else down_slot<DT, LPR, NPB, F16G, DT, false, false>(h, p, bx, blockIdx.z, sh);
     } else {
         down_slot<DT, LPR, NPB, F16G>(h, p, bx, blockIdx.z, sh);
     }
@@ -1024,10 +1042,12 @@ static void launch_b_n(const DecodeParams& p, hipStream_t stream, const KernelEv
     const size_t lds = (size_t)p.S * act_lds_bytes(64 * LPR);   // the slots' digits
     if (ev.armed_b())
         hipExtLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB, F16G>), grid, dim3(64 * p.S), lds, stream, ev.b_start,
-                              ev.b_stop, 0, p.ids, p.act, p.weights, p.top_k, p.S, p.has_shared, p.n_experts, nbx, p);
+                              ev.b_stop, 0, p.ids, p.act, p.weights, p.top_k, p.S, p.has_shared, p.n_experts, nbx,
+                              (const float*)p.sh_scale, p.sh_down, p);
     else
         hipLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB, F16G>), grid, dim3(64 * p.S), lds, stream, p.ids, p.act,
-                           p.weights, p.top_k, p.S, p.has_shared, p.n_experts, nbx, p);
+                           p.weights, p.top_k, p.S, p.has_shared, p.n_experts, nbx, (const float*)p.sh_scale, p.sh_down,
+                           p);
 }
 
 // Row groups per wave: one while the grid is small (a single token: every

@@ -30,25 +30,33 @@ __device__ __forceinline__ float ord_score(uint32_t ord) {
     return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord);
 }
 
-// One step of the wavefront maximum: the DPP move and the maximum stay two
-// instructions (the empty asm keeps the compiler from folding them into one
-// DPP maximum).  Lanes outside ROW_MASK keep their own value.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint32_t dpp_max_step(uint32_t v) {
-    int o = __builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROW_MASK, 0xF, false);
+// One step of the wavefront maximum inside each row of 16 lanes: the DPP move
+// and the maximum stay two instructions (the empty asm keeps the compiler from
+// folding them into one DPP maximum).  The patterns used write every lane (row
+// and bank masks full, every source lane inside the row), so the move carries
+// no old value and needs no copy ahead of it.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_max_full(uint32_t v) {
+    int o = __builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
     __asm__ volatile("" : "+v"(o));
     return (uint32_t)o > v ? (uint32_t)o : v;
 }
 
-// Maximum over the wavefront, returned uniform.
+// Maximum over the wavefront, returned uniform: each row's maximum by four DPP
+// steps, then the four rows' (lanes 15, 31, 47, 63) in scalar registers (two
+// more DPP steps across rows and one read of lane 63 took longer: the routed
+// decode 13.99 -> 13.77 us per layer).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = dpp_max_step<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
-    v = dpp_max_step<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
-    v = dpp_max_step<0x141, 0xF>(v);   // row_half_mirror
-    v = dpp_max_step<0x140, 0xF>(v);   // row_mirror: every lane holds its row's maximum
-    v = dpp_max_step<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
-    v = dpp_max_step<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3: lane 63 holds the maximum
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+    v = dpp_max_full<0xB1>(v);    // quad_perm [1,0,3,2]
+    v = dpp_max_full<0x4E>(v);    // quad_perm [2,3,0,1]
+    v = dpp_max_full<0x141>(v);   // row_half_mirror
+    v = dpp_max_full<0x140>(v);   // row_mirror: every lane holds its row's maximum
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+    const uint32_t a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
+    return a > b ? a : b;
 }
 
 // The ords of one token's n_experts scores (st), NM per lane (expert

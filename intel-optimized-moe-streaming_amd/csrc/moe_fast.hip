@@ -728,8 +728,11 @@ __device__ __forceinline__ void down_slot(const DecodeHot& h, const DecodeParams
             const float w_raw = h.weights[t * h.top_k + s];
             const uint8_t* down = p.down;
             const int64_t down_eb = p.down_eb;
-            __asm__ volatile("" ::"s"(e), "s"(w_raw), "s"(down), "s"(down_eb));
-            if (e < 0 || e >= h.n_experts) { bad = true; e = 0; }
+            // (k_fast_down leaves the expert count out of its preloaded
+            // arguments, -1 here, to make room for the shared expert's pointers)
+            const int n_exp = h.n_experts >= 0 ? h.n_experts : p.n_experts;
+            __asm__ volatile("" ::"s"(e), "s"(w_raw), "s"(down), "s"(down_eb), "s"(n_exp));
+            if (e < 0 || e >= n_exp) { bad = true; e = 0; }
             D = down + (int64_t)e * down_eb;
             w = bad ? 0.0f : w_raw;
         }
@@ -829,25 +832,30 @@ __device__ __forceinline__ void down_combine(const DecodeHot& h, const DecodePar
     }
 }
 
-// SDT: the shared expert's down type (its wave takes that code path).
+// SDT: the shared expert's down type (its wave takes that code path).  The
+// leading arguments are the ones preloaded into scalar registers: the shared
+// expert's gate and down pointers among them, so the shared wave issues its
+// weight loads with no argument load first (config 3 9.24 -> 9.10 us per layer
+// against the down pointer read from the argument block); the expert count
+// comes from the argument block with the expert id.
 // Row group bx = blockIdx.x + 8 blockIdx.y of token blockIdx.z (fast_grid).
 // 64 threads a slot: at intermediate 2048 (LPR 32) at most 12 slots fit the
 // digit LDS (fast_supported), so 768 threads, which leaves the FP16 graph's
 // two-type instances the registers they need (a 1024-thread bound caps them at
 // 128 VGPRs and they spill)
 template <int DT, int SDT, int LPR, int NPB, bool F16G>
-__global__ __launch_bounds__(LPR == 32 ? 768 : 1024) void k_fast_down(const int32_t* ids, float* act, const float* weights, int top_k,
-                                                   int S, int has_shared, int n_experts, int nbx,
-                                                   const float* sh_scale, const uint8_t* sh_down, DecodeParams p) {
+__global__ __launch_bounds__(LPR == 32 ? 768 : 1024) void k_fast_down(const int32_t* ids, float* act, const float* weights,
+                                                   const float* sh_scale, const uint8_t* sh_down, int top_k,
+                                                   int S, int has_shared, int nbx, DecodeParams p) {
     __shared__ SharedB<GeoB<LPR, NPB>::RB> sh;
     const int bx = (int)blockIdx.y * 8 + (int)blockIdx.x;
     if (bx >= nbx) return;   // padding of the last group of eight
-    const DecodeHot h{nullptr, ids, act, weights, nullptr, top_k, S, has_shared, n_experts, 0, 0, sh_scale, sh_down};
+    const DecodeHot h{nullptr, ids, act, weights, nullptr, top_k, S, has_shared, -1, 0, 0, sh_scale, sh_down};
     if constexpr (SDT != DT) {
         // (the shared expert's down weights from the argument block: with the
-        // preloaded argument this two-type kernel measured slower, the Q3_K
-        // layer with a Q6_K shared expert 9.62 -> 9.77 us, where one-type
-        // kernels gained 0.1 us)
+        // preloaded argument this two-type kernel measured no faster, the Q3_K
+        // layer with a Q6_K shared expert 9.68 against 9.70 us, where one-type
+        // kernels gained 0.14 us)
         const int s = uniform(threadIdx.x >> 6);
         if (has_shared && s == top_k) down_slot<SDT, LPR, NPB, F16G, SDT, false, false>(h, p, bx, blockIdx.z, sh);
         else down_slot<DT, LPR, NPB, F16G, DT, false, false>(h, p, bx, blockIdx.z, sh);
@@ -1048,12 +1056,11 @@ static void launch_b_n(const DecodeParams& p, hipStream_t stream, const KernelEv
     const size_t lds = (size_t)p.S * act_lds_bytes(64 * LPR);   // the slots' digits
     if (ev.armed_b())
         hipExtLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB, F16G>), grid, dim3(64 * p.S), lds, stream, ev.b_start,
-                              ev.b_stop, 0, p.ids, p.act, p.weights, p.top_k, p.S, p.has_shared, p.n_experts, nbx,
-                              (const float*)p.sh_scale, p.sh_down, p);
+                              ev.b_stop, 0, p.ids, p.act, p.weights, (const float*)p.sh_scale, p.sh_down, p.top_k, p.S,
+                              p.has_shared, nbx, p);
     else
         hipLaunchKernelGGL((k_fast_down<DT, SDT, LPR, NPB, F16G>), grid, dim3(64 * p.S), lds, stream, p.ids, p.act,
-                           p.weights, p.top_k, p.S, p.has_shared, p.n_experts, nbx, (const float*)p.sh_scale, p.sh_down,
-                           p);
+                           p.weights, (const float*)p.sh_scale, p.sh_down, p.top_k, p.S, p.has_shared, nbx, p);
 }
 
 // Row groups per wave: one while the grid is small (a single token: every

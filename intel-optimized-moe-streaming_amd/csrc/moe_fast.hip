@@ -62,6 +62,9 @@ struct DecodeHot {
     // kernel B: the shared expert's gate (from kernel A) and down weights
     const float* sh_scale;
     const uint8_t* sh_down;
+    // kernel A (given ids): the shared expert's gate and up weights
+    const uint8_t* sh_gate;
+    const uint8_t* sh_up;
 };
 
 // silu(g) * u with the hardware exp2 and reciprocal (a few ulp; the FP32 graph
@@ -373,9 +376,12 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
     // the argument-block fields the weight addresses need, awaited together
     // with the expert id (left to itself the compiler loads the id inside the
     // branch below, after a round trip of its own for these fields)
-    const uint8_t *p_gate = p.gate, *p_up = p.up, *p_sh_gate = p.sh_gate, *p_sh_up = p.sh_up;
+    const uint8_t *p_gate = p.gate, *p_up = p.up;
+    const uint8_t *p_sh_gate = ROUTED ? p.sh_gate : h.sh_gate, *p_sh_up = ROUTED ? p.sh_up : h.sh_up;
     const int64_t gate_eb = p.gate_eb, up_eb = p.up_eb;
-    __asm__ volatile("" ::"s"(p_gate), "s"(p_up), "s"(p_sh_gate), "s"(p_sh_up), "s"(gate_eb), "s"(up_eb), "s"(id_raw));
+    const int n_exp = ROUTED ? h.n_experts : p.n_experts;
+    __asm__ volatile("" ::"s"(p_gate), "s"(p_up), "s"(p_sh_gate), "s"(p_sh_up), "s"(gate_eb), "s"(up_eb), "s"(id_raw),
+                     "s"(n_exp));
     __builtin_amdgcn_sched_barrier(0);
 
     // The expert slices: routed expert e, the shared expert, or -- for a wave
@@ -428,7 +434,7 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
         }
     } else if (live && !shared) {
         int e = id_raw;
-        if (e < 0 || e >= h.n_experts) { bad = true; e = 0; }
+        if (e < 0 || e >= n_exp) { bad = true; e = 0; }
         Gm = p_gate + (int64_t)e * gate_eb; Um = p_up + (int64_t)e * up_eb;
     }
 
@@ -528,7 +534,7 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
                 } else {
                     a = silu_mul(gs, us);
                 }
-                h.act[((int64_t)t * h.S + s) * h.a_inter + row + i * RPI] = bad ? 0.0f : a;
+                (ROUTED ? h.act : p.act)[((int64_t)t * h.S + s) * h.a_inter + row + i * RPI] = bad ? 0.0f : a;
             }
         }
         if (bad && lane == 0 && row0 == 0) atomicOr(&p.flags[FLAG_BAD_ID], 1);
@@ -559,8 +565,7 @@ __device__ __forceinline__ void gate_up_shared_half(const DecodeHot& h, const De
     const int xi = min((int)threadIdx.x, NX - 1) * 4;
     const float4 xv = *(const float4*)(xt + xi);
     const float4 gi = *(const float4*)((gate_wg ? h.sh_gate_inp : xt) + xi);
-    const uint8_t* M = upw ? p.sh_up : p.sh_gate;
-    __asm__ volatile("" ::"s"(M));
+    const uint8_t* M = upw ? h.sh_up : h.sh_gate;   // (preloaded arguments)
     __builtin_amdgcn_sched_barrier(0);
     const int rr = lane / LPR, li = lane % LPR, blk = li / LANES_PER_BLOCK, k = li % LANES_PER_BLOCK;
     const int row = xg * RPI + rr;
@@ -590,7 +595,7 @@ __device__ __forceinline__ void gate_up_shared_half(const DecodeHot& h, const De
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         if (li == 0) {
             const float o = sh.half_dot[!upw][rr];
-            h.act[((int64_t)t * h.S + h.top_k) * h.a_inter + row] = upw ? silu_mul(o, v) : silu_mul(v, o);
+            p.act[((int64_t)t * h.S + h.top_k) * h.a_inter + row] = upw ? silu_mul(o, v) : silu_mul(v, o);
         }
     }
     shared_scale<NX>(p, sh, scale_wg, gate_wg, xv, gi);
@@ -634,12 +639,17 @@ __device__ __forceinline__ void gate_up_waves(const DecodeHot& h, const DecodePa
     gate_up_items<GT, GT, LPR, ROUTED, F16G, IPW>(h, p, sh);
 }
 
+// The leading arguments are the ones preloaded into scalar registers: with the
+// shared expert's gate and up pointers among them (has_shared is S - top_k; the
+// expert count is read from the argument block with the expert id and the
+// output pointer at the end), the shared expert's waves issue their weight
+// loads with no argument load first.
 template <int GT, int SGT, int LPR, bool F16G, int IPW = 1, bool SPLIT = false>
-__global__ __launch_bounds__(1024) void k_fast_gate_up(const float* x, const int32_t* ids, float* act, const float* sh_gate_inp, int top_k,
-                                                  int S, int has_shared, int n_experts, int a_inter, int a_waves,
-                                                  DecodeParams p) {
+__global__ __launch_bounds__(1024) void k_fast_gate_up(const float* x, const int32_t* ids, const float* sh_gate_inp,
+                                                  const uint8_t* sh_gate, const uint8_t* sh_up, int top_k, int S,
+                                                  int a_inter, int a_waves, DecodeParams p) {
     __shared__ SharedX<64 * LPR, F16G> sh;
-    const DecodeHot h{x, ids, act, nullptr, sh_gate_inp, top_k, S, has_shared, n_experts, a_inter, a_waves};
+    const DecodeHot h{x, ids, nullptr, nullptr, sh_gate_inp, top_k, S, S - top_k, -1, a_inter, a_waves, nullptr, nullptr, sh_gate, sh_up};
     gate_up_waves<GT, SGT, LPR, false, F16G, IPW, SPLIT>(h, p, sh);
 }
 
@@ -963,9 +973,9 @@ static void launch_a_ipw(const DecodeParams& p, hipStream_t stream, const Kernel
     const int w = gate_up_waves(items, p.n_tokens, 64 * LPR, device_cus());
     const dim3 grid = fast_grid((items + w - 1) / w, p.n_tokens), block(64 * w);
     if (ev.armed_a())
-        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, IPW>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
+        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, IPW>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.sh_gate_inp, p.sh_gate, p.sh_up, p.top_k, p.S, p.a_inter, w, p);
     else
-        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, IPW>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
+        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, IPW>), grid, block, 0, stream, p.x, p.ids, p.sh_gate_inp, p.sh_gate, p.sh_up, p.top_k, p.S, p.a_inter, w, p);
 }
 
 template <int GT, int SGT, int LPR, bool F16G>
@@ -992,9 +1002,9 @@ static void launch_a(const DecodeParams& p, hipStream_t stream, const KernelEven
         const int per_slot = p.inter / (64 / LPR);
         const dim3 grid = fast_grid(per_slot, 1), block(64 * (p.S + 1));
         if (ev.armed_a())
-            hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, 1, true>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, p.S + 1, p);
+            hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, 1, true>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.sh_gate_inp, p.sh_gate, p.sh_up, p.top_k, p.S, p.a_inter, p.S + 1, p);
         else
-            hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, 1, true>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, p.S + 1, p);
+            hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G, 1, true>), grid, block, 0, stream, p.x, p.ids, p.sh_gate_inp, p.sh_gate, p.sh_up, p.top_k, p.S, p.a_inter, p.S + 1, p);
         return;
     }
     const dim3 grid = fast_grid((items + w - 1) / w, p.n_tokens), block(64 * w);
@@ -1007,9 +1017,9 @@ static void launch_a(const DecodeParams& p, hipStream_t stream, const KernelEven
         return;
     }
     if (ev.armed_a())
-        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
+        hipExtLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G>), grid, block, 0, stream, ev.a_start, ev.a_stop, 0, p.x, p.ids, p.sh_gate_inp, p.sh_gate, p.sh_up, p.top_k, p.S, p.a_inter, w, p);
     else
-        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G>), grid, block, 0, stream, p.x, p.ids, p.act, p.sh_gate_inp, p.top_k, p.S, p.has_shared, p.n_experts, p.a_inter, w, p);
+        hipLaunchKernelGGL((k_fast_gate_up<GT, SGT, LPR, F16G>), grid, block, 0, stream, p.x, p.ids, p.sh_gate_inp, p.sh_gate, p.sh_up, p.top_k, p.S, p.a_inter, w, p);
 }
 
 template <int GT, int SGT, bool F16G>

@@ -100,6 +100,15 @@ void dequantize_iq4_nl_avx2(const uint8_t* src_bytes, float* dst, int rows, int 
  * `dst` must be 16-byte aligned and `src` even.  Returns 0, -1 or -5. */
 int mqh_dequant(int type, const void* src, void* dst, int64_t n, int want_f16, void* stream);
 
+/* A resident weight form with no counterpart in the reference (GGUF has no
+ * such type): Q3_K blocks byte for byte, each in a 112-byte slot whose last
+ * two bytes are zero, so every block starts on a 16-byte boundary (GGUF's
+ * 110-byte blocks leave most decode loads unaligned).  For resident layers
+ * that are decoded often.  Only mqh_moe_decode takes it, on its fast kernels
+ * (routed and shared matrices in this form, or Q6_K shared matrices beside
+ * it); every other call with it returns -2 (unsupported type). */
+#define MQH_TYPE_Q3_K_A112 111
+
 /* Bytes of workspace mqh_moe_decode needs for n_tokens tokens of top_k
  * routed experts (plus one shared slot). */
 int64_t mqh_moe_workspace_bytes(int n_tokens, int top_k, int intermediate, int sh_intermediate);
@@ -114,7 +123,7 @@ int64_t mqh_moe_workspace_bytes(int n_tokens, int top_k, int intermediate, int s
  * hidden] FP32.  The shared expert is optional (sh_gate == NULL: none;
  * sh_gate_inp == NULL: no sigmoid scale).  fp16_graph applies to the routed
  * experts.  Types: the five of moe_quant_expert and IQ4_NL (the latter, like
- * the FP16 graph, through the FP32 generic kernels).
+ * the FP16 graph, through the FP32 generic kernels), and MQH_TYPE_Q3_K_A112.
  * The workspace must hold mqh_moe_workspace_bytes(...) bytes and be
  * zeroed once (mqh_workspace_init) before first use.  Returns 0, -1, -2, -5
  * or -6; kernel-side faults are read with mqh_status. */

@@ -432,8 +432,24 @@ int decode_params(int gate_type, const void* gate, int up_type, const void* up, 
                   int n_experts, int hidden, int intermediate, int sh_gate_type, const void* sh_gate, int sh_up_type,
                   const void* sh_up, int sh_down_type, const void* sh_down, int sh_intermediate,
                   const float* sh_gate_inp, const float* x, int n_tokens, const int32_t* ids, const float* weights,
-                  int top_k, float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, DecodeParams& p) {
+                  int top_k, float* y, int fp16_graph, void* workspace, int64_t workspace_bytes, DecodeParams& p,
+                  bool a112 = false) {
     const bool has_shared = sh_gate != nullptr;
+    // the 112-byte Q3_K resident form: validated as Q3_K; only the fast decode
+    // kernels read it (checked once the call's parameters are known)
+    if (a112) {
+        auto base = [](int t) { return t == T_Q3_K_A112 ? (int)T_Q3_K : t; };
+        if (top_k > 0 && !(gate_type == T_Q3_K_A112) + !(up_type == T_Q3_K_A112) + !(down_type == T_Q3_K_A112) < 3) {
+            const int st = check_expert_types(base(gate_type), base(up_type), base(down_type), hidden, intermediate, true);
+            if (st) return st;
+        }
+        if (has_shared && !(sh_gate_type == T_Q3_K_A112) + !(sh_up_type == T_Q3_K_A112) + !(sh_down_type == T_Q3_K_A112) < 3) {
+            const int st = check_expert_types(base(sh_gate_type), base(sh_up_type), base(sh_down_type), hidden,
+                                              sh_intermediate > 0 ? sh_intermediate : 256, true);
+            if (st) return st;
+        }
+    }
+    auto dev_ok = [a112](int t) { return a112 && t == T_Q3_K_A112; };
     if (!x || !y || !workspace) return ST_ARG;
     if (hidden <= 0 || hidden > 65536 || n_tokens <= 0 || top_k < 0 || top_k > 64 ||
         (top_k == 0 && !has_shared) || (fp16_graph != 0 && fp16_graph != 1))
@@ -443,7 +459,8 @@ int decode_params(int gate_type, const void* gate, int up_type, const void* up, 
         if (!gate || !up || !down || !ids || !weights) return ST_ARG;
         if (odd(gate) || odd(up) || odd(down)) return ST_ARG;
         if (n_experts <= 0 || intermediate <= 0 || intermediate > 65536) return ST_ARG;
-        st = check_expert_types(gate_type, up_type, down_type, hidden, intermediate, true);
+        if (!(dev_ok(gate_type) || dev_ok(up_type) || dev_ok(down_type)))
+            st = check_expert_types(gate_type, up_type, down_type, hidden, intermediate, true);
         if (st) return st;
     } else {
         intermediate = 0;
@@ -451,7 +468,8 @@ int decode_params(int gate_type, const void* gate, int up_type, const void* up, 
     if (has_shared) {
         if (!sh_up || !sh_down || sh_intermediate <= 0 || sh_intermediate > 65536) return ST_ARG;
         if (odd(sh_gate) || odd(sh_up) || odd(sh_down)) return ST_ARG;
-        st = check_expert_types(sh_gate_type, sh_up_type, sh_down_type, hidden, sh_intermediate, true);
+        if (!(dev_ok(sh_gate_type) || dev_ok(sh_up_type) || dev_ok(sh_down_type)))
+            st = check_expert_types(sh_gate_type, sh_up_type, sh_down_type, hidden, sh_intermediate, true);
         if (st) return st;
     }
     const WorkspaceLayout wl = decode_workspace_layout(n_tokens, top_k, intermediate, has_shared ? sh_intermediate : 0);
@@ -495,8 +513,13 @@ int mqh_moe_decode(int gate_type, const void* gate, int up_type, const void* up,
     const int st = decode_params(gate_type, gate, up_type, up, down_type, down, n_experts, hidden, intermediate,
                                  sh_gate_type, sh_gate, sh_up_type, sh_up, sh_down_type, sh_down, sh_intermediate,
                                  sh_gate_inp, x, n_tokens, ids, weights, top_k, y, fp16_graph, workspace,
-                                 workspace_bytes, p);
+                                 workspace_bytes, p, true);
     if (st) return st;
+    // the 112-byte Q3_K form runs on the fast kernels only
+    const auto a = [&](int t) { return t == T_Q3_K_A112; };
+    const bool uses_a112 = (p.top_k > 0 && (a(p.gate_type) || a(p.up_type) || a(p.down_type))) ||
+                           (p.has_shared && (a(p.sh_gate_type) || a(p.sh_up_type) || a(p.sh_down_type)));
+    if (uses_a112 && (g_decode_path == 1 || !fast_supported(p))) return ST_TYPE;
     return launch_decode(p, (hipStream_t)stream) == hipSuccess ? ST_OK : ST_HIP;
 }
 

@@ -31,13 +31,17 @@
 namespace mqh {
 
 enum : int { T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_NL = 20 };
+// A resident form of this library, not a GGUF type: Q3_K blocks, byte for byte,
+// each in a 112-byte slot (two zero bytes after the 110), so that every block and
+// its 16-byte fields start on a 16-byte boundary.  Only the decode kernels take it.
+enum : int { T_Q3_K_A112 = 111 };
 
 __host__ __device__ constexpr int block_size(int t) {
-    return (t == T_Q8_0 || t == T_IQ4_NL) ? 32 : (t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 256 : 0;
+    return (t == T_Q8_0 || t == T_IQ4_NL) ? 32 : (t == T_Q3_K || t == T_Q3_K_A112 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 256 : 0;
 }
 
 __host__ __device__ constexpr int block_bytes(int t) {
-    return t == T_Q8_0 ? 34 : t == T_Q3_K ? 110 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210
+    return t == T_Q8_0 ? 34 : t == T_Q3_K ? 110 : t == T_Q3_K_A112 ? 112 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210
          : t == T_IQ4_NL ? 18 : 0;
 }
 

@@ -128,6 +128,9 @@ template <> struct LaneGeo<T_Q4_K> { static constexpr int NR = 2, RL = 32, NRAW 
 template <> struct LaneGeo<T_Q5_K> { static constexpr int NR = 2, RL = 32, NRAW = 20; };
 template <> struct LaneGeo<T_Q6_K> { static constexpr int NR = 2, RL = 32, NRAW = 19; };
 template <> struct LaneGeo<T_Q3_K> { static constexpr int NR = 4, RL = 16, NRAW = 12; };
+// Q3_K in 112-byte slots: the same lane code (the final branches of the type
+// switches below), a block every 112 bytes
+template <> struct LaneGeo<T_Q3_K_A112> : LaneGeo<T_Q3_K> {};
 template <> struct LaneGeo<T_Q8_0> { static constexpr int NR = 2, RL = 32, NRAW = 17; };
 
 // Bytes of one 256-column unit of a row: a K-quant super-block, or 8 Q8_0 blocks.

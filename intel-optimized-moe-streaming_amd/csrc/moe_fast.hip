@@ -505,7 +505,7 @@ __device__ __forceinline__ void gate_up_items(const DecodeHot& h, const DecodePa
         // 3. gate and up dot products (the zero-accumulator dot form except in
         // the two-item Q3_K and Q8_0 instances, where it spilled: the 16-token
         // Q3_K layer 53.4 -> 63.6 us)
-        constexpr bool Z = IPW == 1 || (GT != T_Q3_K && GT != T_Q8_0);
+        constexpr bool Z = IPW == 1 || (GT != T_Q3_K && GT != T_Q3_K_A112 && GT != T_Q8_0);
 #pragma unroll
         for (int i = 0; i < IPW; ++i) {
             if (sw) {
@@ -892,7 +892,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
 // ------------------------------------------------------------------ launch
 
 static bool fast_type(int t) {
-    return t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_0;
+    return t == T_Q3_K || t == T_Q3_K_A112 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_0;
 }
 static bool fast_dim(int n) { return n == 256 || n == 512 || n == 1024 || n == 2048; }
 
@@ -1122,6 +1122,7 @@ static hipError_t launch_fast(const DecodeParams& p0, hipStream_t stream, const 
         case T_Q5_K: launch_a_t<T_Q5_K, F16G>(p, stream, ev); break;
         case T_Q6_K: launch_a_t<T_Q6_K, F16G>(p, stream, ev); break;
         case T_Q8_0: launch_a_t<T_Q8_0, F16G>(p, stream, ev); break;
+        case T_Q3_K_A112: launch_a_t<T_Q3_K_A112, F16G>(p, stream, ev); break;
         default: launch_a_t<T_Q3_K, F16G>(p, stream, ev); break;
     }
     hipError_t err = hipGetLastError();
@@ -1131,6 +1132,7 @@ static hipError_t launch_fast(const DecodeParams& p0, hipStream_t stream, const 
         case T_Q5_K: launch_b_t<T_Q5_K, F16G>(p, stream, ev); break;
         case T_Q6_K: launch_b_t<T_Q6_K, F16G>(p, stream, ev); break;
         case T_Q8_0: launch_b_t<T_Q8_0, F16G>(p, stream, ev); break;
+        case T_Q3_K_A112: launch_b_t<T_Q3_K_A112, F16G>(p, stream, ev); break;
         default: launch_b_t<T_Q3_K, F16G>(p, stream, ev); break;
     }
     return hipGetLastError();

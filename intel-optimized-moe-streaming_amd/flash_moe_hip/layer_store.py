@@ -16,7 +16,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from .quant_types import DEVICE_TYPES, name_of, tensor_bytes
+from .quant_types import DECODE_TYPES, Q3_K_A112, name_of, pad_blocks, tensor_bytes
 
 ROLES = ("gate", "up", "down")
 
@@ -55,7 +55,7 @@ class ExpertLayer:
 
         self.types = {r: int(types[r]) for r in ROLES}
         for r in ROLES:
-            if self.types[r] not in DEVICE_TYPES:
+            if self.types[r] not in DECODE_TYPES:
                 raise ValueError(f"{r}: unsupported ggml type {self.types[r]}")
         self.n_experts, self.hidden, self.intermediate = int(n_experts), int(hidden), int(intermediate)
         self.tensors = {"gate": gate, "up": up, "down": down}
@@ -96,6 +96,27 @@ class ExpertLayer:
         return self._router_dev
 
     # ------------------------------------------------------------- geometry
+    def aligned_q3k(self) -> "ExpertLayer":
+        """This layer with every Q3_K matrix (routed and shared) in the 112-byte
+        resident form: the same blocks, each starting on a 16-byte boundary
+        (GGUF's 110-byte blocks leave most decode loads unaligned).  Decode
+        only: prefill and dequantization reject the form."""
+        def conv(t, ty):
+            return (pad_blocks(t, 110, 112), Q3_K_A112) if ty == 11 else (t, ty)
+        tens, types = {}, {}
+        for r in ROLES:
+            tens[r], types[r] = conv(self.tensors[r], self.types[r])
+        sh = None
+        if self.shared is not None:
+            s = self.shared
+            parts, st = {}, {}
+            for r in ROLES:
+                parts[r], st[r] = conv(getattr(s, r), s.types[r])
+            sh = SharedWeights(parts["gate"], parts["up"], parts["down"], types=st, intermediate=s.intermediate,
+                               gate_inp=s.gate_inp)
+        return ExpertLayer(tens["gate"], tens["up"], tens["down"], types, self.n_experts, self.hidden,
+                           self.intermediate, sh, router_weights=getattr(self, "router_weights", None))
+
     def expert_bytes(self, role: str) -> int:
         rows, cols = _shape(role, self.hidden, self.intermediate)
         return tensor_bytes(self.types[role], rows, cols)

@@ -17,6 +17,16 @@ SUPPORTED_TYPES = frozenset(GGML_TYPE_IDS.values())
 # fast_dequant library, cpp/fast_dequant.cpp:40-65).
 DEVICE_TYPES = SUPPORTED_TYPES | {IQ4_NL}
 
+# A resident form of this library (not a GGUF type): Q3_K blocks byte for byte,
+# each in a 112-byte slot (two zero bytes after the 110), so that every block
+# starts on a 16-byte boundary.  Only the decode entry point takes it
+# (``mqh_moe_decode`` on its fast kernels); ``pad_blocks`` makes it.
+Q3_K_A112 = 111
+RESIDENT_BLOCK_INFO: dict[str, tuple[int, int]] = {"Q3_K_A112": (256, 112)}
+TYPE_NAMES[Q3_K_A112] = "Q3_K_A112"
+# what a resident layer may hold
+DECODE_TYPES = DEVICE_TYPES | {Q3_K_A112}
+
 # name -> (block_size, bytes_per_block) for every GGUF type the reference names.
 GGML_BLOCK_INFO: dict[str, tuple[int, int]] = {
     "F32": (1, 4),
@@ -46,7 +56,19 @@ def block_info(ggml_type: int) -> tuple[int, int]:
     name = TYPE_NAMES.get(int(ggml_type))
     if name is None:
         raise ValueError(f"unsupported ggml type {ggml_type}")
-    return GGML_BLOCK_INFO[name]
+    return RESIDENT_BLOCK_INFO.get(name) or GGML_BLOCK_INFO[name]
+
+
+def pad_blocks(t, block_bytes: int, slot_bytes: int):
+    """A flat uint8 tensor of whole blocks, each copied into a zero-padded slot."""
+    import torch
+
+    if t.numel() % block_bytes:
+        raise ValueError(f"{t.numel()} bytes is not a whole number of {block_bytes}-byte blocks")
+    v = t.reshape(-1, block_bytes)
+    out = torch.zeros((v.shape[0], slot_bytes), dtype=torch.uint8, device=t.device)
+    out[:, :block_bytes] = v
+    return out.reshape(-1)
 
 
 def name_of(ggml_type: int) -> str:

@@ -583,9 +583,12 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
     U = [len(np.unique(v)) for v in IDh]
     nbytes = float(np.mean([(u + 1) * layers[0].bytes_per_expert() for u in U]))
     runner = MoeRunner(dev)
+    # the same layers in the 112-byte-slot Q3_K resident form (decode only)
+    aligned = [L.aligned_q3k() for L in layers]
     paths = {
         "prefill": lambda l: runner.prefill(layers[l], X[l], IDS[l], WS[l], y=Y),
         "decode": lambda l: runner.decode(layers[l], X[l], IDS[l], WS[l], y=Y),
+        "decode_aligned_q3k": lambda l: runner.decode(aligned[l], X[l], IDS[l], WS[l], y=Y),
     }
     res = {}
     want = _oracle_tokens(layers[0], types, Xh[0], IDh[0], WSh[0], [0, 7, 15])
@@ -610,10 +613,13 @@ def bench_batched_decode(dev, n_layers: int, steps: int, cpu_seconds: float) -> 
     dom = "A" if kb["A"] >= kb["B"] else "B"
     frac = frac_a if dom == "A" else 1 - frac_a
     kname = {"prefill": {"A": "mqh::k_prefill_gate_up<11, 11, 8, false, 2>", "B": "mqh::k_prefill_down<11, 11, 2, 1>"},
-             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32, false, 2, false>", "B": "mqh::k_fast_down_bal<11, 11, 8, 4>"}}[best][dom]
+             "decode": {"A": "mqh::k_fast_gate_up<11, 11, 32, false, 2, false>", "B": "mqh::k_fast_down_bal<11, 11, 8, 4>"},
+             "decode_aligned_q3k": {"A": "mqh::k_fast_gate_up<111, 111, 32, false, 2, false>",
+                                    "B": "mqh::k_fast_down_bal<111, 111, 8, 4>"}}[best][dom]
     out = {
         "workload": f"batched decode: {T} tokens, hidden {H}, {E} experts x intermediate {I}, top-8 of N(0,1) "
-                    f"logits + shared, all Q3_K, {n_layers} resident layers rotated",
+                    f"logits + shared, all Q3_K, {n_layers} resident layers rotated (path decode_aligned_q3k: the "
+                    f"same blocks in 112-byte slots; GB/s counts the GGUF bytes)",
         "metric": "quant-weight GB/s per layer-step (weights of the U distinct routed experts + shared)",
         "value": res[best]["gbs"], "unit": "GB/s", "us_per_layer": res[best]["us_per_layer"],
         "path": best, "paths": res, "distinct_experts_mean": float(np.mean(U)),
@@ -942,6 +948,25 @@ def bench_decode_mixes(dev, n_layers: int, reps: int) -> dict:
                 "us_per_layer": round(ms * 1e3, 3), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                 "kernels_us": {"A": round(kern["a_us"], 3), "B": round(kern["b_us"], 3)},
                 "parity_max_rel_err": float(f"{err:.3e}")}
+            if 11 in types.values():
+                # the same layers with their Q3_K matrices in 112-byte slots
+                y0 = Y.clone()
+                layers_a = [L.aligned_q3k() for L in layers]
+
+                def sweep_a(n=n_layers):
+                    for l in range(n):
+                        runner.decode(layers_a[l], X[l:l + 1], IDS[l:l + 1], WS[l:l + 1], y=Y[l:l + 1],
+                                      fp16_graph=fp16)
+
+                sweep_a()
+                torch.cuda.synchronize()
+                assert runner.status() == 0 and torch.equal(Y.view(torch.int32), y0.view(torch.int32))
+                ms_a = _time(_graph(sweep_a, dev), reps) / n_layers
+                row["fp16_graph" if fp16 else "fp32_graph"]["aligned_q3k"] = {
+                    "us_per_layer": round(ms_a * 1e3, 3), "outputs_bit_identical": True}
+                log(f"decode, {name} ({'FP16' if fp16 else 'FP32'} graph), Q3_K in 112-byte slots: "
+                    f"{ms_a * 1e3:.2f} us/layer")
+                del layers_a
             log(f"decode, {name} ({'FP16' if fp16 else 'FP32'} graph): {ms * 1e3:.2f} us/layer, parity {err:.2e}; "
                 f"kernels {kern['a_us']:.2f} / {kern['b_us']:.2f} us")
             del layers
